@@ -1,0 +1,131 @@
+/*
+ * libsvhip — MI355X (gfx950) kernels for StreamVoxel's per-step generation hot path, behind a plain C ABI.
+ *
+ * Every entry point takes caller-owned device pointers, plain sizes and strides (in elements), and a HIP stream
+ * (`hipStream_t` passed as `void*`); it enqueues work on that stream and returns without synchronising, so calls
+ * can be recorded into a HIP graph. No entry point allocates device memory: scratch space comes from a
+ * caller-provided workspace whose size the matching `*_workspace_bytes` query returns.
+ *
+ * Return value: SVHIP_OK (0) on success, a negative status otherwise; `svhip_last_error()` then describes the
+ * failure (thread-local string). No entry point aborts the process.
+ *
+ * Booleans are bytes holding 0 or 1 (torch.bool storage). Index order of a column window is the flat YZX order
+ * `(y * Z + z) * X + x`.
+ */
+#ifndef SVHIP_H
+#define SVHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum svhip_dtype { SVHIP_F32 = 0, SVHIP_BF16 = 1, SVHIP_FP8_E4M3 = 3 };
+
+enum svhip_status { SVHIP_OK = 0, SVHIP_EINVAL = -1, SVHIP_ELAUNCH = -2, SVHIP_EWORKSPACE = -3 };
+
+enum svhip_lel_mode { SVHIP_LEL_LAYER = 0, SVHIP_LEL_BAND = 1, SVHIP_LEL_COLUMN = 2 };
+
+/* Library version (major * 10000 + minor * 100 + patch) and the last error of the calling thread. */
+int svhip_version(void);
+const char* svhip_last_error(void);
+
+/*
+ * Negative Shannon entropy per voxel, score = sum_c p_c log p_c (nats, fp32 arithmetic), for `batch` windows of
+ * `n` voxels with `classes` logits each. Element (b, c, i) of `logits` is at b*stride_b + c*stride_c + i*stride_n.
+ * Class-major [B,C,N] (stride_n == 1) and voxel-major [B,N,C] (stride_c == 1) layouts take vectorised paths.
+ * dtype: SVHIP_F32 or SVHIP_BF16. out: fp32 [batch, n] contiguous.
+ * Replaces: entropy_scores (streamvoxel/sampling/entropy.py:1-4), entropy_triton (streamvoxel/stream/fast_ops.py:420-430).
+ */
+int svhip_entropy(const void* logits, int dtype, int64_t batch, int64_t classes, int64_t n, int64_t stride_b,
+                  int64_t stride_c, int64_t stride_n, float* out, void* stream);
+
+/*
+ * Air probability per voxel: sum over the `n_air` class ids in `air_ids` (device int32) of softmax(logits)_c.
+ * Same layout rules as svhip_entropy. out: fp32 [batch, n].
+ * Replaces: `logits.float().softmax(0)[air].sum(0)` (streamvoxel/stream/slot.py:126).
+ */
+int svhip_air_prob(const void* logits, int dtype, int64_t batch, int64_t classes, int64_t n, int64_t stride_b,
+                   int64_t stride_c, int64_t stride_n, const int32_t* air_ids, int32_t n_air, float* out,
+                   void* stream);
+
+/*
+ * Low-entropy-last update, in place on `last`:
+ *   bad = (mask & air <= fp32(1 - eps)) | solid
+ *   SVHIP_LEL_COLUMN: last [B,Y,Z,X] |= the top run (from y = Y-1 down) of clean voxels of every (z, x) column;
+ *   SVHIP_LEL_LAYER / SVHIP_LEL_BAND: last [B,Y] |= the top run of clean layers (bands of 8 layers).
+ * mask, air, solid: [B,Y,Z,X]; `mask` NULL means all true, `solid` NULL means all false.
+ * Replaces: low_entropy_last_update (streamvoxel/sampling/low_entropy_last.py:8-17).
+ */
+int svhip_lel_update(uint8_t* last, const uint8_t* mask, const float* air, const uint8_t* solid, double eps,
+                     int32_t mode, int64_t batch, int64_t Y, int64_t Z, int64_t X, void* stream);
+
+/*
+ * Global top-k mask: out[b] = the `count` largest `scores[b]` among `eligible[b]`, ties to the lower index;
+ * count <= 0 selects nothing and a count above the number of eligible voxels selects all of them. The count is
+ * `count_dev[b]` (device int64) when count_dev is non-NULL, else `count_host`. Scores must be finite.
+ * scores fp32 [batch, n]; eligible, out: bytes [batch, n].
+ * Replaces: top_mask (streamvoxel/sampling/block_quota.py:4-12), top_mask_nosync (streamvoxel/stream/fast_ops.py:433-439).
+ */
+int svhip_top_mask(const float* scores, const uint8_t* eligible, int64_t batch, int64_t n, const int64_t* count_dev,
+                   int64_t count_host, uint8_t* out, void* stream);
+
+/*
+ * Block-quota selection of `k[b]` voxels of `mask[b]` over b^3 blocks of a [Y,Z,X] window, for `batch` windows:
+ * per-block quotas apportioned from frac[b] * n_total[b, j] with the remainder handed out by ascending
+ * -(fractional part) * 1e6 + pos[b, j], the quota-many highest scores taken inside each block, then a global trim
+ * (more than k) or top-up (fewer) by score. bad[b] is set to 1 when the result does not hold exactly k voxels.
+ *   score fp32 [B,N]; mask bytes [B,N]; k, committed int64 [B]; frac fp64 [B]; pos, n_total int64 [B, nb];
+ *   chosen bytes [B,N] (written); bad bytes [B] (written), nb = N / b^3.
+ * Replaces: quota_select_nosync (streamvoxel/stream/fast_ops.py:442-473) and, with committed = the number of
+ * committed non-deferred voxels, block_quota_select (streamvoxel/sampling/block_quota.py:20-38).
+ */
+size_t svhip_quota_select_workspace_bytes(int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_t block);
+int svhip_quota_select(const float* score, const uint8_t* mask, int64_t batch, int64_t Y, int64_t Z, int64_t X,
+                       int64_t block, const int64_t* k, const int64_t* pos, const double* frac,
+                       const int64_t* n_total, const int64_t* committed, uint8_t* chosen, uint8_t* bad,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The whole EASE selection of one solid step for `batch` windows, without host synchronisation:
+ *   selectable = (tokens == mask_token) & ~last, score = entropy(logits), chosen = block-quota select
+ * (as svhip_quota_select), bad = quota violation. tokens int64 [B,N]; last bytes [B,N]; logits as in
+ * svhip_entropy; scores_out (optional, may be NULL) receives the fp32 scores [B,N].
+ * Replaces: FastLowEntropyLastSlot.select (streamvoxel/stream/fast_ops.py:534-540) for all slots of a batch.
+ */
+size_t svhip_ease_select_workspace_bytes(int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_t block);
+int svhip_ease_select(const void* logits, int dtype, int64_t classes, int64_t stride_b, int64_t stride_c,
+                      int64_t stride_n, const int64_t* tokens, int64_t mask_token, const uint8_t* last,
+                      int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_t block, const int64_t* k,
+                      const int64_t* pos, const double* frac, const int64_t* n_total, const int64_t* committed,
+                      uint8_t* chosen, uint8_t* bad, float* scores_out, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/*
+ * Cross attention over per-window, variable-length cached keys:
+ *   O[b,h,q,:] = sum_{j < L_b} softmax_j(scale * Q[b,h,q,:] . K[b,h,j,:]) V[b,h,j,:]
+ * with L_b = min(kv_len[b], kv_cap) (device int32 [B]) or, for the packed layout, cu_seqlens[b+1] - cu_seqlens[b] with key j of
+ * window b at row cu_seqlens[b] + j. A window with L_b = 0 gets zeros.
+ * Q, O: bf16, element (b,h,q,d) at b*s?_b + h*s?_h + q*s?_q + d. K: element (b,h,j,d) at
+ * b*sk_b + h*sk_h + row*sk_k + d; V: at b*sv_b + h*sv_h + row*sv_k + d*sv_d, where either sv_d == 1 (rows of
+ * head_dim, the reference layout) or sv_k == 1 (V stored transposed, keys contiguous: the fast staging path);
+ * row = j, or cu_seqlens[b] + j in the packed layout (sk_b / sv_b are then ignored). kv_dtype SVHIP_BF16, or
+ * SVHIP_FP8_E4M3 (OCP e4m3fn bytes) with per-(window, head) fp32 dequantisation scales k_scale/v_scale [B,H].
+ * head_dim: 64 (48 is accepted and zero-padded to 64 inside the kernel). fp32 accumulation.
+ * Replaces: flex_attention over PackedKeys' block mask in cross_flex (streamvoxel/stream/fast_ops.py:104-108,
+ * 122-159) and the masked SDPA in SlotCrossAttention.forward / cross_sdpa (streamvoxel/stream/engine.py:28-47,
+ * streamvoxel/stream/fast_ops.py:111-115).
+ */
+int svhip_xattn_fwd(const void* q, const void* k, const void* v, void* o, int kv_dtype, const int32_t* kv_len,
+                    const int32_t* cu_seqlens, const float* k_scale, const float* v_scale, int64_t B, int64_t H,
+                    int64_t Q, int64_t D, int64_t kv_cap, int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b,
+                    int64_t sk_h, int64_t sk_k, int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d,
+                    int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SVHIP_H */

@@ -1,0 +1,68 @@
+"""Builds libsvhip.so (all HIP sources under csrc/) for gfx950 with hipcc, in-tree next to this file.
+
+    python -m streamvoxel_amd.build            # or streamvoxel_amd.build.build()
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, 'csrc')
+LIB = os.path.join(HERE, 'libsvhip.so')
+ARCH = os.environ.get('SVHIP_ARCH', 'gfx950')
+
+SOURCES = ['api.hip', 'entropy.hip', 'select.hip', 'xattn.hip']
+
+FLAGS = [
+    '-O3', '-std=c++17', '-fPIC', '-shared', f'--offload-arch={ARCH}',
+    # Packed fp32 VALU forms are kept out of the generated code.
+    '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    '-Wall', '-Wno-unused-function', '-Wno-unused-variable',
+]
+
+
+def hipcc():
+    path = shutil.which('hipcc') or '/opt/rocm/bin/hipcc'
+    if not os.path.exists(path):
+        raise RuntimeError('hipcc not found; the ROCm toolchain is required to build libsvhip')
+    return path
+
+
+def build(verbose=False, jobs=4):
+    """Compile each source to an object in parallel, then link the shared library. Returns the library path."""
+    objdir = os.path.join(HERE, '_build')
+    os.makedirs(objdir, exist_ok=True)
+    procs = []
+    objects = []
+    for src in SOURCES:
+        obj = os.path.join(objdir, src.replace('.hip', '.o'))
+        objects.append(obj)
+        cmd = [hipcc(), *[f for f in FLAGS if f != '-shared'], '-c', os.path.join(CSRC, src), '-o', obj]
+        if verbose:
+            print(' '.join(cmd), flush=True)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+    failed = []
+    for src, proc in procs:
+        out, _ = proc.communicate()
+        text = out.decode(errors='replace')
+        text = '\n'.join(line for line in text.splitlines() if 'packed-fp32-ops' not in line)
+        if proc.returncode != 0:
+            failed.append((src, text))
+        elif verbose and text.strip():
+            print(text)
+    if failed:
+        raise RuntimeError('hipcc failed:\n' + '\n'.join(f'--- {s}\n{t}' for s, t in failed))
+    tmp = LIB + '.tmp'
+    cmd = [hipcc(), *FLAGS, *objects, '-o', tmp]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    if res.returncode != 0:
+        raise RuntimeError('link failed:\n' + res.stdout.decode(errors='replace'))
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == '__main__':
+    print(build(verbose='-v' in sys.argv))

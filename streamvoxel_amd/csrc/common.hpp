@@ -1,0 +1,100 @@
+// Shared device/host helpers for the gfx950 kernels of libsvhip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/svhip.h"
+
+namespace svhip {
+
+// ------------------------------------------------------------------------------------------ host error handling
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define SVHIP_REQUIRE(cond, ...)             \
+  do {                                       \
+    if (!(cond)) {                           \
+      ::svhip::set_error(__VA_ARGS__);       \
+      return SVHIP_EINVAL;                   \
+    }                                        \
+  } while (0)
+
+#define SVHIP_LAUNCHED(what)                                                            \
+  do {                                                                                  \
+    hipError_t _e = hipGetLastError();                                                  \
+    if (_e != hipSuccess) {                                                             \
+      ::svhip::set_error("%s: launch failed: %s", what, hipGetErrorString(_e));         \
+      return SVHIP_ELAUNCH;                                                             \
+    }                                                                                   \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ----------------------------------------------------------------------------------------------- device helpers
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
+__device__ __forceinline__ float bf16_bits_to_float(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ float to_float(T v);
+template <>
+__device__ __forceinline__ float to_float<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_float<uint16_t>(uint16_t v) { return bf16_bits_to_float(v); }
+
+// DPP row-local (16-lane) all-reduce: after the four steps every lane of a 16-lane row holds the row result.
+// quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  return v;
+}
+
+// Order-preserving fp32 -> u32 map (ascending float -> ascending key); -0.0 is folded onto +0.0 first so that the
+// two compare equal, as IEEE comparisons (and torch's sort) treat them.
+__device__ __forceinline__ uint32_t ordered_u32(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) == 0u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Key that sorts descending scores first: smaller key = larger score.
+__device__ __forceinline__ uint32_t desc_key(float f) { return ~ordered_u32(f); }
+
+__device__ __forceinline__ uint64_t ordered_u64(double d) {
+  uint64_t u = static_cast<uint64_t>(__double_as_longlong(d));
+  if ((u & 0x7fffffffffffffffull) == 0ull) u = 0ull;
+  return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace svhip

@@ -1,0 +1,457 @@
+// Cross attention over per-window variable-length cached K/V, bf16 MFMA (gfx950), fp32 accumulation.
+//
+// Work item: one workgroup = (window b, head h, 128-query tile), 4 waves x 32 queries. Keys are walked in
+// 64-key blocks staged through LDS (double-buffered; the next block's global loads are in flight while the
+// current block is computed).
+//
+// Per wave and key block (v_mfma_f32_32x32x16_bf16 throughout):
+//   S^T[key, q] = K . Q^T         A = K rows from LDS, B = the wave's Q (registers, loaded once)
+//   P^T = exp2(S^T * scale*log2e - m)   online softmax; every lane owns one query column (q = lane % 32) and
+//                                       16 of every 32 keys, its partner lane (lane ^ 32) the other 16
+//   O^T[d, q] += V^T . P^T        A = V^T rows from LDS, B = P^T straight from the S^T accumulators
+// The C layout of a 32x32 MFMA gives lane l the rows 8*(i/4) + 4*(l/32) + i%4 of column l%32. K rows are
+// stored in LDS under the involution sigma (swap of the 4-row groups 1 and 2 of every 16 rows), so accumulator
+// entries i = 0..7 of lane l hold keys 8*(l/32) + i and i = 8..15 keys 16 + 8*(l/32) + (i-8): exactly the B
+// operand slice (k index 8*(l/32) + j) the second product needs, with no cross-lane movement.
+// Because O^T's columns are queries too, the per-query rescale (alpha) and the final 1/l are lane-local.
+//
+// K/V dtypes: bf16, or OCP e4m3fn bytes converted exactly to bf16 during staging; the fp8 scales are folded into
+// the softmax scale (k_scale) and the output (v_scale). V may be stored row-major ([key][d], transposed while
+// staging) or transposed ([d][key], staged with 16-byte copies).
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace svhip {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kQTile = 128;   // queries per workgroup
+constexpr int kKB = 64;       // keys per block
+constexpr int kDPad = 64;     // head_dim handled by the MFMA tiles (smaller head_dim is zero-padded)
+constexpr int kRow = 72;      // LDS row stride in bf16 elements (144 bytes: conflict-free 16-byte reads)
+constexpr int kThreads = 256;
+
+struct XattnParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  const int32_t* kv_len;
+  const int32_t* cu_seqlens;
+  const float* k_scale;
+  const float* v_scale;
+  int64_t B, H, Q, D, kv_cap;
+  int64_t sq_b, sq_h, sq_q;
+  int64_t sk_b, sk_h, sk_k;
+  int64_t sv_b, sv_h, sv_k, sv_d;
+  int64_t so_b, so_h, so_q;
+  float scale_log2;  // softmax scale * log2(e)
+  int q_tiles;
+};
+
+// Row of key `key` (0..63) of a block inside the LDS K tile.
+__device__ __forceinline__ int sigma_row(int key) {
+  const int y = key & 15;
+  const int g = y >> 2;
+  const int swapped = (g == 1) ? y + 4 : (g == 2 ? y - 4 : y);
+  return (key & ~15) | swapped;
+}
+
+// OCP e4m3fn byte -> bf16 bits (exact: every e4m3 value is a bf16 value).
+__device__ __forceinline__ uint32_t e4m3_to_bf16_bits(uint32_t byte) {
+  const uint32_t s = (byte & 0x80u) << 8;
+  const uint32_t e = (byte >> 3) & 0xfu;
+  const uint32_t m = byte & 0x7u;
+  if (e == 0xfu && m == 0x7u) return s | 0x7fc0u;  // NaN
+  if (e != 0u) return s | ((e + 120u) << 7) | (m << 4);
+  if (m == 0u) return s;
+  const float f = static_cast<float>(m) * 0x1p-9f;  // subnormal: m * 2^-9
+  return s | (__float_as_uint(f) >> 16);
+}
+
+// 8 fp8 bytes (two dwords) -> 8 bf16 packed in a uint4.
+__device__ __forceinline__ uint4 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t src = i == 0 ? lo : hi;
+    w[2 * i] = e4m3_to_bf16_bits(src & 0xffu) | (e4m3_to_bf16_bits((src >> 8) & 0xffu) << 16);
+    w[2 * i + 1] = e4m3_to_bf16_bits((src >> 16) & 0xffu) | (e4m3_to_bf16_bits(src >> 24) << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <bool FP8>
+struct Elem {
+  using T = typename std::conditional<FP8, uint8_t, uint16_t>::type;
+};
+
+// Load 8 consecutive elements (bf16 or e4m3) as 8 bf16 in a uint4; `valid` elements only (rest zero).
+template <bool FP8>
+__device__ __forceinline__ uint4 load8(const typename Elem<FP8>::T* p, int valid, bool aligned) {
+  if (valid >= 8 && aligned) {
+    if constexpr (FP8) {
+      const uint2 r = *reinterpret_cast<const uint2*>(p);
+      return fp8x8_to_bf16x8(r.x, r.y);
+    } else {
+      return *reinterpret_cast<const uint4*>(p);
+    }
+  }
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (e < valid) {
+      uint32_t bits;
+      if constexpr (FP8) {
+        bits = e4m3_to_bf16_bits(p[e]);
+      } else {
+        bits = p[e];
+      }
+      w[e >> 1] |= bits << (16 * (e & 1));
+    }
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <bool FP8, bool VT>
+struct Stage {
+  uint4 k[2];
+  uint4 v[2];
+};
+
+// Global -> registers for key block starting at kv0 (2 chunks of 8 elements per thread for each of K and V).
+template <bool FP8, bool VT>
+__device__ __forceinline__ void stage_load(Stage<FP8, VT>& st, const XattnParams& p, int64_t kbase,
+                                           int64_t vbase, int64_t off, int L, int kv0) {
+  using T = typename Elem<FP8>::T;
+  const T* K = static_cast<const T*>(p.k);
+  const T* V = static_cast<const T*>(p.v);
+  const int dvalid_chunks = static_cast<int>(p.D / 8);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int c = threadIdx.x + kThreads * r;  // 0..511
+    {
+      const int key = c >> 3, dc = c & 7;
+      const int kg = kv0 + key;
+      if (kg < L && dc < dvalid_chunks) {
+        const T* src = K + kbase + (off + kg) * p.sk_k + dc * 8;
+        st.k[r] = load8<FP8>(src, 8, true);
+      } else {
+        st.k[r] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+    if constexpr (VT) {
+      const int d = c >> 3, kc = c & 7;
+      const int kg = kv0 + kc * 8;
+      if (d < p.D && kg < L) {
+        const T* src = V + vbase + d * p.sv_d + (off + kg) * p.sv_k;
+        const int valid = (L - kg) < 8 ? (L - kg) : 8;
+        const bool aligned = ((reinterpret_cast<uintptr_t>(src) & (FP8 ? 7 : 15)) == 0);
+        st.v[r] = load8<FP8>(src, valid, aligned);
+      } else {
+        st.v[r] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    } else {
+      const int key = c >> 3, dc = c & 7;
+      const int kg = kv0 + key;
+      if (kg < L && dc < dvalid_chunks) {
+        const T* src = V + vbase + (off + kg) * p.sv_k + dc * 8;
+        st.v[r] = load8<FP8>(src, 8, true);
+      } else {
+        st.v[r] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+}
+
+// Registers -> LDS (K rows under sigma; V as V^T [d][key]).
+template <bool FP8, bool VT>
+__device__ __forceinline__ void stage_store(const Stage<FP8, VT>& st, uint16_t* sK, uint16_t* sV) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int c = threadIdx.x + kThreads * r;
+    {
+      const int key = c >> 3, dc = c & 7;
+      *reinterpret_cast<uint4*>(sK + sigma_row(key) * kRow + dc * 8) = st.k[r];
+    }
+    if constexpr (VT) {
+      const int d = c >> 3, kc = c & 7;
+      *reinterpret_cast<uint4*>(sV + d * kRow + kc * 8) = st.v[r];
+    } else {
+      const int key = c >> 3, dc = c & 7;
+      const uint32_t w[4] = {st.v[r].x, st.v[r].y, st.v[r].z, st.v[r].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sV[(dc * 8 + e) * kRow + key] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
+template <bool FP8, bool VT>
+__global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKB * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kDPad * kRow];
+
+  // Workgroup -> (window, head, query tile). Consecutive workgroup ids are dispatched round robin over the 8
+  // XCDs, so XCD x (= id % 8) is given the (window, head) pairs bh = x, x + 8, ... with all query tiles of one
+  // pair back to back: the pair's K/V is read from HBM once into that XCD's L2, and windows of different
+  // lengths are mixed on every XCD.
+  const int64_t wg = blockIdx.x;
+  int qt;
+  int64_t bh;
+  if ((p.B * p.H) % 8 == 0) {
+    const int64_t seq = wg >> 3;
+    qt = static_cast<int>(seq % p.q_tiles);
+    bh = (wg & 7) + 8 * (seq / p.q_tiles);
+  } else {
+    qt = static_cast<int>(wg % p.q_tiles);
+    bh = wg / p.q_tiles;
+  }
+  const int64_t h = bh % p.H;
+  const int64_t b = bh / p.H;
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int col = lane & 31;  // query column within the wave
+  const int hh = lane >> 5;   // lane half
+  const int64_t q = static_cast<int64_t>(qt) * kQTile + w * 32 + col;
+  const bool q_ok = q < p.Q;
+
+  int64_t off = 0;
+  int L;
+  if (p.cu_seqlens) {
+    off = p.cu_seqlens[b];
+    L = p.cu_seqlens[b + 1] - p.cu_seqlens[b];
+  } else {
+    L = p.kv_len[b];
+  }
+  if (L > p.kv_cap && !p.cu_seqlens) L = static_cast<int>(p.kv_cap);
+  if (L < 0) L = 0;
+
+  const uint16_t* Qp = static_cast<const uint16_t*>(p.q) + b * p.sq_b + h * p.sq_h;
+  uint16_t* Op = static_cast<uint16_t*>(p.o) + b * p.so_b + h * p.so_h;
+
+  float kscale = 1.f, vscale = 1.f;
+  if (FP8) {
+    kscale = p.k_scale[b * p.H + h];
+    vscale = p.v_scale[b * p.H + h];
+  }
+  const float sl2 = p.scale_log2 * kscale;
+
+  if (L == 0) {
+    if (q_ok) {
+      for (int d = hh; d < p.D; d += 2) Op[q * p.so_q + d] = 0;
+    }
+    return;
+  }
+
+  // The wave's Q as B operands: k-step s covers d = 16 s + 8 hh + 0..7.
+  bf16x8_t qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int d0 = 16 * s + 8 * hh;
+    uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+    if (q_ok && d0 < p.D) raw = *reinterpret_cast<const uint4*>(Qp + q * p.sq_q + d0);
+    qf[s] = __builtin_bit_cast(bf16x8_t, raw);
+  }
+
+  const int64_t kbase = (p.cu_seqlens ? 0 : b * p.sk_b) + h * p.sk_h;
+  const int64_t vbase = (p.cu_seqlens ? 0 : b * p.sv_b) + h * p.sv_h;
+  const int nblocks = (L + kKB - 1) / kKB;
+
+  f32x16_t o0 = {0}, o1 = {0};  // O^T tiles: d in [0,32) and [32,64)
+  float m = -INFINITY;
+  float lsum = 0.f;
+
+  Stage<FP8, VT> st;
+  stage_load<FP8, VT>(st, p, kbase, vbase, off, L, 0);
+  stage_store<FP8, VT>(st, sK[0], sV[0]);
+  __syncthreads();
+
+  for (int blk = 0; blk < nblocks; ++blk) {
+    const int cur = blk & 1;
+    const bool more = blk + 1 < nblocks;
+    if (more) stage_load<FP8, VT>(st, p, kbase, vbase, off, L, (blk + 1) * kKB);
+
+    const uint16_t* K = sK[cur];
+    const uint16_t* Vt = sV[cur];
+    // S^T for the two 32-key tiles.
+    f32x16_t s0 = {0}, s1 = {0};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(K + col * kRow + 16 * s + 8 * hh);
+      const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(K + (32 + col) * kRow + 16 * s + 8 * hh);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[s], s1, 0, 0, 0);
+    }
+    // Entry i of tile t is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8).
+    const int kv0 = blk * kKB;
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kin = (i < 8) ? (8 * hh + i) : (16 + 8 * hh + (i - 8));
+      x[i] = (kv0 + kin < L) ? s0[i] * sl2 : -INFINITY;
+      x[16 + i] = (kv0 + 32 + kin < L) ? s1[i] * sl2 : -INFINITY;
+    }
+    float bmax = x[0];
+#pragma unroll
+    for (int i = 1; i < 32; ++i) bmax = fmaxf(bmax, x[i]);
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    const float mn = fmaxf(m, bmax);
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);  // m = -inf on the first block -> 0
+    m = mn;
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      x[i] = __builtin_amdgcn_exp2f(x[i] - mn);
+      psum += x[i];
+    }
+    lsum = lsum * alpha + psum;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      o0[i] *= alpha;
+      o1[i] *= alpha;
+    }
+    // P^T as B operands: k-step (tile t, half s) = entries 16 t + 8 s + 0..7.
+    bf16x8_t pb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8_t v;
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        f32x2_t two = {x[8 * ks + j], x[8 * ks + j + 1]};
+        const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
+        v[j] = c[0];
+        v[j + 1] = c[1];
+      }
+      pb[ks] = v;
+    }
+    // O^T += V^T . P^T ; k-step ks covers keys 16 ks + 8 hh + 0..7 of the block.
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(Vt + col * kRow + 16 * ks + 8 * hh);
+      const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(Vt + (32 + col) * kRow + 16 * ks + 8 * hh);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pb[ks], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pb[ks], o1, 0, 0, 0);
+    }
+    if (more) stage_store<FP8, VT>(st, sK[cur ^ 1], sV[cur ^ 1]);
+    __syncthreads();
+  }
+
+  lsum += __shfl_xor(lsum, 32, 64);
+  const float inv = vscale / lsum;
+  if (q_ok) {
+    // O^T entry i of tile t: d = 32 t + 8 (i / 4) + 4 hh + i % 4 ; four consecutive d per group.
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = 32 * t + 8 * g4 + 4 * hh;
+        if (d0 < p.D) {
+          float vals[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vals[e] = (t == 0 ? o0[4 * g4 + e] : o1[4 * g4 + e]) * inv;
+          f32x2_t a = {vals[0], vals[1]}, c = {vals[2], vals[3]};
+          const bf16x2_t ba = __builtin_convertvector(a, bf16x2_t);
+          const bf16x2_t bc = __builtin_convertvector(c, bf16x2_t);
+          uint2 packed;
+          packed.x = __builtin_bit_cast(uint32_t, ba);
+          packed.y = __builtin_bit_cast(uint32_t, bc);
+          *reinterpret_cast<uint2*>(Op + q * p.so_q + d0) = packed;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace svhip
+
+using namespace svhip;
+
+extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void* o, int kv_dtype,
+                               const int32_t* kv_len, const int32_t* cu_seqlens, const float* k_scale,
+                               const float* v_scale, int64_t B, int64_t H, int64_t Q, int64_t D, int64_t kv_cap,
+                               int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b, int64_t sk_h, int64_t sk_k,
+                               int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d, int64_t so_b, int64_t so_h,
+                               int64_t so_q, float scale, void* stream) {
+  const char* name = "svhip_xattn_fwd";
+  clear_error();
+  SVHIP_REQUIRE(q && k && v && o, "%s: null pointer", name);
+  SVHIP_REQUIRE(kv_len || cu_seqlens, "%s: need kv_len or cu_seqlens", name);
+  SVHIP_REQUIRE(B >= 0 && H >= 1 && Q >= 0, "%s: bad sizes", name);
+  SVHIP_REQUIRE(D >= 8 && D <= kDPad && D % 8 == 0, "%s: head_dim %lld unsupported (multiple of 8, <= 64)", name,
+                (long long)D);
+  SVHIP_REQUIRE(kv_dtype == SVHIP_BF16 || kv_dtype == SVHIP_FP8_E4M3, "%s: kv dtype %d unsupported", name, kv_dtype);
+  const bool fp8 = kv_dtype == SVHIP_FP8_E4M3;
+  SVHIP_REQUIRE(!fp8 || (k_scale && v_scale), "%s: fp8 K/V need k_scale and v_scale", name);
+  SVHIP_REQUIRE(sv_k == 1 || sv_d == 1, "%s: V needs a unit stride along keys or head_dim", name);
+  const bool vt = sv_k == 1 && sv_d != 1;
+  const size_t eb = fp8 ? 1 : 2;
+  // Row starts must allow 16-byte (bf16) / 8-byte (fp8) vector loads.
+  const uintptr_t align = fp8 ? 8 : 16;
+  SVHIP_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && (sq_q * 2) % 16 == 0 && (sq_h * 2) % 16 == 0 &&
+                    (sq_b * 2) % 16 == 0,
+                "%s: Q rows must be 16-byte aligned", name);
+  SVHIP_REQUIRE(reinterpret_cast<uintptr_t>(o) % 8 == 0 && (so_q * 2) % 8 == 0 && (so_h * 2) % 8 == 0 &&
+                    (so_b * 2) % 8 == 0,
+                "%s: O rows must be 8-byte aligned", name);
+  SVHIP_REQUIRE(reinterpret_cast<uintptr_t>(k) % align == 0 && (sk_k * eb) % align == 0 &&
+                    (sk_h * eb) % align == 0 && (sk_b * eb) % align == 0,
+                "%s: K rows must be %d-byte aligned", name, (int)align);
+  if (!vt) {
+    SVHIP_REQUIRE(reinterpret_cast<uintptr_t>(v) % align == 0 && (sv_k * eb) % align == 0 &&
+                      (sv_h * eb) % align == 0 && (sv_b * eb) % align == 0,
+                  "%s: V rows must be %d-byte aligned", name, (int)align);
+  }
+  if (B == 0 || Q == 0) return SVHIP_OK;
+  XattnParams p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = o;
+  p.kv_len = kv_len;
+  p.cu_seqlens = cu_seqlens;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.B = B;
+  p.H = H;
+  p.Q = Q;
+  p.D = D;
+  p.kv_cap = kv_cap;
+  p.sq_b = sq_b;
+  p.sq_h = sq_h;
+  p.sq_q = sq_q;
+  p.sk_b = sk_b;
+  p.sk_h = sk_h;
+  p.sk_k = sk_k;
+  p.sv_b = sv_b;
+  p.sv_h = sv_h;
+  p.sv_k = sv_k;
+  p.sv_d = sv_d;
+  p.so_b = so_b;
+  p.so_h = so_h;
+  p.so_q = so_q;
+  p.scale_log2 = scale * kLog2e;
+  p.q_tiles = static_cast<int>(cdiv(Q, kQTile));
+  const int64_t grid = static_cast<int64_t>(p.q_tiles) * H * B;
+  SVHIP_REQUIRE(grid < (1ll << 31), "%s: grid too large", name);
+  hipStream_t s = as_stream(stream);
+  if (fp8) {
+    if (vt) {
+      xattn_fwd_kernel<true, true><<<static_cast<unsigned>(grid), kThreads, 0, s>>>(p);
+    } else {
+      xattn_fwd_kernel<true, false><<<static_cast<unsigned>(grid), kThreads, 0, s>>>(p);
+    }
+  } else {
+    if (vt) {
+      xattn_fwd_kernel<false, true><<<static_cast<unsigned>(grid), kThreads, 0, s>>>(p);
+    } else {
+      xattn_fwd_kernel<false, false><<<static_cast<unsigned>(grid), kThreads, 0, s>>>(p);
+    }
+  }
+  SVHIP_LAUNCHED(name);
+  return SVHIP_OK;
+}

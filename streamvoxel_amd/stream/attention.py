@@ -1,0 +1,88 @@
+"""Cross attention over packed, variable-length cached K/V on the GPU.
+
+Replaces the attention core of `cross_flex` (`flex_attention()(query, key, val, block_mask=...)`,
+streamvoxel/stream/fast_ops.py:104-108) and of the masked SDPA forms (streamvoxel/stream/engine.py:28-47,
+streamvoxel/stream/fast_ops.py:111-115): per window b only the first L_b keys are attended.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from streamvoxel_amd import _lib
+
+FP8_DTYPES = tuple(getattr(torch, n) for n in ('float8_e4m3fn',) if hasattr(torch, n))
+
+
+def _kv_code(t):
+    if t.dtype == torch.bfloat16:
+        return _lib.SVHIP_BF16
+    if t.dtype in FP8_DTYPES or t.dtype == torch.uint8:
+        return _lib.SVHIP_FP8_E4M3
+    raise TypeError(f'K/V dtype {t.dtype} unsupported (bfloat16, float8_e4m3fn or uint8 e4m3 codes)')
+
+
+def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scale=None, v_scale=None, out=None):
+    """softmax(scale * Q K^T) V over the first L_b keys of every window b.
+
+    query [B,H,Q,D] bf16 (head_dim contiguous; any other strides). key, val: padded [B,H,Kcap,D] with
+    lengths int32 [B] (device), or packed [H, sum L, D] with cu_seqlens int32 [B+1] (device). `val` may be a
+    transposed view (keys contiguous, e.g. `vt.transpose(-1, -2)` of a [B,H,D,Kcap] buffer), which the kernel
+    stages fastest. K/V in float8_e4m3fn (or uint8 codes) need k_scale / v_scale fp32 [B,H] (device).
+    `out` (optional) [B,H,Q,D] bf16 with head_dim contiguous, e.g. a [B,Q,H,D] buffer's transpose(1, 2) view.
+    Returns out."""
+    _lib.require_gpu(query, key, val, lengths, cu_seqlens, k_scale, v_scale, out)
+    if query.dtype != torch.bfloat16:
+        raise TypeError('query must be bfloat16')
+    B, H, Q, D = query.shape
+    if (lengths is None) == (cu_seqlens is None):
+        raise ValueError('pass exactly one of lengths / cu_seqlens')
+    code = _kv_code(key)
+    if _kv_code(val) != code:
+        raise TypeError('key and val must share a dtype')
+    if code == _lib.SVHIP_FP8_E4M3 and (k_scale is None or v_scale is None):
+        raise ValueError('fp8 K/V need k_scale and v_scale')
+    if query.stride(-1) != 1 or key.stride(-1) != 1:
+        raise ValueError('query and key need a contiguous head_dim')
+    if out is None:
+        out = torch.empty((B, H, Q, D), dtype=torch.bfloat16, device=query.device)
+    if out.shape != (B, H, Q, D) or out.stride(-1) != 1 or out.dtype != torch.bfloat16:
+        raise ValueError('out must be bf16 [B,H,Q,D] with a contiguous head_dim')
+    if cu_seqlens is not None:
+        if key.dim() != 3 or val.dim() != 3:
+            raise ValueError('packed K/V are [H, sum L, D]')
+        if cu_seqlens.dtype != torch.int32 or cu_seqlens.numel() != B + 1:
+            raise ValueError('cu_seqlens must be int32 [B+1]')
+        kcap = key.shape[1]
+        sk = (0, key.stride(0), key.stride(1))
+        sv = (0, val.stride(0), val.stride(1), val.stride(2))
+    else:
+        if key.dim() != 4 or key.shape[:2] != (B, H) or val.shape != key.shape:
+            raise ValueError('padded K/V are [B,H,Kcap,D] like the query')
+        if lengths.dtype != torch.int32 or lengths.numel() != B:
+            raise ValueError('lengths must be int32 [B]')
+        kcap = key.shape[2]
+        sk = (key.stride(0), key.stride(1), key.stride(2))
+        sv = (val.stride(0), val.stride(1), val.stride(2), val.stride(3))
+    if key.shape[-1] != D or val.shape[-1] != D:
+        raise ValueError('head_dim mismatch')
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    lib = _lib.load()
+    kp = key.view(torch.uint8) if code == _lib.SVHIP_FP8_E4M3 else key
+    vp = val.view(torch.uint8) if code == _lib.SVHIP_FP8_E4M3 else val
+    _lib.check(lib.svhip_xattn_fwd(
+        _lib.ptr(query), _lib.ptr(kp), _lib.ptr(vp), _lib.ptr(out), code, _lib.ptr(lengths), _lib.ptr(cu_seqlens),
+        _lib.ptr(k_scale), _lib.ptr(v_scale), B, H, Q, D, kcap, query.stride(0), query.stride(1), query.stride(2),
+        *sk, *sv, out.stride(0), out.stride(1), out.stride(2), scale, _lib.stream_of(query)), 'svhip_xattn_fwd')
+    return out
+
+
+def quantize_e4m3(x, dim_b=0, dim_h=1):
+    """Per-(window, head) e4m3 quantisation of cached K or V [B,H,L,D] (or a transposed view): scale = amax / 448
+    (the reference's e4m3 convention, scripts/bench_ops.py:506-522). Returns (codes float8_e4m3fn, scale fp32 [B,H]).
+    Runs once per window at load time with torch ops; not on the per-step path."""
+    amax = x.detach().abs().float().amax(dim=(2, 3))
+    scale = torch.clamp(amax / 448.0, min=1e-12)
+    codes = (x.float() / scale[:, :, None, None]).to(torch.float8_e4m3fn)
+    return codes, scale.contiguous()

@@ -1,0 +1,68 @@
+"""CPU checks of the C ABI: the library builds/loads and exports every function include/svhip.h declares, and the
+host-side argument checks reject bad input without touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'svhip.h')
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(svhip_[a-z0-9_]+)\s*\(', text)))
+
+
+@pytest.fixture(scope='module')
+def lib():
+    from streamvoxel_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from streamvoxel_amd.build import build
+        build()
+    return _lib.load()
+
+
+def test_header_declares_the_hot_path_entry_points():
+    names = declared_functions()
+    for expected in ('svhip_entropy', 'svhip_air_prob', 'svhip_lel_update', 'svhip_top_mask', 'svhip_quota_select',
+                     'svhip_quota_select_workspace_bytes', 'svhip_ease_select', 'svhip_ease_select_workspace_bytes',
+                     'svhip_xattn_fwd', 'svhip_last_error', 'svhip_version'):
+        assert expected in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from streamvoxel_amd import _lib
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+    assert lib.svhip_version() >= 100
+
+
+def test_workspace_queries_and_argument_errors(lib):
+    n = lib.svhip_quota_select_workspace_bytes(8, 256, 16, 16, 4)
+    assert n >= 8 * 1024 * 16 + 8 * 8
+    assert lib.svhip_ease_select_workspace_bytes(8, 256, 16, 16, 4) >= n + 8 * 65536 * 4
+    assert lib.svhip_quota_select_workspace_bytes(1, 256, 16, 16, 3) == 0          # unsupported block size
+    assert b'unsupported' in lib.svhip_last_error()
+    assert lib.svhip_quota_select_workspace_bytes(1, 256, 16, 12, 8) == 0          # 12 not divisible by 8
+    assert b'divisible' in lib.svhip_last_error()
+    # null pointers are rejected on the host (no launch happens)
+    rc = lib.svhip_entropy(None, 0, 1, 256, 65536, 0, 65536, 1, None, None)
+    assert rc == -1 and b'null' in lib.svhip_last_error()
+    rc = lib.svhip_xattn_fwd(*([None] * 4), 1, None, None, None, None, 1, 1, 1, 64, 64, *([0] * 13), 0.125, None)
+    assert rc == -1
+    rc = lib.svhip_top_mask(None, None, 1, 16, None, 3, None, None)
+    assert rc == -1
+
+
+def test_product_refuses_host_tensors():
+    import torch
+    from streamvoxel_amd.sampling.entropy import entropy_scores
+    from streamvoxel_amd.sampling.block_quota import top_mask
+    with pytest.raises(RuntimeError, match='GPU'):
+        entropy_scores(torch.zeros(4, 2, 2, 2))
+    with pytest.raises(RuntimeError, match='GPU'):
+        top_mask(torch.zeros(8), torch.ones(8, dtype=torch.bool), 3)
