@@ -1,0 +1,337 @@
+"""Benchmark of the per-step generation hot path on one MI355X.
+
+Workload (one "step" = one HIP-graph replay): 8 windows (slots) of [256,16,16] voxels, 12 cross-attention layers
+(bf16, 12 heads x 64, 1024 queries per window, cached K/V of L_b = 1552 + 1024 k_b keys, k_b ~ U{0..8}) followed by
+the EASE selection of the step over [8 x 65536, 256] fp32 logits (entropy, 4^3 block quota with trim / top-up,
+commit of the chosen voxels). A window is 26 forwards: one low-entropy-last marking step and 25 solid steps with
+the quarter-cosine quotas; the high-entropy share of the logits drifts from 30% to 5% over the window.
+
+  value = voxels/s = 8 * 65536 / (26 * t_step)
+
+The backbone (self-attention, MLP), the logit producer and the categorical sampling tail are not part of the step.
+Queries are drawn N(0,1)/8 per step and layer, logits per step, all resident in HBM before timing; K/V are
+projected once from seeded context tokens with random-init weights (no checkpoint is published).
+
+Prints one JSON line (rank 0). `--gpus N` with N > 1 is refused: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = 'voxels/sec on 1 GPU (8 slots); cross-attn MFMA util; EASE select HBM GB/s'
+SLOTS, LAYERS, HEADS, HEAD_DIM, QUERIES, WIDTH = 8, 12, 12, 64, 1024, 768
+SHAPE, CLASSES, BLOCK, STEPS_PER_WINDOW = (256, 16, 16), 256, 4, 26
+VOXELS = SHAPE[0] * SHAPE[1] * SHAPE[2]
+PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
+LAST_EPS = 1e-4
+
+
+def log(msg):
+    print(f'[bench] {msg}', file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=26)
+    p.add_argument('--warmup', type=int, default=26)
+    p.add_argument('--seed', type=int, default=2026)
+    p.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
+    p.add_argument('--cpu-seconds', type=float, default=15.0, help='bounded CPU sample budget')
+    p.add_argument('--kv-dtype', default='bf16', choices=['bf16', 'fp8'])
+    return p.parse_args()
+
+
+def window_schedule(last_counts):
+    """Per window slot: the 25 solid quotas of a quarter-cosine schedule with the deferred count taken from the
+    tail (the smallest cap giving 25 positive quotas)."""
+    from streamvoxel_amd.sampling.low_entropy_last import low_entropy_last_quotas
+    out = []
+    for n_last in last_counts:
+        cap = STEPS_PER_WINDOW - 1
+        while True:
+            q = low_entropy_last_quotas(VOXELS, cap, n_last)
+            if len(q) >= STEPS_PER_WINDOW - 1:
+                break
+            cap += 1
+        out.append(q[:STEPS_PER_WINDOW - 1] if len(q) == STEPS_PER_WINDOW - 1 else q)
+    return out
+
+
+class Workload:
+    def __init__(self, dev, seed, kv_dtype):
+        import torch
+        from streamvoxel_amd import synth
+        from streamvoxel_amd.stream.step import CachedContext, EaseSelect
+
+        self.dev = dev
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.lengths = synth.kv_lengths(SLOTS, seed)
+        kv_cap = max(self.lengths)
+        log(f'kv lengths {self.lengths}')
+        self.ctx = CachedContext(LAYERS, SLOTS, HEADS, HEAD_DIM, synth.MAX_KEYS, dev, kv_dtype)
+        # K/V projected once per window from seeded context tokens (random-init projection per layer).
+        for layer in range(LAYERS):
+            w = torch.randn(WIDTH, 2 * WIDTH, device=dev, generator=g) / math.sqrt(WIDTH)
+            for b, L in enumerate(self.lengths):
+                tokens = torch.randn(L, WIDTH, device=dev, generator=g)
+                kv = (tokens @ w).reshape(L, 2, HEADS, HEAD_DIM).permute(1, 2, 0, 3)   # [2, H, L, D]
+                self.ctx.write(layer, b, kv[0].to(torch.bfloat16), kv[1].to(torch.bfloat16))
+        # Queries: one [8,12,1024,64] bf16 tensor per (step, layer), produced in the projection's [B,Q,H,D] layout.
+        self.q = [[(torch.randn(SLOTS, QUERIES, HEADS, HEAD_DIM, device=dev, generator=g) / 8).to(torch.bfloat16)
+                   .transpose(1, 2) for _ in range(LAYERS)] for _ in range(STEPS_PER_WINDOW)]
+        self.o = [torch.empty(SLOTS, QUERIES, HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+                  for _ in range(LAYERS)]
+        # Marking logits: certain air (class 0 + 30) above a seeded terrain height per column.
+        self.sel = EaseSelect(SLOTS, SHAPE, CLASSES, BLOCK, dev, air_ids=(0,))
+        mark = torch.empty(SLOTS * VOXELS, CLASSES, device=dev)
+        synth.bimodal_logits_(mark, 0.7, generator=g)
+        height = torch.randint(64, 192, (SLOTS, 1, SHAPE[1], SHAPE[2]), device=dev, generator=g)
+        y = torch.arange(SHAPE[0], device=dev).reshape(1, -1, 1, 1)
+        air = (y > height).reshape(-1)
+        mark[air, 0] += 30.0
+        self.mark_logits = mark
+        # Solid-step logits, the uncertain share drifting 30% -> 5%.
+        solid = STEPS_PER_WINDOW - 1
+        self.logits = []
+        for s in range(solid):
+            x = torch.empty(SLOTS * VOXELS, CLASSES, device=dev)
+            synth.bimodal_logits_(x, 1.0 - synth.high_entropy_share(s, solid), generator=g)
+            self.logits.append(x)
+        # One marking pass (eager) gives the deferred counts -> per-slot quotas (host, once per window).
+        self.sel.tokens.fill_(CLASSES)
+        self.sel.last.zero_()
+        self.sel.mark(self.mark_logits, LAST_EPS)
+        torch.cuda.synchronize()
+        self.last_counts = self.sel.last.sum(1).tolist()
+        self.quotas = window_schedule(self.last_counts)
+        log(f'last counts {self.last_counts}; solid quotas slot0 {self.quotas[0][:4]}...{self.quotas[0][-2:]}')
+        orders = [torch.randperm(VOXELS // BLOCK ** 3, generator=torch.Generator().manual_seed(seed + 9173 + b))
+                  for b in range(SLOTS)]
+        for b in range(SLOTS):
+            self.sel.bind_window(b, orders[b])
+        # Per-step scalar tables (copied into the select buffers inside each step's graph).
+        ks, coms, fracs = [], [], []
+        for s in range(solid):
+            k = [self.quotas[b][s] for b in range(SLOTS)]
+            com = [sum(self.quotas[b][:s]) for b in range(SLOTS)]
+            fr = [(com[b] + k[b]) / (VOXELS - self.last_counts[b]) for b in range(SLOTS)]
+            ks.append(torch.tensor(k, dtype=torch.int64, device=dev))
+            coms.append(torch.tensor(com, dtype=torch.int64, device=dev))
+            fracs.append(torch.tensor(fr, dtype=torch.float64, device=dev))
+        self.k_tab, self.com_tab, self.frac_tab = ks, coms, fracs
+        self.bad_seen = torch.zeros(SLOTS, dtype=torch.bool, device=dev)
+        self.flops_per_layer = 4 * HEADS * HEAD_DIM * QUERIES * sum(self.lengths)
+        self.select_bytes = SLOTS * VOXELS * (CLASSES * 4 + 8 + 1 + 1)
+
+    # -- step bodies (captured)
+    def attention_layers(self, step):
+        for layer in range(LAYERS):
+            self.ctx.attend(layer, self.q[step][layer], out=self.o[layer].transpose(1, 2))
+
+    def marking_step(self):
+        self.sel.tokens.fill_(CLASSES)
+        self.sel.last.zero_()
+        self.attention_layers(0)
+        self.sel.mark(self.mark_logits, LAST_EPS)
+
+    def solid_step(self, s):
+        self.sel.k.copy_(self.k_tab[s])
+        self.sel.committed.copy_(self.com_tab[s])
+        self.sel.frac.copy_(self.frac_tab[s])
+        self.attention_layers(s + 1)
+        self.sel.run(self.logits[s])
+        self.bad_seen |= self.sel.bad
+        self.sel.tokens.masked_fill_(self.sel.chosen.view(SLOTS, VOXELS), 1)
+        if s == STEPS_PER_WINDOW - 2:
+            self.sel.tokens.masked_fill_(self.sel.last, 0)     # finish: deferred voxels become air
+
+    def capture(self):
+        import torch
+        stream = torch.cuda.Stream(self.dev)
+        stream.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(stream):
+            self.marking_step()
+            for s in range(STEPS_PER_WINDOW - 1):
+                self.solid_step(s)
+        torch.cuda.current_stream(self.dev).wait_stream(stream)
+        torch.cuda.synchronize()
+        graphs = []
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            self.marking_step()
+        graphs.append(g)
+        for s in range(STEPS_PER_WINDOW - 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                self.solid_step(s)
+            graphs.append(g)
+        torch.cuda.synchronize()
+        self.bad_seen.zero_()
+        return graphs
+
+
+def time_events(fn, reps, warm=3):
+    import torch
+    for _ in range(warm):
+        fn()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps / 1e3   # seconds per call
+
+
+def measured_peaks(dev):
+    import torch
+    out = {}
+    a = torch.empty(1 << 28, dtype=torch.float32, device=dev)     # 1 GiB
+    b = torch.empty_like(a)
+    a.normal_()
+    t = time_events(lambda: b.copy_(a), 10)
+    out['copy_GBps'] = 2 * a.numel() * 4 / t / 1e9
+    del a, b
+    m = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+    n = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+    t = time_events(lambda: torch.mm(m, n), 10)
+    out['bf16_gemm_TFLOPs'] = 2 * 8192 ** 3 / t / 1e12
+    return out
+
+
+def cpu_baseline(w, budget_s):
+    """The oracle (CPU restatement of the reference path) on the host cores, on a bounded sample: masked fp32 SDPA
+    over the padded keys of one layer for 2 windows, and the entropy + block-quota selection of 1 window;
+    extrapolated linearly to the full step (8 windows x 12 layers + 8 selections)."""
+    import numpy as np
+    import torch
+
+    from oracle import attention as A
+    from oracle import sampling as S
+    threads = torch.get_num_threads()
+    kcap = w.ctx.kv_cap
+    lengths = torch.tensor(w.lengths, dtype=torch.int64)
+    q = w.q[1][0].float().cpu()
+    k = w.ctx.k[0].float().cpu()
+    v = w.ctx.vt[0].float().cpu().transpose(2, 3).contiguous()
+    sel_logits = w.logits[0][:VOXELS].cpu()                    # window 0, voxel-major [N, C]
+    tokens = w.sel.tokens.new_full((VOXELS,), CLASSES).cpu().numpy()
+    last = w.sel.last[0].cpu().numpy()
+    pos = w.sel.pos[0].cpu().numpy()
+    n_total = w.sel.n_total[0].cpu().numpy()
+    k0 = int(w.k_tab[0][0])
+    frac0 = float(w.frac_tab[0][0])
+    attn_times, sel_times = [], []
+    began = time.perf_counter()
+    while True:
+        for b in (0, 1):
+            t0 = time.perf_counter()
+            A.masked_sdpa(q[b:b + 1], k[b:b + 1], v[b:b + 1], lengths[b:b + 1])
+            attn_times.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        score = S.entropy_scores(sel_logits.T).numpy().reshape(SHAPE)
+        selectable = ((tokens == CLASSES) & ~last).reshape(SHAPE)
+        S.quota_select_nosync(score, selectable, k0, BLOCK, pos, frac0, n_total, 0)
+        sel_times.append(time.perf_counter() - t0)
+        if time.perf_counter() - began > budget_s or len(sel_times) >= 5:
+            break
+    t_attn = float(np.median(attn_times))          # one window, one layer
+    t_sel = float(np.median(sel_times))            # one window
+    t_step = SLOTS * LAYERS * t_attn + SLOTS * t_sel
+    return dict(value=SLOTS * VOXELS / (STEPS_PER_WINDOW * t_step), unit='voxels/s', cores=threads, kind='port',
+                sample=(f'{len(attn_times)} x masked fp32 SDPA (1 window, 1 layer, {HEADS}x{HEAD_DIM}, {QUERIES} '
+                        f'queries, {kcap} padded keys) + {len(sel_times)} x fp32 entropy + block-quota select of one '
+                        f'[256,16,16] window (C={CLASSES}); step extrapolated x{SLOTS * LAYERS} / x{SLOTS}'),
+                seconds_per_step=t_step, attn_s_per_window_layer=t_attn, select_s_per_window=t_sel,
+                cpu_count=os.cpu_count(), wall_s=time.perf_counter() - began)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps(dict(error='this build measures one GPU; --gpus must be 1', n_gpus=args.gpus)), flush=True)
+        sys.exit(2)
+    import torch
+    import streamvoxel_amd
+    streamvoxel_amd.load()
+    dev = torch.device('cuda:0')
+    t0 = time.perf_counter()
+    w = Workload(dev, args.seed, args.kv_dtype)
+    log(f'inputs ready in {time.perf_counter() - t0:.1f}s')
+    graphs = w.capture()
+    log('graphs captured')
+    n_graphs = len(graphs)
+    for i in range(args.warmup):
+        graphs[i % n_graphs].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(args.steps):
+        graphs[i % n_graphs].replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / args.steps
+    bad = bool(w.bad_seen.any())
+    log(f'{ms_per_step:.3f} ms/step, bad={bad}')
+    value = SLOTS * VOXELS / (STEPS_PER_WINDOW * ms_per_step / 1e3)
+
+    # Component timings with HIP events on the launching stream (the current stream).
+    t_layer = time_events(lambda: w.ctx.attend(0, w.q[1][0], out=w.o[0].transpose(1, 2)), 20)
+    w.sel.k.copy_(w.k_tab[0])
+    w.sel.committed.copy_(w.com_tab[0])
+    w.sel.frac.copy_(w.frac_tab[0])
+    w.sel.tokens.fill_(CLASSES)
+    t_select = time_events(lambda: w.sel.run(w.logits[0]), 20)
+    from streamvoxel_amd.sampling.entropy import entropy_batched
+    ent_out = torch.empty(SLOTS, VOXELS, device=dev)
+    t_entropy = time_events(lambda: entropy_batched(w.logits[0].view(SLOTS, VOXELS, CLASSES), 'voxel_major',
+                                                    out=ent_out), 20)
+    xattn_tflops = w.flops_per_layer / t_layer / 1e12
+    select_gbs = w.select_bytes / t_select / 1e9
+    entropy_bytes = SLOTS * VOXELS * (CLASSES * 4 + 4)
+    peaks = measured_peaks(dev)
+    log(f'xattn {t_layer * 1e6:.1f} us/layer = {xattn_tflops:.1f} TFLOP/s; select {t_select * 1e6:.1f} us = '
+        f'{select_gbs:.0f} GB/s; entropy {t_entropy * 1e6:.1f} us; peaks {peaks}')
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(w, args.cpu_seconds)
+        log(f'cpu baseline {cpu["value"]:.1f} voxels/s ({cpu["seconds_per_step"]:.2f} s/step)')
+    result = dict(
+        metric=METRIC, value=value, unit='voxels/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=ms_per_step, higher_is_better=True, scaling='weak', vs_baseline=None, dtype='bf16',
+        data='synthetic',
+        config=dict(workload=('8-slot step: 12 cross-attn layers (bf16 MFMA, 12x64 heads, 1024 queries, cached K/V '
+                              'L_b=1552+1024k_b) + EASE select over [8x65536,256] fp32 logits, one HIP graph per step; '
+                              '26 steps per window'),
+                    slots=SLOTS, layers=LAYERS, heads=HEADS, head_dim=HEAD_DIM, queries=QUERIES,
+                    kv_lengths=w.lengths, kv_dtype=args.kv_dtype, window=list(SHAPE), classes=CLASSES, block=BLOCK,
+                    steps_per_window=STEPS_PER_WINDOW, parallelism='single GPU (slots are independent)'),
+        roofline=dict(kernel='xattn_fwd_kernel', bound='mfma', achieved=xattn_tflops, peak=PEAK_BF16_TFLOPS,
+                      unit='TFLOP/s', frac=xattn_tflops / PEAK_BF16_TFLOPS, traffic=None,
+                      flops_per_launch=w.flops_per_layer, avg_launch_us=t_layer * 1e6),
+        roofline_select=dict(kernel='svhip_ease_select (entropy + apportion + in-block + fix)', bound='hbm',
+                             achieved=select_gbs, peak=PEAK_HBM_GBS, unit='GB/s', frac=select_gbs / PEAK_HBM_GBS,
+                             bytes_per_call=w.select_bytes, avg_call_us=t_select * 1e6,
+                             entropy_kernel_GBps=entropy_bytes / t_entropy / 1e9, entropy_us=t_entropy * 1e6),
+        components=dict(xattn_ms_per_step=LAYERS * t_layer * 1e3, select_ms_per_step=t_select * 1e3,
+                        selection_bad_flag_seen=bad),
+        measured_peaks=peaks,
+        cpu_baseline=cpu,
+    )
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()
