@@ -113,7 +113,8 @@ int svhip_ease_select(const void* logits, int dtype, int64_t classes, int64_t st
  * head_dim, the reference layout) or sv_k == 1 (V stored transposed, keys contiguous: the fast staging path);
  * row = j, or cu_seqlens[b] + j in the packed layout (sk_b / sv_b are then ignored). kv_dtype SVHIP_BF16, or
  * SVHIP_FP8_E4M3 (OCP e4m3fn bytes) with per-(window, head) fp32 dequantisation scales k_scale/v_scale [B,H].
- * head_dim: 64 (48 is accepted and zero-padded to 64 inside the kernel). fp32 accumulation.
+ * head_dim: a multiple of 8 up to 64 (48 and below are zero-padded to 64 inside the kernel). fp32 accumulation.
+ * scale: the softmax scale, > 0 (the reference uses 1/sqrt(head_dim)).
  * Replaces: flex_attention over PackedKeys' block mask in cross_flex (streamvoxel/stream/fast_ops.py:104-108,
  * 122-159) and the masked SDPA in SlotCrossAttention.forward / cross_sdpa (streamvoxel/stream/engine.py:28-47,
  * streamvoxel/stream/fast_ops.py:111-115).

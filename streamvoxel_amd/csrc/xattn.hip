@@ -13,11 +13,23 @@
 // stored in LDS under the involution sigma (swap of the 4-row groups 1 and 2 of every 16 rows), so accumulator
 // entries i = 0..7 of lane l hold keys 8*(l/32) + i and i = 8..15 keys 16 + 8*(l/32) + (i-8): exactly the B
 // operand slice (k index 8*(l/32) + j) the second product needs, with no cross-lane movement.
-// Because O^T's columns are queries too, the per-query rescale (alpha) and the final 1/l are lane-local.
+// Because O^T's columns are queries too, the per-query rescale and the final 1/l are lane-local.
 //
-// K/V dtypes: bf16, or OCP e4m3fn bytes converted exactly to bf16 during staging; the fp8 scales are folded into
-// the softmax scale (k_scale) and the output (v_scale). V may be stored row-major ([key][d], transposed while
-// staging) or transposed ([d][key], staged with 16-byte copies).
+// The softmax is VALU-bound at head_dim 64 (one exp per score against 2 x 64 MACs), so per score it costs one
+// max3 third, one fma (scale and max subtraction fused), one exp, half a bf16 pack and half a bf16 dot (the row
+// sum is taken over the packed bf16 P, the same values the second product consumes):
+//   * the stored running max m is only raised when a block's max exceeds it by more than kLazy (log2 units);
+//     otherwise P may reach 2^kLazy, harmless in fp32 sums and bf16 P, and the O / l rescale is skipped for the
+//     whole wave. O and l always share the same m, so O / l is unchanged.
+//   * key masking runs only in the last, partial block; padding keys are staged as zeros.
+//
+// K/V dtypes: bf16, or OCP e4m3fn bytes converted exactly to bf16 during staging (v_cvt_scalef32_pk_bf16_fp8
+// with scale 1); the fp8 scales are folded into the softmax scale (k_scale) and the output (v_scale). V may be
+// stored row-major ([key][d], transposed while staging) or transposed ([d][key], staged with vector copies).
+//
+// Workgroup order: windows are ranked by key count (longest first, ties by index) inside the kernel, so the
+// longest (window, head) pairs start first; consecutive workgroup ids go round robin to the 8 XCDs and all query
+// tiles of one (window, head) pair land on the same XCD, which reads that pair's K/V into its L2 once.
 #include <type_traits>
 
 #include "common.hpp"
@@ -34,6 +46,8 @@ constexpr int kKB = 64;       // keys per block
 constexpr int kDPad = 64;     // head_dim handled by the MFMA tiles (smaller head_dim is zero-padded)
 constexpr int kRow = 72;      // LDS row stride in bf16 elements (144 bytes: conflict-free 16-byte reads)
 constexpr int kThreads = 256;
+constexpr float kLazy = 8.0f;  // log2-domain headroom before the running max is raised
+constexpr int kMaxRankWindows = 4096;
 
 struct XattnParams {
   const void* q;
@@ -49,7 +63,7 @@ struct XattnParams {
   int64_t sk_b, sk_h, sk_k;
   int64_t sv_b, sv_h, sv_k, sv_d;
   int64_t so_b, so_h, so_q;
-  float scale_log2;  // softmax scale * log2(e)
+  float scale_log2;  // softmax scale * log2(e), > 0
   int q_tiles;
 };
 
@@ -61,28 +75,22 @@ __device__ __forceinline__ int sigma_row(int key) {
   return (key & ~15) | swapped;
 }
 
-// OCP e4m3fn byte -> bf16 bits (exact: every e4m3 value is a bf16 value).
-__device__ __forceinline__ uint32_t e4m3_to_bf16_bits(uint32_t byte) {
-  const uint32_t s = (byte & 0x80u) << 8;
-  const uint32_t e = (byte >> 3) & 0xfu;
-  const uint32_t m = byte & 0x7u;
-  if (e == 0xfu && m == 0x7u) return s | 0x7fc0u;  // NaN
-  if (e != 0u) return s | ((e + 120u) << 7) | (m << 4);
-  if (m == 0u) return s;
-  const float f = static_cast<float>(m) * 0x1p-9f;  // subnormal: m * 2^-9
-  return s | (__float_as_uint(f) >> 16);
+// 8 OCP e4m3fn bytes (two dwords) -> 8 bf16 packed in a uint4 (exact: every e4m3 value is a bf16 value).
+__device__ __forceinline__ uint4 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+  const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+  const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+  const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+  return make_uint4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, c),
+                    __builtin_bit_cast(uint32_t, d));
 }
 
-// 8 fp8 bytes (two dwords) -> 8 bf16 packed in a uint4.
-__device__ __forceinline__ uint4 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t src = i == 0 ? lo : hi;
-    w[2 * i] = e4m3_to_bf16_bits(src & 0xffu) | (e4m3_to_bf16_bits((src >> 8) & 0xffu) << 16);
-    w[2 * i + 1] = e4m3_to_bf16_bits((src >> 16) & 0xffu) | (e4m3_to_bf16_bits(src >> 24) << 16);
-  }
-  return make_uint4(w[0], w[1], w[2], w[3]);
+// v_max3_f32 without the operand canonicalisation the compiler adds around fmaxf (the MFMA results feeding it
+// are never signalling NaNs).
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
 }
 
 template <bool FP8>
@@ -90,24 +98,28 @@ struct Elem {
   using T = typename std::conditional<FP8, uint8_t, uint16_t>::type;
 };
 
-// Load 8 consecutive elements (bf16 or e4m3) as 8 bf16 in a uint4; `valid` elements only (rest zero).
+// 8 consecutive elements (bf16 or e4m3) as 8 bf16 in a uint4, with one vector load (16 / 8 bytes, aligned).
 template <bool FP8>
-__device__ __forceinline__ uint4 load8(const typename Elem<FP8>::T* p, int valid, bool aligned) {
-  if (valid >= 8 && aligned) {
-    if constexpr (FP8) {
-      const uint2 r = *reinterpret_cast<const uint2*>(p);
-      return fp8x8_to_bf16x8(r.x, r.y);
-    } else {
-      return *reinterpret_cast<const uint4*>(p);
-    }
+__device__ __forceinline__ uint4 load8_vec(const typename Elem<FP8>::T* p) {
+  if constexpr (FP8) {
+    const uint2 r = *reinterpret_cast<const uint2*>(p);
+    return fp8x8_to_bf16x8(r.x, r.y);
+  } else {
+    return *reinterpret_cast<const uint4*>(p);
   }
+}
+
+// The first `valid` (0..8) of 8 consecutive elements, any alignment; the rest are zero.
+template <bool FP8>
+__device__ __forceinline__ uint4 load8_scalar(const typename Elem<FP8>::T* p, int valid) {
   uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     if (e < valid) {
       uint32_t bits;
       if constexpr (FP8) {
-        bits = e4m3_to_bf16_bits(p[e]);
+        const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<uint32_t>(p[e]), 1.0f, false);
+        bits = __builtin_bit_cast(uint32_t, c) & 0xffffu;
       } else {
         bits = p[e];
       }
@@ -123,47 +135,36 @@ struct Stage {
   uint4 v[2];
 };
 
-// Global -> registers for key block starting at kv0 (2 chunks of 8 elements per thread for each of K and V).
-template <bool FP8, bool VT>
-__device__ __forceinline__ void stage_load(Stage<FP8, VT>& st, const XattnParams& p, int64_t kbase,
-                                           int64_t vbase, int64_t off, int L, int kv0) {
-  using T = typename Elem<FP8>::T;
-  const T* K = static_cast<const T*>(p.k);
-  const T* V = static_cast<const T*>(p.v);
-  const int dvalid_chunks = static_cast<int>(p.D / 8);
+// Global -> registers for the key block starting at kv0: each thread moves 2 chunks of 8 elements of K and of V.
+// TAIL: the block holds keys >= L (they are staged as zeros). vt_vec: V^T rows allow vector loads.
+template <bool FP8, bool VT, bool TAIL>
+__device__ __forceinline__ void stage_load(Stage<FP8, VT>& st, const XattnParams& p, const typename Elem<FP8>::T* K,
+                                           const typename Elem<FP8>::T* V, int L, int kv0, int dchunks,
+                                           bool vt_vec) {
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int c = threadIdx.x + kThreads * r;  // 0..511
     {
       const int key = c >> 3, dc = c & 7;
       const int kg = kv0 + key;
-      if (kg < L && dc < dvalid_chunks) {
-        const T* src = K + kbase + (off + kg) * p.sk_k + dc * 8;
-        st.k[r] = load8<FP8>(src, 8, true);
-      } else {
-        st.k[r] = make_uint4(0u, 0u, 0u, 0u);
-      }
+      const bool ok = dc < dchunks && (!TAIL || kg < L);
+      st.k[r] = ok ? load8_vec<FP8>(K + kg * p.sk_k + dc * 8) : make_uint4(0u, 0u, 0u, 0u);
     }
     if constexpr (VT) {
       const int d = c >> 3, kc = c & 7;
       const int kg = kv0 + kc * 8;
-      if (d < p.D && kg < L) {
-        const T* src = V + vbase + d * p.sv_d + (off + kg) * p.sv_k;
-        const int valid = (L - kg) < 8 ? (L - kg) : 8;
-        const bool aligned = ((reinterpret_cast<uintptr_t>(src) & (FP8 ? 7 : 15)) == 0);
-        st.v[r] = load8<FP8>(src, valid, aligned);
+      const auto* src = V + d * p.sv_d + kg;
+      if (d < p.D && (!TAIL || kg < L)) {
+        const int valid = TAIL ? ((L - kg) < 8 ? (L - kg) : 8) : 8;
+        st.v[r] = (vt_vec && valid == 8) ? load8_vec<FP8>(src) : load8_scalar<FP8>(src, valid);
       } else {
         st.v[r] = make_uint4(0u, 0u, 0u, 0u);
       }
     } else {
       const int key = c >> 3, dc = c & 7;
       const int kg = kv0 + key;
-      if (kg < L && dc < dvalid_chunks) {
-        const T* src = V + vbase + (off + kg) * p.sv_k + dc * 8;
-        st.v[r] = load8<FP8>(src, 8, true);
-      } else {
-        st.v[r] = make_uint4(0u, 0u, 0u, 0u);
-      }
+      const bool ok = dc < dchunks && (!TAIL || kg < L);
+      st.v[r] = ok ? load8_vec<FP8>(V + kg * p.sv_k + dc * 8) : make_uint4(0u, 0u, 0u, 0u);
     }
   }
 }
@@ -191,27 +192,63 @@ __device__ __forceinline__ void stage_store(const Stage<FP8, VT>& st, uint16_t* 
 }
 
 template <bool FP8, bool VT>
+__device__ __forceinline__ void stage_block(Stage<FP8, VT>& st, const XattnParams& p,
+                                            const typename Elem<FP8>::T* K, const typename Elem<FP8>::T* V, int L,
+                                            int kv0, int dchunks, bool vt_vec) {
+  if (kv0 + kKB <= L) {
+    stage_load<FP8, VT, false>(st, p, K, V, L, kv0, dchunks, vt_vec);
+  } else {
+    stage_load<FP8, VT, true>(st, p, K, V, L, kv0, dchunks, vt_vec);
+  }
+}
+
+__device__ __forceinline__ int window_length(const XattnParams& p, int64_t b) {
+  int64_t L;
+  if (p.cu_seqlens) {
+    L = static_cast<int64_t>(p.cu_seqlens[b + 1]) - p.cu_seqlens[b];
+  } else {
+    L = p.kv_len[b];
+    if (L > p.kv_cap) L = p.kv_cap;
+  }
+  return L < 0 ? 0 : static_cast<int>(L);
+}
+
+template <bool FP8, bool VT>
 __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKB * kRow];
   __shared__ __attribute__((aligned(16))) uint16_t sV[2][kDPad * kRow];
+  __shared__ int s_window;
 
-  // Workgroup -> (window, head, query tile). Consecutive workgroup ids are dispatched round robin over the 8
-  // XCDs, so XCD x (= id % 8) is given the (window, head) pairs bh = x, x + 8, ... with all query tiles of one
-  // pair back to back: the pair's K/V is read from HBM once into that XCD's L2, and windows of different
-  // lengths are mixed on every XCD.
+  // Workgroup -> (rank, head, query tile): XCD x (= id % 8) takes the (rank, head) units x, x + 8, ... with all
+  // query tiles of a unit back to back. rank 0 is the window with the most keys.
   const int64_t wg = blockIdx.x;
   int qt;
-  int64_t bh;
+  int64_t unit;
   if ((p.B * p.H) % 8 == 0) {
     const int64_t seq = wg >> 3;
     qt = static_cast<int>(seq % p.q_tiles);
-    bh = (wg & 7) + 8 * (seq / p.q_tiles);
+    unit = (wg & 7) + 8 * (seq / p.q_tiles);
   } else {
     qt = static_cast<int>(wg % p.q_tiles);
-    bh = wg / p.q_tiles;
+    unit = wg / p.q_tiles;
   }
-  const int64_t h = bh % p.H;
-  const int64_t b = bh / p.H;
+  const int64_t h = unit % p.H;
+  const int64_t rank = unit / p.H;
+  int64_t b = rank;
+  if (p.B > 1 && p.B <= kMaxRankWindows) {
+    // The window whose (length desc, index asc) rank is `rank`: every thread ranks its candidate windows.
+    for (int64_t c = threadIdx.x; c < p.B; c += kThreads) {
+      const int Lc = window_length(p, c);
+      int64_t r = 0;
+      for (int64_t o = 0; o < p.B; ++o) {
+        const int Lo = window_length(p, o);
+        r += (Lo > Lc || (Lo == Lc && o < c)) ? 1 : 0;
+      }
+      if (r == rank) s_window = static_cast<int>(c);
+    }
+    __syncthreads();
+    b = s_window;
+  }
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -220,16 +257,8 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   const int64_t q = static_cast<int64_t>(qt) * kQTile + w * 32 + col;
   const bool q_ok = q < p.Q;
 
-  int64_t off = 0;
-  int L;
-  if (p.cu_seqlens) {
-    off = p.cu_seqlens[b];
-    L = p.cu_seqlens[b + 1] - p.cu_seqlens[b];
-  } else {
-    L = p.kv_len[b];
-  }
-  if (L > p.kv_cap && !p.cu_seqlens) L = static_cast<int>(p.kv_cap);
-  if (L < 0) L = 0;
+  const int L = window_length(p, b);
+  const int64_t off = p.cu_seqlens ? p.cu_seqlens[b] : 0;
 
   const uint16_t* Qp = static_cast<const uint16_t*>(p.q) + b * p.sq_b + h * p.sq_h;
   uint16_t* Op = static_cast<uint16_t*>(p.o) + b * p.so_b + h * p.so_h;
@@ -258,72 +287,95 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
     qf[s] = __builtin_bit_cast(bf16x8_t, raw);
   }
 
-  const int64_t kbase = (p.cu_seqlens ? 0 : b * p.sk_b) + h * p.sk_h;
-  const int64_t vbase = (p.cu_seqlens ? 0 : b * p.sv_b) + h * p.sv_h;
+  using T = typename Elem<FP8>::T;
+  const T* K = static_cast<const T*>(p.k) + (p.cu_seqlens ? 0 : b * p.sk_b) + h * p.sk_h + off * p.sk_k;
+  const T* V = static_cast<const T*>(p.v) + (p.cu_seqlens ? 0 : b * p.sv_b) + h * p.sv_h + off * p.sv_k;
+  const int dchunks = static_cast<int>(p.D / 8);
+  // V^T rows allow vector loads when every 8-key run starts aligned (the base, the row stride and the offset).
+  const bool vt_vec = VT && ((reinterpret_cast<uintptr_t>(V) & (FP8 ? 7 : 15)) == 0) && (p.sv_d % 8 == 0);
   const int nblocks = (L + kKB - 1) / kKB;
 
   f32x16_t o0 = {0}, o1 = {0};  // O^T tiles: d in [0,32) and [32,64)
-  float m = -INFINITY;
-  float lsum = 0.f;
+  float m = -INFINITY;          // stored running max (log2 units), shared by O and l
+  float l0 = 0.f, l1 = 0.f;     // row-sum partials of this lane's keys
 
   Stage<FP8, VT> st;
-  stage_load<FP8, VT>(st, p, kbase, vbase, off, L, 0);
+  stage_block<FP8, VT>(st, p, K, V, L, 0, dchunks, vt_vec);
   stage_store<FP8, VT>(st, sK[0], sV[0]);
   __syncthreads();
+
+  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
   for (int blk = 0; blk < nblocks; ++blk) {
     const int cur = blk & 1;
     const bool more = blk + 1 < nblocks;
-    if (more) stage_load<FP8, VT>(st, p, kbase, vbase, off, L, (blk + 1) * kKB);
+    if (more) stage_block<FP8, VT>(st, p, K, V, L, (blk + 1) * kKB, dchunks, vt_vec);
 
-    const uint16_t* K = sK[cur];
+    const uint16_t* Ks = sK[cur];
     const uint16_t* Vt = sV[cur];
     // S^T for the two 32-key tiles.
     f32x16_t s0 = {0}, s1 = {0};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(K + col * kRow + 16 * s + 8 * hh);
-      const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(K + (32 + col) * kRow + 16 * s + 8 * hh);
+      const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(Ks + col * kRow + 16 * s + 8 * hh);
+      const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(Ks + (32 + col) * kRow + 16 * s + 8 * hh);
       s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[s], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[s], s1, 0, 0, 0);
     }
-    // Entry i of tile t is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8).
     const int kv0 = blk * kKB;
-    float x[32];
+    if (kv0 + kKB > L) {
+      // Entry i of tile t is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8).
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kin = (i < 8) ? (8 * hh + i) : (16 + 8 * hh + (i - 8));
-      x[i] = (kv0 + kin < L) ? s0[i] * sl2 : -INFINITY;
-      x[16 + i] = (kv0 + 32 + kin < L) ? s1[i] * sl2 : -INFINITY;
+      for (int i = 0; i < 16; ++i) {
+        const int kin = (i < 8) ? (8 * hh + i) : (16 + 8 * hh + (i - 8));
+        if (kv0 + kin >= L) s0[i] = -INFINITY;
+        if (kv0 + 32 + kin >= L) s1[i] = -INFINITY;
+      }
     }
-    float bmax = x[0];
+    // Block max of the raw scores (scale > 0, so it commutes with the scaling): 16 three-input maxes.
+    float ma = max3(s0[0], s0[1], s0[2]);
+    float mb = max3(s1[0], s1[1], s1[2]);
 #pragma unroll
-    for (int i = 1; i < 32; ++i) bmax = fmaxf(bmax, x[i]);
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float mn = fmaxf(m, bmax);
-    const float alpha = __builtin_amdgcn_exp2f(m - mn);  // m = -inf on the first block -> 0
-    m = mn;
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      x[i] = __builtin_amdgcn_exp2f(x[i] - mn);
-      psum += x[i];
+    for (int i = 3; i < 15; i += 2) {
+      ma = max3(ma, s0[i], s0[i + 1]);
+      mb = max3(mb, s1[i], s1[i + 1]);
     }
-    lsum = lsum * alpha + psum;
+    float mr = max3(ma, s0[15], mb);
+    mr = max3(mr, s1[15], s1[15]);
+    const float partner = __shfl_xor(mr, 32, 64);
+    mr = max3(mr, partner, partner);
+    const float cand = mr * sl2;
+    const bool raise = cand > m + kLazy;
+    if (__builtin_amdgcn_ballot_w64(raise) != 0ull) {
+      const float mn = raise ? cand : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 1 where m stays; 0 on the first block
+      m = mn;
+      l0 *= alpha;
+      l1 *= alpha;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      o0[i] *= alpha;
-      o1[i] *= alpha;
+      for (int i = 0; i < 16; ++i) {
+        o0[i] *= alpha;
+        o1[i] *= alpha;
+      }
     }
-    // P^T as B operands: k-step (tile t, half s) = entries 16 t + 8 s + 0..7.
+    const float neg_m = -m;
+    // P^T as B operands: k-step (tile t, half s) = entries 16 t + 8 s + 0..7; the row sum over the packed bf16.
     bf16x8_t pb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
+      const f32x16_t& src = (ks < 2) ? s0 : s1;
+      const int base = 8 * (ks & 1);
       bf16x8_t v;
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
-        f32x2_t two = {x[8 * ks + j], x[8 * ks + j + 1]};
+        f32x2_t two = {__builtin_amdgcn_exp2f(__builtin_fmaf(src[base + j], sl2, neg_m)),
+                       __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + j + 1], sl2, neg_m))};
         const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
+        if (j & 2) {
+          l1 = __builtin_amdgcn_fdot2_f32_bf16(c, ones, l1, false);
+        } else {
+          l0 = __builtin_amdgcn_fdot2_f32_bf16(c, ones, l0, false);
+        }
         v[j] = c[0];
         v[j + 1] = c[1];
       }
@@ -341,6 +393,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
     __syncthreads();
   }
 
+  float lsum = l0 + l1;
   lsum += __shfl_xor(lsum, 32, 64);
   const float inv = vscale / lsum;
   if (q_ok) {
@@ -384,6 +437,7 @@ extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void
   SVHIP_REQUIRE(B >= 0 && H >= 1 && Q >= 0, "%s: bad sizes", name);
   SVHIP_REQUIRE(D >= 8 && D <= kDPad && D % 8 == 0, "%s: head_dim %lld unsupported (multiple of 8, <= 64)", name,
                 (long long)D);
+  SVHIP_REQUIRE(scale > 0.f && scale < 3.0e38f, "%s: softmax scale must be positive and finite", name);
   SVHIP_REQUIRE(kv_dtype == SVHIP_BF16 || kv_dtype == SVHIP_FP8_E4M3, "%s: kv dtype %d unsupported", name, kv_dtype);
   const bool fp8 = kv_dtype == SVHIP_FP8_E4M3;
   SVHIP_REQUIRE(!fp8 || (k_scale && v_scale), "%s: fp8 K/V need k_scale and v_scale", name);
@@ -407,6 +461,7 @@ extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void
                   "%s: V rows must be %d-byte aligned", name, (int)align);
   }
   if (B == 0 || Q == 0) return SVHIP_OK;
+  SVHIP_REQUIRE(kv_cap >= 0 && kv_cap < (1ll << 31), "%s: kv_cap out of range", name);
   XattnParams p;
   p.q = q;
   p.k = k;

@@ -157,3 +157,28 @@ def test_fp8_e4m3_cached_kv(dev):
     assert torch.equal(out, out_t)
     # and against the unquantised inputs, the contract's looser bound
     check(out, A.cross_attention(q, k, v, lengths), FP8_ATOL)
+
+
+def test_fp8_decode_is_exact_for_every_code(dev):
+    """One key per window and K = 0: the output is the dequantised V row itself, so every finite e4m3 code must
+    come out as its exact value (all e4m3 values are bf16 values), pinned by the format table of the oracle."""
+    from streamvoxel_amd.stream.attention import attention
+    if not hasattr(torch, 'float8_e4m3fn'):
+        pytest.skip('torch without float8_e4m3fn')
+    codes = torch.tensor([c for c in range(256) if c not in (0x7f, 0xff)], dtype=torch.uint8)
+    B, H, Q, D, kcap = 4, 1, 8, 64, 64
+    _case('xattn fp8 decode table')
+    v = torch.zeros(B, H, kcap, D, dtype=torch.uint8)
+    # window b, key 0, head_dim d holds code index 64 b + d
+    flat = torch.zeros(B * D, dtype=torch.uint8)
+    flat[:codes.numel()] = codes
+    v[:, 0, 0, :] = flat.reshape(B, D)
+    k = torch.zeros(B, H, kcap, D, dtype=torch.uint8)
+    q = torch.zeros(B, H, Q, D, dtype=torch.bfloat16)
+    ones = torch.ones(B, H, dtype=torch.float32, device=dev)
+    out = attention(q.to(dev), k.to(dev), v.to(dev), lengths=torch.ones(B, dtype=torch.int32, device=dev),
+                    k_scale=ones, v_scale=ones)
+    torch.cuda.synchronize()
+    expect = A.dequant_e4m3(v[:, :, 0, :], 1.0)                      # [B, H, D] float64
+    got = out.cpu().double()[:, :, 0, :]
+    assert torch.equal(got, expect), (got - expect).abs().max()
