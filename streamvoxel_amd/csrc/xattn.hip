@@ -1,8 +1,8 @@
 // Cross attention over per-window variable-length cached K/V, bf16 MFMA (gfx950), fp32 accumulation.
 //
 // Work item: one workgroup = (window b, head h, 128-query tile), 4 waves x 32 queries. Keys are walked in
-// 64-key blocks staged through LDS (double-buffered; the next block's global loads are in flight while the
-// current block is computed).
+// 64-key blocks staged through LDS, double-buffered: the next block is in flight while the current one is
+// computed, one workgroup barrier per block.
 //
 // Per wave and key block (v_mfma_f32_32x32x16_bf16 throughout):
 //   S^T[key, q] = K . Q^T         A = K rows from LDS, B = the wave's Q (registers, loaded once)
@@ -22,10 +22,15 @@
 //     otherwise P may reach 2^kLazy, harmless in fp32 sums and bf16 P, and the O / l rescale is skipped for the
 //     whole wave. O and l always share the same m, so O / l is unchanged.
 //   * key masking runs only in the last, partial block; padding keys are staged as zeros.
+//   * the partner lane's block max comes over v_permlane32_swap, not an LDS round trip.
 //
-// K/V dtypes: bf16, or OCP e4m3fn bytes converted exactly to bf16 during staging (v_cvt_scalef32_pk_bf16_fp8
-// with scale 1); the fp8 scales are folded into the softmax scale (k_scale) and the output (v_scale). V may be
-// stored row-major ([key][d], transposed while staging) or transposed ([d][key], staged with vector copies).
+// Staging. LDS tiles hold 64 rows of 144 bytes (8 16-byte chunks + 16 bytes of padding, which keeps the 16-byte
+// operand reads conflict-free); a K row is one key's head_dim, a V^T row one head_dim element's 64 keys. bf16 K
+// and V^T of the padded [B,H,Kcap,*] layout with 16-byte aligned rows take global_load_lds_dwordx4, which moves
+// a full block straight into LDS without registers. Every other form goes through registers, prefetched one
+// block ahead: OCP e4m3fn K/V converted exactly to bf16 (v_cvt_scalef32_pk_bf16_fp8 with scale 1; the fp8 scales
+// are folded into the softmax scale (k_scale) and the output (v_scale)), row-major V transposed on the way, the
+// packed cu_seqlens layout, and the last partial block of a window.
 //
 // Workgroup order: windows are ranked by key count (longest first, ties by index) inside the kernel, so the
 // longest (window, head) pairs start first; consecutive workgroup ids go round robin to the 8 XCDs and all query
@@ -46,6 +51,7 @@ constexpr int kKB = 64;       // keys per block
 constexpr int kDPad = 64;     // head_dim handled by the MFMA tiles (smaller head_dim is zero-padded)
 constexpr int kRow = 72;      // LDS row stride in bf16 elements (144 bytes: conflict-free 16-byte reads)
 constexpr int kThreads = 256;
+constexpr int kSlots = kKB * kRow / 8;  // 16-byte slots of an LDS tile (64 rows x 9)
 constexpr float kLazy = 8.0f;  // log2-domain headroom before the running max is raised
 constexpr int kMaxRankWindows = 4096;
 
@@ -213,10 +219,38 @@ __device__ __forceinline__ int window_length(const XattnParams& p, int64_t b) {
   return L < 0 ? 0 : static_cast<int>(L);
 }
 
-template <bool FP8, bool VT>
+// Direct path (bf16 K and V^T, full block): global_load_lds_dwordx4 moves the block straight into LDS without
+// registers; each wave instruction fills 64 consecutive 16-byte slots of a tile (row R at slots 9 R .. 9 R + 8,
+// the ninth being padding), the 9 instructions of a tile spread over the 4 waves. Padding slots and chunks past
+// head_dim are not loaded (K's are zeroed once; V^T rows past head_dim only feed outputs that are never stored).
+__device__ __forceinline__ void stage_direct(const XattnParams& p, const uint16_t* K, const uint16_t* V, int kv0,
+                                             int dchunks, uint16_t* sK, uint16_t* sV) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = w; i < kSlots / 64; i += kThreads / 64) {
+    const int slot = 64 * i + lane;
+    const int row = slot / 9, c = slot - 9 * (slot / 9);
+    if (c < dchunks) {
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(K + (kv0 + sigma_row(row)) * p.sk_k + c * 8),
+                                       reinterpret_cast<void*>(sK + 64 * 8 * i), 16, 0, 0);
+    }
+    if (row < 8 * dchunks && c < 8) {
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(V + row * p.sv_d + kv0 + 8 * c),
+                                       reinterpret_cast<void*>(sV + 64 * 8 * i), 16, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// DIRECT: bf16 K and V^T of the padded layout with 16-byte aligned rows (chosen on the host); full blocks are
+// staged with direct loads.
+template <bool FP8, bool VT, bool DIRECT>
 __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKB * kRow];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kDPad * kRow];
+  // Four distinct LDS objects (not one indexed array): the compiler can then tell the direct loads into one
+  // buffer from the operand reads of the other and does not wait for the loads in flight before those reads.
+  __shared__ __attribute__((aligned(16))) uint16_t sK0[kKB * kRow], sK1[kKB * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t sV0[kDPad * kRow], sV1[kDPad * kRow];
   __shared__ int s_window;
 
   // Workgroup -> (rank, head, query tile): XCD x (= id % 8) takes the (rank, head) units x, x + 8, ... with all
@@ -295,24 +329,54 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   const bool vt_vec = VT && ((reinterpret_cast<uintptr_t>(V) & (FP8 ? 7 : 15)) == 0) && (p.sv_d % 8 == 0);
   const int nblocks = (L + kKB - 1) / kKB;
 
+  if (DIRECT && dchunks < 8) {
+    // Chunks past head_dim of both K tiles are never loaded by the direct path; they must hold zeros.
+    for (int i = threadIdx.x; i < kSlots; i += kThreads) {
+      const int c = i - 9 * (i / 9);
+      if (c >= dchunks && c < 8) {
+        *reinterpret_cast<uint4*>(sK0 + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(sK1 + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+
   f32x16_t o0 = {0}, o1 = {0};  // O^T tiles: d in [0,32) and [32,64)
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
   float l0 = 0.f, l1 = 0.f;     // row-sum partials of this lane's keys
 
+  // Stages block `blk` into (sK, sV): direct loads for a full block on the direct path (complete at the next
+  // vmem wait), registers otherwise (prefetched into `st` when `st_ready`, else loaded here).
   Stage<FP8, VT> st;
-  stage_block<FP8, VT>(st, p, K, V, L, 0, dchunks, vt_vec);
-  stage_store<FP8, VT>(st, sK[0], sV[0]);
+  auto stage_now = [&](int blk, uint16_t* sK, uint16_t* sV) {
+    const int kv0 = blk * kKB;
+    if (DIRECT && kv0 + kKB <= L) {
+      stage_direct(p, reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V), kv0, dchunks, sK,
+                   sV);
+    } else {
+      Stage<FP8, VT> tmp;
+      stage_block<FP8, VT>(tmp, p, K, V, L, kv0, dchunks, vt_vec);
+      stage_store<FP8, VT>(tmp, sK, sV);
+    }
+  };
+  stage_now(0, sK0, sV0);
+  wait_vmem();
   __syncthreads();
 
   const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
-  for (int blk = 0; blk < nblocks; ++blk) {
-    const int cur = blk & 1;
+  auto iteration = [&](int blk, const uint16_t* Ks, const uint16_t* Vt, uint16_t* nK, uint16_t* nV) {
     const bool more = blk + 1 < nblocks;
-    if (more) stage_block<FP8, VT>(st, p, K, V, L, (blk + 1) * kKB, dchunks, vt_vec);
+    const int kv_next = (blk + 1) * kKB;
+    // Next block: direct loads now (full blocks of the direct path), register prefetch now (register path), or
+    // a synchronous register staging after the compute (the last, partial block of the direct path).
+    const bool next_direct = DIRECT && more && kv_next + kKB <= L;
+    if (next_direct) {
+      stage_direct(p, reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V), kv_next, dchunks,
+                   nK, nV);
+    } else if (!DIRECT && more) {
+      stage_block<FP8, VT>(st, p, K, V, L, kv_next, dchunks, vt_vec);
+    }
 
-    const uint16_t* Ks = sK[cur];
-    const uint16_t* Vt = sV[cur];
     // S^T for the two 32-key tiles.
     f32x16_t s0 = {0}, s1 = {0};
 #pragma unroll
@@ -332,7 +396,8 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
         if (kv0 + 32 + kin >= L) s1[i] = -INFINITY;
       }
     }
-    // Block max of the raw scores (scale > 0, so it commutes with the scaling): 16 three-input maxes.
+    // Block max of the raw scores (scale > 0, so it commutes with the scaling): 16 three-input maxes, and the
+    // partner lane's over v_permlane32_swap, which gives (x[l % 32], x[l % 32 + 32]) in every lane.
     float ma = max3(s0[0], s0[1], s0[2]);
     float mb = max3(s1[0], s1[1], s1[2]);
 #pragma unroll
@@ -342,8 +407,8 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
     }
     float mr = max3(ma, s0[15], mb);
     mr = max3(mr, s1[15], s1[15]);
-    const float partner = __shfl_xor(mr, 32, 64);
-    mr = max3(mr, partner, partner);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mr), __float_as_int(mr), false, false);
+    mr = max3(__int_as_float(sw[0]), __int_as_float(sw[1]), __int_as_float(sw[1]));
     const float cand = mr * sl2;
     const bool raise = cand > m + kLazy;
     if (__builtin_amdgcn_ballot_w64(raise) != 0ull) {
@@ -389,12 +454,26 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
       o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pb[ks], o0, 0, 0, 0);
       o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pb[ks], o1, 0, 0, 0);
     }
-    if (more) stage_store<FP8, VT>(st, sK[cur ^ 1], sV[cur ^ 1]);
+    if (more && !next_direct) {
+      if constexpr (DIRECT) {
+        stage_now(blk + 1, nK, nV);
+      } else {
+        stage_store<FP8, VT>(st, nK, nV);
+      }
+    }
+    wait_vmem();
     __syncthreads();
+  };
+  for (int blk = 0; blk < nblocks; blk += 2) {
+    iteration(blk, sK0, sV0, sK1, sV1);
+    if (blk + 1 < nblocks) iteration(blk + 1, sK1, sV1, sK0, sV0);
   }
 
   float lsum = l0 + l1;
-  lsum += __shfl_xor(lsum, 32, 64);
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(lsum), __float_as_int(lsum), false, false);
+    lsum = __int_as_float(sw[0]) + __int_as_float(sw[1]);
+  }
   const float inv = vscale / lsum;
   if (q_ok) {
     // O^T entry i of tile t: d = 32 t + 8 (i / 4) + 4 hh + i % 4 ; four consecutive d per group.
@@ -493,19 +572,24 @@ extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void
   p.q_tiles = static_cast<int>(cdiv(Q, kQTile));
   const int64_t grid = static_cast<int64_t>(p.q_tiles) * H * B;
   SVHIP_REQUIRE(grid < (1ll << 31), "%s: grid too large", name);
+  // Direct-to-LDS staging: bf16 K and V^T of the padded layout whose rows (and every 8-key run of V^T) start on
+  // 16-byte boundaries.
+  const bool direct = !fp8 && vt && !cu_seqlens && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_d % 8 == 0 &&
+                      sv_h % 8 == 0 && sv_b % 8 == 0;
   hipStream_t s = as_stream(stream);
+  const unsigned g = static_cast<unsigned>(grid);
   if (fp8) {
     if (vt) {
-      xattn_fwd_kernel<true, true><<<static_cast<unsigned>(grid), kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<true, true, false><<<g, kThreads, 0, s>>>(p);
     } else {
-      xattn_fwd_kernel<true, false><<<static_cast<unsigned>(grid), kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<true, false, false><<<g, kThreads, 0, s>>>(p);
     }
+  } else if (direct) {
+    xattn_fwd_kernel<false, true, true><<<g, kThreads, 0, s>>>(p);
+  } else if (vt) {
+    xattn_fwd_kernel<false, true, false><<<g, kThreads, 0, s>>>(p);
   } else {
-    if (vt) {
-      xattn_fwd_kernel<false, true><<<static_cast<unsigned>(grid), kThreads, 0, s>>>(p);
-    } else {
-      xattn_fwd_kernel<false, false><<<static_cast<unsigned>(grid), kThreads, 0, s>>>(p);
-    }
+    xattn_fwd_kernel<false, false, false><<<g, kThreads, 0, s>>>(p);
   }
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;

@@ -182,3 +182,28 @@ def test_fp8_decode_is_exact_for_every_code(dev):
     expect = A.dequant_e4m3(v[:, :, 0, :], 1.0)                      # [B, H, D] float64
     got = out.cpu().double()[:, :, 0, :]
     assert torch.equal(got, expect), (got - expect).abs().max()
+
+
+@pytest.mark.parametrize('D', [64, 48])
+def test_transposed_v_padded_layout_fast_path(dev, D):
+    """V stored transposed in a padded [B,H,D,Kcap] buffer (the cached-context layout) takes the direct-to-LDS
+    staging: full blocks, a partial last block, a window shorter than one block; NaN in the padding must not
+    leak, and the result must equal the row-major-V path bit for bit."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, kcap = 4, 3, 160, 448
+    lengths = [448, 100, 64, 7]
+    _case(f'xattn direct V^T D={D} lengths={lengths}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=11 + D)
+    ref = A.cross_attention(q, k, v, lengths)
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    vt = v.transpose(2, 3).contiguous()
+    kg = k.clone()
+    for b, n in enumerate(lengths):
+        vt[b, :, :, n:] = float('nan')
+        kg[b, :, n:] = float('nan')
+    vt_dev = vt.to(dev)
+    out_direct = attention(q.to(dev), kg.to(dev), vt_dev.transpose(2, 3), lengths=lt)
+    out_rows = attention(q.to(dev), k.to(dev), v.to(dev), lengths=lt)
+    torch.cuda.synchronize()
+    check(out_direct, ref, BF16_ATOL, BF16_RTOL)
+    assert torch.equal(out_direct, out_rows)
