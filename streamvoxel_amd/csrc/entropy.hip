@@ -70,12 +70,16 @@ __global__ __launch_bounds__(256) void stats_voxel_major(const T* __restrict__ x
     const int64_t i = voxel - b * n;
     const T* row = x + b * sb + i * sn;
     float v[NV * E];
+    // All NV loads are issued before any is used: the index is clamped instead of branched on (a load inside a
+    // branch is waited for before the branch ends), and the lanes past the row are masked afterwards.
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int64_t c0 = static_cast<int64_t>(g + 16 * j) * E;
-      if (c0 < C) {
-        load16<T>(row + c0, v + j * E);
-      } else {
+      load16<T>(row + (c0 < C ? c0 : 0), v + j * E);
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      if (static_cast<int64_t>(g + 16 * j) * E >= C) {
 #pragma unroll
         for (int e = 0; e < E; ++e) v[j * E + e] = -INFINITY;
       }

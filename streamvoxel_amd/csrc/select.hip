@@ -41,11 +41,38 @@ __device__ __forceinline__ int64_t block_sum_i64(int64_t v, int64_t* scratch /* 
   return t;
 }
 
-template <typename K>
+// Radix histogram: kCopies copies per bin (bin d of copy c at hist[kCopies d + c], lane l adds into copy
+// l % kCopies). Scores cluster in a few bins, and with a single copy the lanes of a wave would serialise on the
+// same LDS counter; 64 copies make every lane's counter its own.
+// Block-wide minimum / maximum of one uint64 per thread (all threads of a kWG-thread block must call them).
+__device__ __forceinline__ uint64_t block_min_u64(uint64_t v, int64_t* scratch /* >= kWaves */) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = __shfl_xor(v, off, 64);
+    v = o < v ? o : v;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = static_cast<int64_t>(v);
+  __syncthreads();
+  uint64_t r = static_cast<uint64_t>(scratch[0]);
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) {
+    const uint64_t o = static_cast<uint64_t>(scratch[i]);
+    r = o < r ? o : r;
+  }
+  return r;
+}
+
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, int64_t* scratch /* >= kWaves */) {
+  return ~block_min_u64(~v, scratch);
+}
+
+template <typename K, int kCopies = 1>
 struct SelectShared {
-  uint32_t hist[256];
+  static constexpr int copies = kCopies;
+  uint32_t hist[256 * kCopies];
+  uint32_t bins[256];
   int64_t red[kWaves];
-  int64_t tie_counts[2][kWaves];
   K prefix;
   int64_t remaining;
 };
@@ -62,11 +89,51 @@ struct SelectPlan {
   int64_t eligible;
 };
 
-template <typename K, typename Get>
-__device__ SelectPlan<K> wg_select_plan(Get get, int64_t n, int64_t count, SelectShared<K>& sh) {
+constexpr int kUnroll = 8;  // keys each thread has in flight in the streaming passes
+// Boundary candidates kept per 4^3 block for the trim / top-up pass: the kBoundary last chosen and the kBoundary
+// first unchosen selectable voxels of the block, in (key, flat index) order.
+constexpr int kBoundary = 16;
+
+// Calls f(key) for the key of every element i in [0, n); each thread loads kUnroll keys (strided by kWG, so the
+// loads of a wave stay coalesced) before it uses any, so the passes are not bound by load latency.
+template <typename K, typename Get, typename F>
+__device__ __forceinline__ void for_each_key(Get get, int64_t n, F f) {
+  for (int64_t base = threadIdx.x; base < n; base += static_cast<int64_t>(kWG) * kUnroll) {
+    K keys[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + static_cast<int64_t>(u) * kWG;
+      keys[u] = i < n ? get(i) : KeyTraits<K>::kSentinel;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) f(keys[u]);
+  }
+}
+
+// Block-wide exclusive prefix sum of one int64 per thread (all threads of a kWG-thread block must call it).
+__device__ __forceinline__ int64_t block_exclusive_scan_i64(int64_t v, int64_t* scratch /* >= kWaves */) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int64_t incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t up = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += up;
+  }
+  __syncthreads();
+  if (lane == 63) scratch[w] = incl;
+  __syncthreads();
+  int64_t before = 0;
+#pragma unroll
+  for (int q = 0; q < kWaves; ++q) before += (q < w) ? scratch[q] : 0;
+  return before + incl - v;
+}
+
+template <typename K, typename Get, typename Shared>
+__device__ SelectPlan<K> wg_select_plan(Get get, int64_t n, int64_t count, Shared& sh) {
+  constexpr int kCopies = Shared::copies;
   constexpr K kSent = KeyTraits<K>::kSentinel;
   int64_t local = 0;
-  for (int64_t i = threadIdx.x; i < n; i += kWG) local += (get(i) != kSent) ? 1 : 0;
+  for_each_key<K>(get, n, [&](K key) { local += (key != kSent) ? 1 : 0; });
   const int64_t eligible = block_sum_i64(local, sh.red);
   SelectPlan<K> plan{0, K(0), 0, eligible};
   if (count <= 0 || eligible == 0) return plan;
@@ -77,16 +144,26 @@ __device__ SelectPlan<K> wg_select_plan(Get get, int64_t n, int64_t count, Selec
   K prefix = 0, hi_mask = 0;
   int64_t remaining = count;
   for (int shift = KeyTraits<K>::kBits - 8; shift >= 0; shift -= 8) {
-    for (int t = threadIdx.x; t < 256; t += kWG) sh.hist[t] = 0u;
+    for (int t = threadIdx.x; t < 256 * kCopies; t += kWG) sh.hist[t] = 0u;
     __syncthreads();
-    for (int64_t i = threadIdx.x; i < n; i += kWG) {
-      const K key = get(i);
-      if (key != kSent && (key & hi_mask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 0xff], 1u);
+    const int copy = threadIdx.x % kCopies;
+    for_each_key<K>(get, n, [&](K key) {
+      if (key != kSent && (key & hi_mask) == prefix) {
+        atomicAdd(&sh.hist[kCopies * static_cast<int>((key >> shift) & 0xff) + copy], 1u);
+      }
+    });
+    __syncthreads();
+    // Fold the copies into bins[].
+    for (int d = threadIdx.x; d < 256; d += kWG) {
+      uint32_t sum = 0;
+#pragma unroll 16
+      for (int c = 0; c < kCopies; ++c) sum += sh.hist[kCopies * d + ((c + d) % kCopies)];
+      sh.bins[d] = sum;
     }
     __syncthreads();
     if (threadIdx.x < 64) {
       const int l = threadIdx.x;
-      const uint32_t h0 = sh.hist[4 * l], h1 = sh.hist[4 * l + 1], h2 = sh.hist[4 * l + 2], h3 = sh.hist[4 * l + 3];
+      const uint32_t h0 = sh.bins[4 * l], h1 = sh.bins[4 * l + 1], h2 = sh.bins[4 * l + 2], h3 = sh.bins[4 * l + 3];
       const int64_t mine = static_cast<int64_t>(h0) + h1 + h2 + h3;
       int64_t incl = mine;
 #pragma unroll
@@ -117,45 +194,49 @@ __device__ SelectPlan<K> wg_select_plan(Get get, int64_t n, int64_t count, Selec
   return plan;
 }
 
-// Applies a plan: apply(i, selected) is called once for every i in [0, n) (every thread walks index-ordered
-// rounds of kWG elements so that ties are taken in index order).
-template <typename K, typename Get, typename Apply>
-__device__ void wg_select_apply(const SelectPlan<K>& plan, Get get, int64_t n, SelectShared<K>& sh, Apply apply) {
+// Applies a plan: apply(i, selected) is called once for every i in [0, n). Thread t owns the contiguous run
+// [t C, t C + C) of the elements (C = ceil(n / kWG)); ties are taken in index order through an exclusive scan of
+// the per-thread tie counts. apply(i, .) may write element i: no other thread reads it.
+template <typename K, typename Get, typename Shared, typename Apply>
+__device__ void wg_select_apply(const SelectPlan<K>& plan, Get get, int64_t n, Shared& sh, Apply apply) {
   constexpr K kSent = KeyTraits<K>::kSentinel;
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  int64_t running = 0;
-  int parity = 0;
-  for (int64_t base = 0; base < n; base += kWG) {
-    const int64_t i = base + threadIdx.x;
-    const bool inside = i < n;
-    const K key = inside ? get(i) : kSent;
-    bool sel = false;
-    bool tie = false;
-    if (plan.mode == 1) {
-      sel = key != kSent;
-    } else if (plan.mode == 2) {
-      sel = key < plan.threshold;
-      tie = key == plan.threshold;
-    }
-    if (plan.mode == 2) {
-      const uint64_t ballot = __ballot(tie);
-      if (lane == 0) sh.tie_counts[parity][w] = __popcll(ballot);
-      __syncthreads();
-      int64_t before = running;
-      int64_t round_total = 0;
+  const int64_t C = (n + kWG - 1) / kWG;
+  const int64_t lo = threadIdx.x * C < n ? threadIdx.x * C : n;
+  const int64_t hi = lo + C < n ? lo + C : n;
+  int64_t ties_before = 0;
+  if (plan.mode == 2) {
+    int64_t mine = 0;
+    for (int64_t base = lo; base < hi; base += kUnroll) {
+      K keys[kUnroll];
 #pragma unroll
-      for (int q = 0; q < kWaves; ++q) {
-        const int64_t c = sh.tie_counts[parity][q];
-        if (q < w) before += c;
-        round_total += c;
-      }
-      before += __popcll(ballot & ((1ull << lane) - 1ull));
-      if (tie && before < plan.take_ties) sel = true;
-      running += round_total;
-      parity ^= 1;
+      for (int u = 0; u < kUnroll; ++u) keys[u] = base + u < hi ? get(base + u) : kSent;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) mine += (keys[u] == plan.threshold) ? 1 : 0;
     }
-    if (inside) apply(i, sel);
+    ties_before = block_exclusive_scan_i64(mine, sh.red);
+  }
+  for (int64_t base = lo; base < hi; base += kUnroll) {
+    K keys[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) keys[u] = base + u < hi ? get(base + u) : kSent;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (base + u < hi) {
+        const K key = keys[u];
+        bool sel = false;
+        if (plan.mode == 1) {
+          sel = key != kSent;
+        } else if (plan.mode == 2) {
+          if (key < plan.threshold) {
+            sel = true;
+          } else if (key == plan.threshold) {
+            sel = ties_before < plan.take_ties;
+            ++ties_before;
+          }
+        }
+        apply(base + u, sel);
+      }
+    }
   }
 }
 
@@ -175,12 +256,26 @@ struct MaskTokens {
   int64_t mask_token;
   int64_t n;
   __device__ __forceinline__ bool operator()(int64_t b, int64_t flat) const {
-    return tokens[b * n + flat] == mask_token && last[b * n + flat] == 0;
+    const int64_t t = tokens[b * n + flat];
+    const uint8_t l = last[b * n + flat];
+    return (t == mask_token) & (l == 0);
   }
 };
 
 struct Geometry {
   int64_t Y, Z, X, b, nb, n, nz, nx;  // nz = Z / b, nx = X / b
+  // Flat index of in-block entry i of block j for a compile-time block edge BB (32-bit arithmetic: every
+  // index of a selection call fits, which the host checks).
+  template <int BB>
+  __device__ __forceinline__ int flat32(int j, int i) const {
+    const int nzx = static_cast<int>(nz * nx), nx32 = static_cast<int>(nx);
+    const int by = j / nzx;
+    const int rem = j - by * nzx;
+    const int bz = rem / nx32;
+    const int bx = rem - bz * nx32;
+    const int dy = i / (BB * BB), dz = (i / BB) % BB, dx = i % BB;
+    return ((by * BB + dy) * static_cast<int>(Z) + bz * BB + dz) * static_cast<int>(X) + bx * BB + dx;
+  }
   __host__ __device__ int64_t flat_of(int64_t j, int64_t i) const {
     const int64_t by = j / (nz * nx);
     const int64_t bz = (j / nx) % nz;
@@ -195,14 +290,12 @@ struct Geometry {
 // ---------------------------------------------------------------------------------------------- apportionment
 
 // One workgroup per window: target[j] = base[j] + (j among the `extra` smallest apportionment keys).
-// Also clears the window's `got` counter for the in-block pass that follows on the same stream.
 __global__ __launch_bounds__(kWG) void apportion_kernel(const int64_t* __restrict__ n_total,
                                                         const int64_t* __restrict__ pos,
                                                         const double* __restrict__ frac,
                                                         const int64_t* __restrict__ k,
                                                         const int64_t* __restrict__ committed, int64_t nb,
-                                                        uint64_t* __restrict__ keys, int64_t* __restrict__ target,
-                                                        int64_t* __restrict__ got) {
+                                                        uint64_t* __restrict__ keys, int64_t* __restrict__ target) {
 #pragma clang fp contract(off)
   __shared__ SelectShared<uint64_t> sh;
   const int64_t b = blockIdx.x;
@@ -226,7 +319,6 @@ __global__ __launch_bounds__(kWG) void apportion_kernel(const int64_t* __restric
   const int64_t base_sum = block_sum_i64(local, sh.red);
   int64_t extra = committed[b] + k[b] - base_sum;
   if (extra < 0) extra = 0;
-  if (threadIdx.x == 0) got[b] = 0;
   if (extra == 0) return;
   __syncthreads();  // keys written by other threads
   auto get = [&](int64_t j) -> uint64_t { return ky[j]; };
@@ -236,25 +328,155 @@ __global__ __launch_bounds__(kWG) void apportion_kernel(const int64_t* __restric
   });
 }
 
+// The same for windows of at most 64 kPerLane blocks, one wave per window (4 windows per workgroup) with the
+// keys in registers and no workgroup barriers: an MSB-first 8-bit radix select over the 64-bit keys with the
+// histogram in the wave's own LDS, then the `extra` smallest (key, block index) get one more voxel.
+constexpr int kPerLane = 16;
+
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(256) void apportion_wave_kernel(const int64_t* __restrict__ n_total,
+                                                             const int64_t* __restrict__ pos,
+                                                             const double* __restrict__ frac,
+                                                             const int64_t* __restrict__ k,
+                                                             const int64_t* __restrict__ committed, int64_t batch,
+                                                             int64_t nb, int64_t* __restrict__ target) {
+#pragma clang fp contract(off)
+  __shared__ uint32_t hist_all[4][256];
+  const int lane = threadIdx.x & 63;
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (b >= batch) return;
+  uint32_t* hist = hist_all[threadIdx.x >> 6];
+  const double f = frac[b];
+  const int64_t* nt = n_total + b * nb;
+  const int64_t* ps = pos + b * nb;
+  int64_t* tg = target + b * nb;
+  // Block j = lane + 64 t is held by this lane in slot t; absent blocks get the sentinel key.
+  // Loads are unconditional (clamped index) so that all of them are in flight at once; a conditional load would
+  // be waited for inside its branch.
+  int64_t ntv[kPerLane], psv[kPerLane];
+#pragma unroll
+  for (int t = 0; t < kPerLane; ++t) {
+    const int64_t j = lane + 64 * t < nb ? lane + 64 * t : nb - 1;
+    ntv[t] = nt[j];
+    psv[t] = ps[j];
+  }
+  uint64_t key[kPerLane];
+  int64_t base[kPerLane];
+  int64_t local = 0;
+#pragma unroll
+  for (int t = 0; t < kPerLane; ++t) {
+    const double ideal = f * static_cast<double>(ntv[t]);
+    const double shifted = ideal + 1e-9;
+    const double bse = floor(shifted);
+    const double neg_frac = -(ideal - bse);
+    const double scaled = neg_frac * 1e6;
+    const double kd = scaled + static_cast<double>(psv[t]);
+    const bool in = lane + 64 * t < nb;
+    key[t] = in ? ordered_u64(kd) : ~0ull;
+    base[t] = in ? static_cast<int64_t>(bse) : 0;
+    local += base[t];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) local += __shfl_xor(local, off, 64);
+  const int64_t extra = committed[b] + k[b] - local;
+  int64_t add[kPerLane];
+#pragma unroll
+  for (int t = 0; t < kPerLane; ++t) add[t] = 0;
+  if (extra >= nb) {
+#pragma unroll
+    for (int t = 0; t < kPerLane; ++t) add[t] = 1;
+  } else if (extra > 0) {
+    // Threshold key T and how many T-ties to take (remaining) after the last digit.
+    uint64_t prefix = 0, hi_mask = 0;
+    int64_t remaining = extra;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) hist[4 * lane + q] = 0u;
+      wave_sync_lds();
+#pragma unroll
+      for (int t = 0; t < kPerLane; ++t) {
+        if (key[t] != ~0ull && (key[t] & hi_mask) == prefix) atomicAdd(&hist[(key[t] >> shift) & 0xff], 1u);
+      }
+      wave_sync_lds();
+      const uint32_t hs[4] = {hist[4 * lane], hist[4 * lane + 1], hist[4 * lane + 2], hist[4 * lane + 3]};
+      const int64_t mine = static_cast<int64_t>(hs[0]) + hs[1] + hs[2] + hs[3];
+      int64_t incl = mine;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int64_t up = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += up;
+      }
+      // The lane whose four bins hold the remaining-th key finds the bin; everyone reads it from that lane.
+      const uint64_t who = __ballot(incl - mine < remaining && remaining <= incl);
+      const int src = __builtin_ctzll(who);
+      int64_t before = incl - mine;
+      int bin = 4 * lane + 3;
+      bool found = false;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (!found) {
+          if (before + hs[q] < remaining) {
+            before += hs[q];
+          } else {
+            bin = 4 * lane + q;
+            found = true;
+          }
+        }
+      }
+      prefix |= static_cast<uint64_t>(__shfl(bin, src, 64)) << shift;
+      remaining -= __shfl(before, src, 64);
+      hi_mask |= static_cast<uint64_t>(0xff) << shift;
+      wave_sync_lds();
+    }
+    // key < T: one more; key == T: the first `remaining` in block order (slot t, then lane).
+    int64_t ties_before = 0;
+#pragma unroll
+    for (int t = 0; t < kPerLane; ++t) {
+      const bool tie = key[t] == prefix && key[t] != ~0ull;
+      const uint64_t tb = __ballot(tie);
+      const int64_t rank = ties_before + __popcll(tb & ((1ull << lane) - 1ull));
+      add[t] = (key[t] < prefix || (tie && rank < remaining)) ? 1 : 0;
+      ties_before += __popcll(tb);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kPerLane; ++t) {
+    const int64_t j = lane + 64 * t;
+    if (j < nb) tg[j] = base[t] + add[t];
+  }
+}
+
 // ------------------------------------------------------------------------------------------ in-block selection
 
+// Every in-block kernel also leaves, for the trim / top-up pass: bq[B, nb] the quota each block took, and
+// ckey[B, N] (flat order) the descending-score key of every selectable voxel (the sentinel elsewhere).
+
 // Blocks of at most 64 voxels (b in {1, 2, 4}): one wave holds 64 / b^3 whole blocks, lane = in-block index.
-template <int B3, typename Mask>
+template <int BB, typename Mask>
 __global__ __launch_bounds__(256) void inblock_wave_kernel(const float* __restrict__ score, Mask mask, Geometry g,
-                                                           int64_t batch, const int64_t* __restrict__ n_total,
+                                                           int total, const int64_t* __restrict__ n_total,
                                                            const int64_t* __restrict__ target,
-                                                           uint8_t* __restrict__ chosen, int64_t* __restrict__ got) {
+                                                           uint8_t* __restrict__ chosen, int32_t* __restrict__ bq,
+                                                           uint32_t* __restrict__ ckey, uint64_t* __restrict__ bnd) {
+  constexpr int B3 = BB * BB * BB;
   const int lane = threadIdx.x & 63;
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // block-major element
-  const int64_t total = batch * g.n;
+  const int e = static_cast<int>(blockIdx.x) * blockDim.x + threadIdx.x;  // block-major element
   if (e - lane >= total) return;  // whole wave past the end (total is a multiple of 64)
-  const int64_t jg = e / B3;
-  const int i = static_cast<int>(e % B3);
-  const int64_t b = jg / g.nb;
-  const int64_t j = jg - b * g.nb;
-  const int64_t flat = g.flat_of(j, i);
+  const int n = static_cast<int>(g.n), nb = static_cast<int>(g.nb);
+  const int jg = e / B3;
+  const int i = e % B3;
+  const int b = jg / nb;
+  const int j = jg - b * nb;
+  const int flat = g.flat32<BB>(j, i);
+  const float sv = score[b * n + flat];
   const bool masked = mask(b, flat);
-  const uint32_t key = masked ? desc_key(score[b * g.n + flat]) : KeyTraits<uint32_t>::kSentinel;
+  const uint32_t key = masked ? desc_key(sv) : KeyTraits<uint32_t>::kSentinel;
+  ckey[b * n + flat] = key;
   const int group0 = lane & ~(B3 - 1);
   const uint64_t ballot = __ballot(masked);
   const uint64_t gmask = (B3 == 64) ? ~0ull : (((1ull << B3) - 1ull) << group0);
@@ -270,12 +492,23 @@ __global__ __launch_bounds__(256) void inblock_wave_kernel(const float* __restri
     rank += (other < key || (other == key && t < i)) ? 1 : 0;
   }
   const bool sel = masked && rank < quota;
-  chosen[b * g.n + flat] = sel ? 1 : 0;
-  // Sum of quotas of this wave's blocks (all in one window since n is a multiple of 64).
-  int64_t q = (i == 0) ? quota : 0;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) q += __shfl_xor(q, off, 64);
-  if (lane == 0) atomicAdd(reinterpret_cast<unsigned long long*>(got + b), static_cast<unsigned long long>(q));
+  chosen[b * n + flat] = sel ? 1 : 0;
+  if (i == 0) bq[jg] = static_cast<int32_t>(quota);
+  if constexpr (B3 == 64) {
+    // Boundary candidates: slot t holds the voxel of in-block rank quota - kBoundary + t as (key << 32 | flat),
+    // the sentinel when that rank does not exist. The wave sorts itself into LDS by rank (ranks of the selectable
+    // voxels are 0 .. legal-1, each held by one lane), then lanes 0 .. 2 kBoundary - 1 gather.
+    __shared__ uint64_t by_rank[256];
+    uint64_t* mine = by_rank + (threadIdx.x & ~63);
+    if (masked) mine[rank] = (static_cast<uint64_t>(key) << 32) | static_cast<uint32_t>(flat);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < 2 * kBoundary) {
+      const int64_t r = quota - kBoundary + lane;
+      bnd[static_cast<int64_t>(jg) * 2 * kBoundary + lane] = (r >= 0 && r < legal) ? mine[r] : ~0ull;
+    }
+  }
 }
 
 // Blocks of more than 64 voxels (b >= 8): one workgroup per block.
@@ -283,7 +516,8 @@ template <typename Mask>
 __global__ __launch_bounds__(kWG) void inblock_wg_kernel(const float* __restrict__ score, Mask mask, Geometry g,
                                                          const int64_t* __restrict__ n_total,
                                                          const int64_t* __restrict__ target,
-                                                         uint8_t* __restrict__ chosen, int64_t* __restrict__ got) {
+                                                         uint8_t* __restrict__ chosen, int32_t* __restrict__ bq,
+                                                         uint32_t* __restrict__ ckey) {
   __shared__ SelectShared<uint32_t> sh;
   const int64_t jg = blockIdx.x;
   const int64_t b = jg / g.nb;
@@ -294,9 +528,14 @@ __global__ __launch_bounds__(kWG) void inblock_wg_kernel(const float* __restrict
     const int64_t flat = g.flat_of(j, i);
     return mask(b, flat) ? desc_key(sc[flat]) : KeyTraits<uint32_t>::kSentinel;
   };
-  // legal = number of masked voxels (the plan counts eligible keys)
+  // legal = number of masked voxels; the keys are also left for the trim / top-up pass
   int64_t local = 0;
-  for (int64_t i = threadIdx.x; i < b3; i += kWG) local += mask(b, g.flat_of(j, i)) ? 1 : 0;
+  for (int64_t i = threadIdx.x; i < b3; i += kWG) {
+    const int64_t flat = g.flat_of(j, i);
+    const uint32_t key = get(i);
+    ckey[b * g.n + flat] = key;
+    local += key != KeyTraits<uint32_t>::kSentinel ? 1 : 0;
+  }
   const int64_t legal = block_sum_i64(local, sh.red);
   int64_t quota = target[jg] - (n_total[jg] - legal);
   if (quota < 0) quota = 0;
@@ -305,29 +544,66 @@ __global__ __launch_bounds__(kWG) void inblock_wg_kernel(const float* __restrict
   wg_select_apply<uint32_t>(plan, get, b3, sh, [&](int64_t i, bool sel) {
     chosen[b * g.n + g.flat_of(j, i)] = sel ? 1 : 0;
   });
-  if (threadIdx.x == 0) atomicAdd(reinterpret_cast<unsigned long long*>(got + b), static_cast<unsigned long long>(quota));
+  if (threadIdx.x == 0) bq[jg] = static_cast<int32_t>(quota);
 }
 
 // ------------------------------------------------------------------------------------------ trim / top-up / bad
 
 // One workgroup per window: if the clamped quotas gave got != k, keep the top k of `chosen` (trim) or add the top
-// (k - got) of mask & ~chosen (top-up), by score; then bad = (final count != k).
-template <typename Mask>
-__global__ __launch_bounds__(kWG) void fix_kernel(const float* __restrict__ score, Mask mask, int64_t n,
-                                                  const int64_t* __restrict__ k, const int64_t* __restrict__ got,
-                                                  uint8_t* __restrict__ chosen, uint8_t* __restrict__ bad) {
-  __shared__ SelectShared<uint32_t> sh;
+// (k - got) of selectable & ~chosen (top-up), by score; then bad = (final count != k). Reads only the keys and the
+// per-block quotas the in-block pass left (a selectable voxel has a non-sentinel key).
+__global__ __launch_bounds__(kWG) void fix_kernel(int64_t n, int64_t nb, const int64_t* __restrict__ k,
+                                                  const int32_t* __restrict__ bq, const uint32_t* __restrict__ ckey,
+                                                  const uint64_t* __restrict__ bnd, uint8_t* __restrict__ chosen,
+                                                  uint8_t* __restrict__ bad) {
+  constexpr uint32_t kSent = KeyTraits<uint32_t>::kSentinel;
+  __shared__ SelectShared<uint32_t, 64> sh;
   const int64_t b = blockIdx.x;
   const int64_t kk = k[b];
-  const int64_t have = got[b];
-  const float* sc = score + b * n;
+  int64_t local = 0;
+  for (int64_t j = threadIdx.x; j < nb; j += kWG) local += bq[b * nb + j];
+  const int64_t have = block_sum_i64(local, sh.red);
+  const uint32_t* ky = ckey + b * n;
   uint8_t* ch = chosen + b * n;
   if (have == kk) {
     if (threadIdx.x == 0) bad[b] = 0;
     return;
   }
+  const int64_t d = have > kk ? have - kk : kk - have;
+  if (bnd != nullptr && d <= kBoundary) {
+    // The d voxels to drop (trim: the last d chosen in (key, index) order) or to add (top-up: the first d
+    // unchosen selectable ones) are among the boundary candidates: such a voxel has fewer than d voxels of its own
+    // block on the far side of it. d rounds of a block-wide extremum over the candidates.
+    const bool trim = have > kk;
+    const uint64_t* cb = bnd + b * nb * 2 * kBoundary;
+    int64_t done = 0;
+    for (int64_t round = 0; round < d; ++round) {
+      // trim: largest candidate (the sentinel is excluded); top-up: smallest.
+      uint64_t best = trim ? 0ull : ~0ull;
+      for (int64_t j = threadIdx.x; j < nb; j += kWG) {
+        for (int64_t t = 0; t < d; ++t) {
+          const uint64_t c = cb[j * 2 * kBoundary + (trim ? kBoundary - 1 - t : kBoundary + t)];
+          if (c == ~0ull) continue;
+          const uint8_t taken = ch[static_cast<uint32_t>(c)];
+          if (trim ? (taken && c > best) : (!taken && c < best)) best = c;
+        }
+      }
+      best = trim ? block_max_u64(best, sh.red) : block_min_u64(best, sh.red);
+      if (trim ? best == 0ull : best == ~0ull) break;  // no candidate left
+      if (threadIdx.x == 0) ch[static_cast<uint32_t>(best)] = trim ? 0 : 1;
+      ++done;
+      __syncthreads();  // the flip is visible to the next round's reads
+    }
+    if (threadIdx.x == 0) bad[b] = (done != d) ? 1 : 0;
+    return;
+  }
+  __syncthreads();
   if (have > kk) {
-    auto get = [&](int64_t i) -> uint32_t { return ch[i] ? desc_key(sc[i]) : KeyTraits<uint32_t>::kSentinel; };
+    auto get = [&](int64_t i) -> uint32_t {
+      const uint8_t c = ch[i];
+      const uint32_t v = ky[i];
+      return c ? v : kSent;
+    };
     const SelectPlan<uint32_t> plan = wg_select_plan<uint32_t>(get, n, kk, sh);
     __syncthreads();
     wg_select_apply<uint32_t>(plan, get, n, sh, [&](int64_t i, bool sel) {
@@ -337,7 +613,9 @@ __global__ __launch_bounds__(kWG) void fix_kernel(const float* __restrict__ scor
     if (threadIdx.x == 0) bad[b] = (final_count != kk) ? 1 : 0;
   } else {
     auto get = [&](int64_t i) -> uint32_t {
-      return (!ch[i] && mask(b, i)) ? desc_key(sc[i]) : KeyTraits<uint32_t>::kSentinel;
+      const uint8_t c = ch[i];
+      const uint32_t v = ky[i];
+      return c ? kSent : v;
     };
     const int64_t need = kk - have;
     const SelectPlan<uint32_t> plan = wg_select_plan<uint32_t>(get, n, need, sh);
@@ -357,7 +635,7 @@ __global__ __launch_bounds__(kWG) void top_mask_kernel(const float* __restrict__
                                                        const uint8_t* __restrict__ eligible, int64_t n,
                                                        const int64_t* __restrict__ count_dev, int64_t count_host,
                                                        uint8_t* __restrict__ out) {
-  __shared__ SelectShared<uint32_t> sh;
+  __shared__ SelectShared<uint32_t, 64> sh;
   const int64_t b = blockIdx.x;
   const float* sc = scores + b * n;
   const uint8_t* el = eligible + b * n;
@@ -439,6 +717,8 @@ static int check_geometry(int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_
   const int64_t n = Y * Z * X;
   SVHIP_REQUIRE(n % 64 == 0, "%s: window voxel count %lld must be a multiple of 64", name, (long long)n);
   SVHIP_REQUIRE(block * block * block <= (1 << 24), "%s: block too large", name);
+  SVHIP_REQUIRE(batch * n < (int64_t(1) << 31), "%s: %lld windows x %lld voxels exceed 2^31 elements", name,
+                (long long)batch, (long long)n);
   g->Y = Y;
   g->Z = Z;
   g->X = X;
@@ -450,16 +730,25 @@ static int check_geometry(int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_
   return SVHIP_OK;
 }
 
+// Boundary candidates are kept for 4^3 blocks only (the block size the window schedule uses).
+static int64_t boundary_entries(int64_t batch, const Geometry& g) {
+  return g.b == 4 ? batch * g.nb * 2 * kBoundary : 0;
+}
+
 static size_t quota_ws_bytes(int64_t batch, const Geometry& g) {
-  // keys u64 [B,nb] + target i64 [B,nb] + got i64 [B], each 256-byte aligned
+  // keys u64 [B,nb] + target i64 [B,nb] + bq i32 [B,nb] + ckey u32 [B,N] + bnd u64 [B,nb,2 kBoundary] (4^3
+  // blocks), each 256-byte aligned
   auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
-  return al(sizeof(uint64_t) * batch * g.nb) + al(sizeof(int64_t) * batch * g.nb) + al(sizeof(int64_t) * batch);
+  return al(sizeof(uint64_t) * batch * g.nb) + al(sizeof(int64_t) * batch * g.nb) + al(sizeof(int32_t) * batch * g.nb) +
+         al(sizeof(uint32_t) * batch * g.n) + al(sizeof(uint64_t) * boundary_entries(batch, g));
 }
 
 struct QuotaWs {
   uint64_t* keys;
   int64_t* target;
-  int64_t* got;
+  int32_t* bq;
+  uint32_t* ckey;
+  uint64_t* bnd;  // null unless the blocks are 4^3
 };
 
 static QuotaWs carve(void* ws, int64_t batch, const Geometry& g) {
@@ -470,7 +759,11 @@ static QuotaWs carve(void* ws, int64_t batch, const Geometry& g) {
   p += al(sizeof(uint64_t) * batch * g.nb);
   w.target = reinterpret_cast<int64_t*>(p);
   p += al(sizeof(int64_t) * batch * g.nb);
-  w.got = reinterpret_cast<int64_t*>(p);
+  w.bq = reinterpret_cast<int32_t*>(p);
+  p += al(sizeof(int32_t) * batch * g.nb);
+  w.ckey = reinterpret_cast<uint32_t*>(p);
+  p += al(sizeof(uint32_t) * batch * g.n);
+  w.bnd = boundary_entries(batch, g) ? reinterpret_cast<uint64_t*>(p) : nullptr;
   return w;
 }
 
@@ -478,30 +771,38 @@ template <typename Mask>
 static int launch_quota(const float* score, Mask mask, int64_t batch, const Geometry& g, const int64_t* k,
                         const int64_t* pos, const double* frac, const int64_t* n_total, const int64_t* committed,
                         uint8_t* chosen, uint8_t* bad, const QuotaWs& w, hipStream_t s, const char* name) {
-  apportion_kernel<<<static_cast<unsigned>(batch), kWG, 0, s>>>(n_total, pos, frac, k, committed, g.nb, w.keys,
-                                                                 w.target, w.got);
+  if (g.nb <= 64 * kPerLane) {
+    apportion_wave_kernel<<<static_cast<unsigned>(cdiv(batch, 4)), 256, 0, s>>>(n_total, pos, frac, k, committed,
+                                                                                batch, g.nb, w.target);
+  } else {
+    apportion_kernel<<<static_cast<unsigned>(batch), kWG, 0, s>>>(n_total, pos, frac, k, committed, g.nb, w.keys,
+                                                                   w.target);
+  }
   SVHIP_LAUNCHED(name);
   const int64_t b3 = g.b * g.b * g.b;
   if (b3 <= 64) {
-    const int64_t threads = batch * g.n;
-    const unsigned grid = static_cast<unsigned>(cdiv(threads, 256));
+    const int total = static_cast<int>(batch * g.n);
+    const unsigned grid = static_cast<unsigned>(cdiv(total, 256));
     switch (b3) {
       case 1:
-        inblock_wave_kernel<1, Mask><<<grid, 256, 0, s>>>(score, mask, g, batch, n_total, w.target, chosen, w.got);
+        inblock_wave_kernel<1, Mask><<<grid, 256, 0, s>>>(score, mask, g, total, n_total, w.target, chosen, w.bq,
+                                                          w.ckey, nullptr);
         break;
       case 8:
-        inblock_wave_kernel<8, Mask><<<grid, 256, 0, s>>>(score, mask, g, batch, n_total, w.target, chosen, w.got);
+        inblock_wave_kernel<2, Mask><<<grid, 256, 0, s>>>(score, mask, g, total, n_total, w.target, chosen, w.bq,
+                                                          w.ckey, nullptr);
         break;
       default:
-        inblock_wave_kernel<64, Mask><<<grid, 256, 0, s>>>(score, mask, g, batch, n_total, w.target, chosen, w.got);
+        inblock_wave_kernel<4, Mask><<<grid, 256, 0, s>>>(score, mask, g, total, n_total, w.target, chosen, w.bq,
+                                                          w.ckey, w.bnd);
         break;
     }
   } else {
     inblock_wg_kernel<Mask><<<static_cast<unsigned>(batch * g.nb), kWG, 0, s>>>(score, mask, g, n_total, w.target,
-                                                                                chosen, w.got);
+                                                                                chosen, w.bq, w.ckey);
   }
   SVHIP_LAUNCHED(name);
-  fix_kernel<Mask><<<static_cast<unsigned>(batch), kWG, 0, s>>>(score, mask, g.n, k, w.got, chosen, bad);
+  fix_kernel<<<static_cast<unsigned>(batch), kWG, 0, s>>>(g.n, g.nb, k, w.bq, w.ckey, w.bnd, chosen, bad);
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;
 }

@@ -270,3 +270,52 @@ def test_ease_select_fused_equals_split_contract(dev):
                                     selectable.reshape(shape), ks[i], b, poss[i], fracs[i], nts[i], coms[i])
         agree = (ref == expect).mean()
         assert agree > 0.999, agree
+
+
+def _trajectory_states(seed, steps=25):
+    """The selection states of one window walked by the oracle: a low-entropy-last deferred top per column, then
+    25 quarter-cosine quotas, each step committing the oracle's own choice over fresh bimodal scores. The clamped
+    block quotas leave small trims and top-ups, the common case of a real window."""
+    g = np.random.default_rng(seed)
+    shape, b = (256, 16, 16), 4
+    tops = g.integers(96, 200, (16, 16))
+    last = np.arange(256)[:, None, None] >= tops[None]
+    n_last = int(last.sum())
+    quotas = S.low_entropy_last_quotas(last.size, steps, n_last)
+    pos = S.order_to_pos(g.permutation(1024))
+    n_total = S.block_view(~last, b).sum(1)
+    committed = np.zeros(shape, bool)
+    done = 0
+    for k in quotas:
+        score = np.where(g.random(shape) < 0.7, -g.random(shape) * 1e-2, -1 - 4 * g.random(shape)).astype(np.float32)
+        selectable = ~last & ~committed
+        frac = (done + k) / int((~last).sum())
+        yield score, selectable, k, pos, frac, n_total, done
+        chosen = S.quota_select_nosync(score, selectable, k, b, pos, frac, n_total, done)
+        committed |= chosen
+        done += k
+
+
+def test_quota_select_window_trajectories_trim_and_top_up(dev):
+    """Bit-exact along whole windows, and the small trim / top-up corrections (up to 16 voxels, resolved from the
+    per-block boundary candidates) as well as larger ones all occur. A committed count below the true one makes the
+    block quotas fall short of k, which is how the top-up cases are made."""
+    from streamvoxel_amd.sampling.block_quota import quota_select
+    seen = {'trim_small': 0, 'topup_small': 0, 'large': 0, 'exact': 0}
+    b = 4
+    cases = []
+    for seed in range(3):
+        for step, (score, selectable, k, pos, frac, n_total, done) in enumerate(_trajectory_states(seed)):
+            for shortfall in (0, 5, 40):
+                cases.append((seed, step, score, selectable, k, pos, frac, n_total, max(done - shortfall, 0)))
+    for seed, step, score, selectable, k, pos, frac, n_total, done in cases:
+        quota, *_ = S.apportion(selectable, n_total, pos, frac, done + k, b)
+        d = int(S.in_block_select(score, selectable, quota, b).sum()) - k
+        seen['exact' if d == 0 else ('large' if abs(d) > 16 else ('trim_small' if d > 0 else 'topup_small'))] += 1
+        _case(f'quota trajectory seed={seed} step={step} k={k} committed={done} got-k={d}')
+        expect = S.quota_select_nosync(score, selectable, k, b, pos, frac, n_total, done)
+        res = quota_select(torch.from_numpy(score).to(dev), torch.from_numpy(selectable).to(dev), k, b,
+                           torch.from_numpy(pos).to(dev), frac, torch.from_numpy(n_total).to(dev), done)
+        assert np.array_equal(res.cpu().numpy(), expect), (seed, step, d)
+    print('trajectory correction cases', seen, flush=True)
+    assert seen['trim_small'] > 0 and seen['topup_small'] > 0 and seen['large'] > 0, seen
