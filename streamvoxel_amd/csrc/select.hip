@@ -8,6 +8,7 @@
 //    select on the key finds the threshold key T and how many of the T-ties to keep, then ties are taken in index
 //    order with a ballot prefix count over index-ordered rounds.
 #include "common.hpp"
+#include "stats.hpp"
 
 namespace svhip {
 
@@ -249,17 +250,27 @@ struct MaskBytes {
   __device__ __forceinline__ bool operator()(int64_t b, int64_t flat) const { return mask[b * n + flat] != 0; }
 };
 
-// selectable = (tokens == mask_token) & ~last
-struct MaskTokens {
-  const int64_t* tokens;
-  const uint8_t* last;
-  int64_t mask_token;
-  int64_t n;
-  __device__ __forceinline__ bool operator()(int64_t b, int64_t flat) const {
-    const int64_t t = tokens[b * n + flat];
-    const uint8_t l = last[b * n + flat];
-    return (t == mask_token) & (l == 0);
+
+// Where the in-block pass gets each voxel's descending-score key (the sentinel for a voxel that is not
+// selectable): load() reads it, publish() leaves it in ckey for the trim / top-up pass.
+template <typename Mask>
+struct KeyFromScore {  // fp32 scores and a selectable mask; the keys are published
+  const float* score;
+  Mask mask;
+  uint32_t* ckey;
+  __device__ __forceinline__ uint32_t load(int64_t b, int64_t n, int64_t flat) const {
+    const float sv = score[b * n + flat];
+    return mask(b, flat) ? desc_key(sv) : KeyTraits<uint32_t>::kSentinel;
   }
+  __device__ __forceinline__ void publish(int64_t b, int64_t n, int64_t flat, uint32_t key) const {
+    ckey[b * n + flat] = key;
+  }
+};
+
+struct KeyStored {  // keys already in ckey (the fused entropy pass wrote them)
+  const uint32_t* ckey;
+  __device__ __forceinline__ uint32_t load(int64_t b, int64_t n, int64_t flat) const { return ckey[b * n + flat]; }
+  __device__ __forceinline__ void publish(int64_t, int64_t, int64_t, uint32_t) const {}
 };
 
 struct Geometry {
@@ -328,10 +339,11 @@ __global__ __launch_bounds__(kWG) void apportion_kernel(const int64_t* __restric
   });
 }
 
-// The same for windows of at most 64 kPerLane blocks, one wave per window (4 windows per workgroup) with the
-// keys in registers and no workgroup barriers: an MSB-first 8-bit radix select over the 64-bit keys with the
-// histogram in the wave's own LDS, then the `extra` smallest (key, block index) get one more voxel.
-constexpr int kPerLane = 16;
+// The same for one window of at most kWaveBlocks blocks, run by one wave without workgroup barriers: the keys in
+// LDS (`skey`, kWaveBlocks entries), an MSB-first 8-bit radix select over the 64-bit keys with the histogram
+// (`hist`, 256 entries) in LDS, then the `extra` smallest (key, block index) get one more voxel. Called by lanes
+// 0..63 of one wave; block j is handled by lane j % 64 throughout, so its global reads and writes need no fence.
+constexpr int kWaveBlocks = 1024;
 
 __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -339,116 +351,122 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__global__ __launch_bounds__(256) void apportion_wave_kernel(const int64_t* __restrict__ n_total,
-                                                             const int64_t* __restrict__ pos,
-                                                             const double* __restrict__ frac,
-                                                             const int64_t* __restrict__ k,
-                                                             const int64_t* __restrict__ committed, int64_t batch,
-                                                             int64_t nb, int64_t* __restrict__ target) {
+struct ApportionArgs {
+  const int64_t* n_total;
+  const int64_t* pos;
+  const double* frac;
+  const int64_t* k;
+  const int64_t* committed;
+  int64_t nb;
+  int64_t* target;
+};
+
+__device__ void apportion_window(const ApportionArgs& a, int64_t b, int lane, uint64_t* skey, uint32_t* hist) {
 #pragma clang fp contract(off)
-  __shared__ uint32_t hist_all[4][256];
-  const int lane = threadIdx.x & 63;
-  const int64_t b = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (b >= batch) return;
-  uint32_t* hist = hist_all[threadIdx.x >> 6];
-  const double f = frac[b];
-  const int64_t* nt = n_total + b * nb;
-  const int64_t* ps = pos + b * nb;
-  int64_t* tg = target + b * nb;
-  // Block j = lane + 64 t is held by this lane in slot t; absent blocks get the sentinel key.
-  // Loads are unconditional (clamped index) so that all of them are in flight at once; a conditional load would
-  // be waited for inside its branch.
-  int64_t ntv[kPerLane], psv[kPerLane];
-#pragma unroll
-  for (int t = 0; t < kPerLane; ++t) {
-    const int64_t j = lane + 64 * t < nb ? lane + 64 * t : nb - 1;
-    ntv[t] = nt[j];
-    psv[t] = ps[j];
-  }
-  uint64_t key[kPerLane];
-  int64_t base[kPerLane];
+  const int64_t nb = a.nb;
+  const double f = a.frac[b];
+  const int64_t* nt = a.n_total + b * nb;
+  const int64_t* ps = a.pos + b * nb;
+  int64_t* tg = a.target + b * nb;
+  constexpr int kUnrollBlocks = 4;
   int64_t local = 0;
+  for (int64_t j0 = lane; j0 < nb; j0 += 64 * kUnrollBlocks) {
+    // Loads are unconditional (clamped index) so that all of them are in flight at once.
+    int64_t ntv[kUnrollBlocks], psv[kUnrollBlocks];
 #pragma unroll
-  for (int t = 0; t < kPerLane; ++t) {
-    const double ideal = f * static_cast<double>(ntv[t]);
-    const double shifted = ideal + 1e-9;
-    const double bse = floor(shifted);
-    const double neg_frac = -(ideal - bse);
-    const double scaled = neg_frac * 1e6;
-    const double kd = scaled + static_cast<double>(psv[t]);
-    const bool in = lane + 64 * t < nb;
-    key[t] = in ? ordered_u64(kd) : ~0ull;
-    base[t] = in ? static_cast<int64_t>(bse) : 0;
-    local += base[t];
+    for (int u = 0; u < kUnrollBlocks; ++u) {
+      const int64_t j = j0 + 64 * u < nb ? j0 + 64 * u : nb - 1;
+      ntv[u] = nt[j];
+      psv[u] = ps[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnrollBlocks; ++u) {
+      const int64_t j = j0 + 64 * u;
+      if (j < nb) {
+        const double ideal = f * static_cast<double>(ntv[u]);
+        const double shifted = ideal + 1e-9;
+        const double base = floor(shifted);
+        const double neg_frac = -(ideal - base);
+        const double scaled = neg_frac * 1e6;
+        const double key = scaled + static_cast<double>(psv[u]);
+        skey[j] = ordered_u64(key);
+        tg[j] = static_cast<int64_t>(base);
+        local += static_cast<int64_t>(base);
+      }
+    }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) local += __shfl_xor(local, off, 64);
-  const int64_t extra = committed[b] + k[b] - local;
-  int64_t add[kPerLane];
-#pragma unroll
-  for (int t = 0; t < kPerLane; ++t) add[t] = 0;
+  const int64_t extra = a.committed[b] + a.k[b] - local;
+  if (extra <= 0) return;
   if (extra >= nb) {
+    for (int64_t j = lane; j < nb; j += 64) tg[j] += 1;
+    return;
+  }
+  wave_sync_lds();
+  // Threshold key T and how many T-ties to take (remaining) after the last digit.
+  uint64_t prefix = 0, hi_mask = 0;
+  int64_t remaining = extra;
+  for (int shift = 56; shift >= 0; shift -= 8) {
 #pragma unroll
-    for (int t = 0; t < kPerLane; ++t) add[t] = 1;
-  } else if (extra > 0) {
-    // Threshold key T and how many T-ties to take (remaining) after the last digit.
-    uint64_t prefix = 0, hi_mask = 0;
-    int64_t remaining = extra;
-    for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int q = 0; q < 4; ++q) hist[4 * lane + q] = 0u;
+    wave_sync_lds();
+    for (int64_t j = lane; j < nb; j += 64) {
+      const uint64_t key = skey[j];
+      if ((key & hi_mask) == prefix) atomicAdd(&hist[(key >> shift) & 0xff], 1u);
+    }
+    wave_sync_lds();
+    const uint32_t hs[4] = {hist[4 * lane], hist[4 * lane + 1], hist[4 * lane + 2], hist[4 * lane + 3]};
+    const int64_t mine = static_cast<int64_t>(hs[0]) + hs[1] + hs[2] + hs[3];
+    int64_t incl = mine;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) hist[4 * lane + q] = 0u;
-      wave_sync_lds();
+    for (int off = 1; off < 64; off <<= 1) {
+      const int64_t up = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += up;
+    }
+    // The lane whose four bins hold the remaining-th key finds the bin; everyone reads it from that lane.
+    const uint64_t who = __ballot(incl - mine < remaining && remaining <= incl);
+    const int src = __builtin_ctzll(who);
+    int64_t before = incl - mine;
+    int bin = 4 * lane + 3;
+    bool found = false;
 #pragma unroll
-      for (int t = 0; t < kPerLane; ++t) {
-        if (key[t] != ~0ull && (key[t] & hi_mask) == prefix) atomicAdd(&hist[(key[t] >> shift) & 0xff], 1u);
-      }
-      wave_sync_lds();
-      const uint32_t hs[4] = {hist[4 * lane], hist[4 * lane + 1], hist[4 * lane + 2], hist[4 * lane + 3]};
-      const int64_t mine = static_cast<int64_t>(hs[0]) + hs[1] + hs[2] + hs[3];
-      int64_t incl = mine;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int64_t up = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += up;
-      }
-      // The lane whose four bins hold the remaining-th key finds the bin; everyone reads it from that lane.
-      const uint64_t who = __ballot(incl - mine < remaining && remaining <= incl);
-      const int src = __builtin_ctzll(who);
-      int64_t before = incl - mine;
-      int bin = 4 * lane + 3;
-      bool found = false;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (!found) {
-          if (before + hs[q] < remaining) {
-            before += hs[q];
-          } else {
-            bin = 4 * lane + q;
-            found = true;
-          }
+    for (int q = 0; q < 4; ++q) {
+      if (!found) {
+        if (before + hs[q] < remaining) {
+          before += hs[q];
+        } else {
+          bin = 4 * lane + q;
+          found = true;
         }
       }
-      prefix |= static_cast<uint64_t>(__shfl(bin, src, 64)) << shift;
-      remaining -= __shfl(before, src, 64);
-      hi_mask |= static_cast<uint64_t>(0xff) << shift;
-      wave_sync_lds();
     }
-    // key < T: one more; key == T: the first `remaining` in block order (slot t, then lane).
-    int64_t ties_before = 0;
-#pragma unroll
-    for (int t = 0; t < kPerLane; ++t) {
-      const bool tie = key[t] == prefix && key[t] != ~0ull;
-      const uint64_t tb = __ballot(tie);
-      const int64_t rank = ties_before + __popcll(tb & ((1ull << lane) - 1ull));
-      add[t] = (key[t] < prefix || (tie && rank < remaining)) ? 1 : 0;
-      ties_before += __popcll(tb);
-    }
+    prefix |= static_cast<uint64_t>(__shfl(bin, src, 64)) << shift;
+    remaining -= __shfl(before, src, 64);
+    hi_mask |= static_cast<uint64_t>(0xff) << shift;
+    wave_sync_lds();
   }
-#pragma unroll
-  for (int t = 0; t < kPerLane; ++t) {
-    const int64_t j = lane + 64 * t;
-    if (j < nb) tg[j] = base[t] + add[t];
+  // key < T: one more; key == T: the first `remaining` in block order.
+  int64_t ties_before = 0;
+  for (int64_t j0 = 0; j0 < nb; j0 += 64) {
+    const int64_t j = j0 + lane;
+    const uint64_t key = j < nb ? skey[j] : ~0ull;
+    const bool tie = j < nb && key == prefix;
+    const uint64_t tb = __ballot(tie);
+    const int64_t rank = ties_before + __popcll(tb & ((1ull << lane) - 1ull));
+    if (j < nb && (key < prefix || (tie && rank < remaining))) tg[j] += 1;
+    ties_before += __popcll(tb);
   }
+}
+
+// Standalone: one wave per window, 4 windows per workgroup.
+__global__ __launch_bounds__(256) void apportion_wave_kernel(ApportionArgs a, int64_t batch) {
+  __shared__ uint64_t skey[4][kWaveBlocks];
+  __shared__ uint32_t hist[4][256];
+  const int w = threadIdx.x >> 6;
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  if (b >= batch) return;
+  apportion_window(a, b, threadIdx.x & 63, skey[w], hist[w]);
 }
 
 // ------------------------------------------------------------------------------------------ in-block selection
@@ -457,12 +475,12 @@ __global__ __launch_bounds__(256) void apportion_wave_kernel(const int64_t* __re
 // ckey[B, N] (flat order) the descending-score key of every selectable voxel (the sentinel elsewhere).
 
 // Blocks of at most 64 voxels (b in {1, 2, 4}): one wave holds 64 / b^3 whole blocks, lane = in-block index.
-template <int BB, typename Mask>
-__global__ __launch_bounds__(256) void inblock_wave_kernel(const float* __restrict__ score, Mask mask, Geometry g,
-                                                           int total, const int64_t* __restrict__ n_total,
+template <int BB, typename KeySrc>
+__global__ __launch_bounds__(256) void inblock_wave_kernel(KeySrc src, Geometry g, int total,
+                                                           const int64_t* __restrict__ n_total,
                                                            const int64_t* __restrict__ target,
                                                            uint8_t* __restrict__ chosen, int32_t* __restrict__ bq,
-                                                           uint32_t* __restrict__ ckey, uint64_t* __restrict__ bnd) {
+                                                           uint64_t* __restrict__ bnd) {
   constexpr int B3 = BB * BB * BB;
   const int lane = threadIdx.x & 63;
   const int e = static_cast<int>(blockIdx.x) * blockDim.x + threadIdx.x;  // block-major element
@@ -473,10 +491,9 @@ __global__ __launch_bounds__(256) void inblock_wave_kernel(const float* __restri
   const int b = jg / nb;
   const int j = jg - b * nb;
   const int flat = g.flat32<BB>(j, i);
-  const float sv = score[b * n + flat];
-  const bool masked = mask(b, flat);
-  const uint32_t key = masked ? desc_key(sv) : KeyTraits<uint32_t>::kSentinel;
-  ckey[b * n + flat] = key;
+  const uint32_t key = src.load(b, n, flat);
+  const bool masked = key != KeyTraits<uint32_t>::kSentinel;
+  src.publish(b, n, flat, key);
   const int group0 = lane & ~(B3 - 1);
   const uint64_t ballot = __ballot(masked);
   const uint64_t gmask = (B3 == 64) ? ~0ull : (((1ull << B3) - 1ull) << group0);
@@ -512,28 +529,22 @@ __global__ __launch_bounds__(256) void inblock_wave_kernel(const float* __restri
 }
 
 // Blocks of more than 64 voxels (b >= 8): one workgroup per block.
-template <typename Mask>
-__global__ __launch_bounds__(kWG) void inblock_wg_kernel(const float* __restrict__ score, Mask mask, Geometry g,
-                                                         const int64_t* __restrict__ n_total,
+template <typename KeySrc>
+__global__ __launch_bounds__(kWG) void inblock_wg_kernel(KeySrc src, Geometry g, const int64_t* __restrict__ n_total,
                                                          const int64_t* __restrict__ target,
-                                                         uint8_t* __restrict__ chosen, int32_t* __restrict__ bq,
-                                                         uint32_t* __restrict__ ckey) {
+                                                         uint8_t* __restrict__ chosen, int32_t* __restrict__ bq) {
   __shared__ SelectShared<uint32_t> sh;
   const int64_t jg = blockIdx.x;
   const int64_t b = jg / g.nb;
   const int64_t j = jg - b * g.nb;
   const int64_t b3 = g.b * g.b * g.b;
-  const float* sc = score + b * g.n;
-  auto get = [&](int64_t i) -> uint32_t {
-    const int64_t flat = g.flat_of(j, i);
-    return mask(b, flat) ? desc_key(sc[flat]) : KeyTraits<uint32_t>::kSentinel;
-  };
-  // legal = number of masked voxels; the keys are also left for the trim / top-up pass
+  auto get = [&](int64_t i) -> uint32_t { return src.load(b, g.n, g.flat_of(j, i)); };
+  // legal = number of selectable voxels; the keys are also left for the trim / top-up pass
   int64_t local = 0;
   for (int64_t i = threadIdx.x; i < b3; i += kWG) {
     const int64_t flat = g.flat_of(j, i);
     const uint32_t key = get(i);
-    ckey[b * g.n + flat] = key;
+    src.publish(b, g.n, flat, key);
     local += key != KeyTraits<uint32_t>::kSentinel ? 1 : 0;
   }
   const int64_t legal = block_sum_i64(local, sh.red);
@@ -767,43 +778,123 @@ static QuotaWs carve(void* ws, int64_t batch, const Geometry& g) {
   return w;
 }
 
-template <typename Mask>
-static int launch_quota(const float* score, Mask mask, int64_t batch, const Geometry& g, const int64_t* k,
-                        const int64_t* pos, const double* frac, const int64_t* n_total, const int64_t* committed,
-                        uint8_t* chosen, uint8_t* bad, const QuotaWs& w, hipStream_t s, const char* name) {
-  if (g.nb <= 64 * kPerLane) {
-    apportion_wave_kernel<<<static_cast<unsigned>(cdiv(batch, 4)), 256, 0, s>>>(n_total, pos, frac, k, committed,
-                                                                                batch, g.nb, w.target);
+// Apportionment alone (the fused entropy pass runs it on the side when the window has at most kWaveBlocks
+// blocks).
+static int launch_apportion(int64_t batch, const Geometry& g, const int64_t* k, const int64_t* pos,
+                            const double* frac, const int64_t* n_total, const int64_t* committed, const QuotaWs& w,
+                            hipStream_t s, const char* name) {
+  if (g.nb <= kWaveBlocks) {
+    const ApportionArgs a{n_total, pos, frac, k, committed, g.nb, w.target};
+    apportion_wave_kernel<<<static_cast<unsigned>(cdiv(batch, 4)), 256, 0, s>>>(a, batch);
   } else {
     apportion_kernel<<<static_cast<unsigned>(batch), kWG, 0, s>>>(n_total, pos, frac, k, committed, g.nb, w.keys,
                                                                    w.target);
   }
   SVHIP_LAUNCHED(name);
+  return SVHIP_OK;
+}
+
+// In-block selection and trim / top-up, after the targets exist.
+template <typename KeySrc>
+static int launch_inblock_fix(KeySrc src, int64_t batch, const Geometry& g, const int64_t* k,
+                              const int64_t* n_total, uint8_t* chosen, uint8_t* bad, const QuotaWs& w,
+                              hipStream_t s, const char* name) {
   const int64_t b3 = g.b * g.b * g.b;
   if (b3 <= 64) {
     const int total = static_cast<int>(batch * g.n);
     const unsigned grid = static_cast<unsigned>(cdiv(total, 256));
     switch (b3) {
       case 1:
-        inblock_wave_kernel<1, Mask><<<grid, 256, 0, s>>>(score, mask, g, total, n_total, w.target, chosen, w.bq,
-                                                          w.ckey, nullptr);
+        inblock_wave_kernel<1, KeySrc><<<grid, 256, 0, s>>>(src, g, total, n_total, w.target, chosen, w.bq, nullptr);
         break;
       case 8:
-        inblock_wave_kernel<2, Mask><<<grid, 256, 0, s>>>(score, mask, g, total, n_total, w.target, chosen, w.bq,
-                                                          w.ckey, nullptr);
+        inblock_wave_kernel<2, KeySrc><<<grid, 256, 0, s>>>(src, g, total, n_total, w.target, chosen, w.bq, nullptr);
         break;
       default:
-        inblock_wave_kernel<4, Mask><<<grid, 256, 0, s>>>(score, mask, g, total, n_total, w.target, chosen, w.bq,
-                                                          w.ckey, w.bnd);
+        inblock_wave_kernel<4, KeySrc><<<grid, 256, 0, s>>>(src, g, total, n_total, w.target, chosen, w.bq, w.bnd);
         break;
     }
   } else {
-    inblock_wg_kernel<Mask><<<static_cast<unsigned>(batch * g.nb), kWG, 0, s>>>(score, mask, g, n_total, w.target,
-                                                                                chosen, w.bq, w.ckey);
+    inblock_wg_kernel<KeySrc><<<static_cast<unsigned>(batch * g.nb), kWG, 0, s>>>(src, g, n_total, w.target, chosen,
+                                                                                  w.bq);
   }
   SVHIP_LAUNCHED(name);
   fix_kernel<<<static_cast<unsigned>(batch), kWG, 0, s>>>(g.n, g.nb, k, w.bq, w.ckey, w.bnd, chosen, bad);
   SVHIP_LAUNCHED(name);
+  return SVHIP_OK;
+}
+
+// --------------------------------------------------------------------------------------- fused EASE entropy pass
+
+// Output of the fused pass: the voxel's key (descending score if tokens == mask_token and not deferred, else the
+// sentinel) into ckey, the fp32 score into `scores` when given.
+struct KeyStore {
+  const int64_t* tokens;
+  const uint8_t* last;
+  int64_t mask_token;
+  uint32_t* ckey;
+  float* scores;
+  struct Pre {
+    int64_t token;
+    uint8_t deferred;
+  };
+  __device__ __forceinline__ Pre prefetch(int64_t voxel) const { return Pre{tokens[voxel], last[voxel]}; }
+  __device__ __forceinline__ void store(int64_t voxel, float value, Pre pre) const {
+    const bool selectable = (pre.token == mask_token) & (pre.deferred == 0);
+    ckey[voxel] = selectable ? desc_key(value) : KeyTraits<uint32_t>::kSentinel;
+    if (scores) scores[voxel] = value;
+  }
+};
+
+// Workgroups [0, side) apportion window blockIdx.x (one wave); the rest run the entropy pass over the logits and
+// write the keys. The apportionment depends only on the selection state, so it runs alongside the HBM-bound pass.
+template <typename T, int LAYOUT, int NV>
+__global__ __launch_bounds__(256) void ease_stats_kernel(const T* __restrict__ x, int64_t batch, int64_t n, int64_t C,
+                                                         int64_t sb, int64_t sc, int64_t sn, KeyStore ks,
+                                                         ApportionArgs ap, int side) {
+  __shared__ uint64_t skey[kWaveBlocks];
+  __shared__ uint32_t hist[256];
+  if (static_cast<int>(blockIdx.x) < side) {
+    if (threadIdx.x < 64) apportion_window(ap, blockIdx.x, threadIdx.x, skey, hist);
+    return;
+  }
+  const int64_t blk = blockIdx.x - side, nblk = gridDim.x - side;
+  if constexpr (LAYOUT == kVoxelMajor) {
+    voxel_major_pass<T, NV, kEntropy>(x, batch * n, n, C, sb, sn, nullptr, ks, blk, nblk);
+  } else {
+    class_major_pass<T, LAYOUT == kClassMajorVec, kEntropy>(x, batch, n, C, sb, sc, sn, nullptr, ks, blk, nblk);
+  }
+}
+
+template <typename T>
+static int launch_ease_stats(const T* x, int64_t batch, int64_t C, int64_t n, int64_t sb, int64_t sc, int64_t sn,
+                             const KeyStore& ks, const ApportionArgs& ap, int side, hipStream_t s) {
+  const StatsPlan plan = plan_stats<T>(x, batch, C, n, sb, sc, sn);
+  const unsigned grid = static_cast<unsigned>(plan.grid + side);
+  if (plan.layout == kVoxelMajor) {
+#define SVHIP_EVM(NVV)                                                                                          \
+  case NVV:                                                                                                     \
+    ease_stats_kernel<T, kVoxelMajor, NVV><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side); \
+    return SVHIP_OK;
+    switch (plan.nv) {
+      SVHIP_EVM(1)
+      SVHIP_EVM(2)
+      SVHIP_EVM(3)
+      SVHIP_EVM(4)
+      SVHIP_EVM(5)
+      SVHIP_EVM(6)
+      SVHIP_EVM(7)
+      SVHIP_EVM(8)
+      default:
+        break;
+    }
+#undef SVHIP_EVM
+  }
+  if (plan.layout == kClassMajorVec) {
+    ease_stats_kernel<T, kClassMajorVec, 0><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side);
+  } else {
+    ease_stats_kernel<T, kClassMajorScalar, 0><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side);
+  }
   return SVHIP_OK;
 }
 
@@ -832,14 +923,18 @@ extern "C" int svhip_quota_select(const float* score, const uint8_t* mask, int64
     set_error("%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
     return SVHIP_EWORKSPACE;
   }
-  return launch_quota(score, MaskBytes{mask, g.n}, batch, g, k, pos, frac, n_total, committed, chosen, bad,
-                      carve(workspace, batch, g), as_stream(stream), name);
+  const QuotaWs w = carve(workspace, batch, g);
+  hipStream_t s = as_stream(stream);
+  rc = launch_apportion(batch, g, k, pos, frac, n_total, committed, w, s, name);
+  if (rc != SVHIP_OK) return rc;
+  return launch_inblock_fix(KeyFromScore<MaskBytes>{score, MaskBytes{mask, g.n}, w.ckey}, batch, g, k, n_total,
+                            chosen, bad, w, s, name);
 }
 
 extern "C" size_t svhip_ease_select_workspace_bytes(int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_t block) {
   Geometry g;
   if (check_geometry(batch, Y, Z, X, block, "svhip_ease_select_workspace_bytes", &g) != SVHIP_OK) return 0;
-  return quota_ws_bytes(batch, g) + ((sizeof(float) * batch * g.n + 255) & ~size_t(255));
+  return quota_ws_bytes(batch, g);
 }
 
 extern "C" int svhip_ease_select(const void* logits, int dtype, int64_t classes, int64_t stride_b, int64_t stride_c,
@@ -855,17 +950,33 @@ extern "C" int svhip_ease_select(const void* logits, int dtype, int64_t classes,
   if (rc != SVHIP_OK) return rc;
   SVHIP_REQUIRE(logits && tokens && last && k && pos && frac && n_total && committed && chosen && bad,
                 "%s: null pointer", name);
-  const size_t qbytes = quota_ws_bytes(batch, g);
-  const size_t need = qbytes + ((sizeof(float) * batch * g.n + 255) & ~size_t(255));
+  SVHIP_REQUIRE(classes >= 1, "%s: bad class count %lld", name, (long long)classes);
+  SVHIP_REQUIRE(dtype == SVHIP_F32 || dtype == SVHIP_BF16, "%s: dtype %d not supported (fp32 or bf16)", name, dtype);
+  const size_t need = quota_ws_bytes(batch, g);
   if (workspace == nullptr || workspace_bytes < need) {
     set_error("%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
     return SVHIP_EWORKSPACE;
   }
-  float* scores = scores_out ? scores_out : reinterpret_cast<float*>(static_cast<char*>(workspace) + qbytes);
-  rc = svhip_entropy(logits, dtype, batch, classes, g.n, stride_b, stride_c, stride_n, scores, stream);
+  const QuotaWs w = carve(workspace, batch, g);
+  hipStream_t s = as_stream(stream);
+  // Windows of at most kWaveBlocks blocks are apportioned by side workgroups of the entropy pass.
+  const int side = g.nb <= kWaveBlocks ? static_cast<int>(batch) : 0;
+  if (side == 0) {
+    rc = launch_apportion(batch, g, k, pos, frac, n_total, committed, w, s, name);
+    if (rc != SVHIP_OK) return rc;
+  }
+  const KeyStore ks{tokens, last, mask_token, w.ckey, scores_out};
+  const ApportionArgs ap{n_total, pos, frac, k, committed, g.nb, w.target};
+  if (dtype == SVHIP_F32) {
+    rc = launch_ease_stats<float>(static_cast<const float*>(logits), batch, classes, g.n, stride_b, stride_c, stride_n,
+                                  ks, ap, side, s);
+  } else {
+    rc = launch_ease_stats<uint16_t>(static_cast<const uint16_t*>(logits), batch, classes, g.n, stride_b, stride_c,
+                                     stride_n, ks, ap, side, s);
+  }
   if (rc != SVHIP_OK) return rc;
-  return launch_quota(scores, MaskTokens{tokens, last, mask_token, g.n}, batch, g, k, pos, frac, n_total, committed,
-                      chosen, bad, carve(workspace, batch, g), as_stream(stream), name);
+  SVHIP_LAUNCHED(name);
+  return launch_inblock_fix(KeyStored{w.ckey}, batch, g, k, n_total, chosen, bad, w, s, name);
 }
 
 extern "C" int svhip_top_mask(const float* scores, const uint8_t* eligible, int64_t batch, int64_t n,

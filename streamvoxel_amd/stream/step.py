@@ -140,8 +140,9 @@ class EaseSelect:
         self.committed[index].fill_(int(committed))
         self.frac[index].fill_(float(frac))
 
-    def run(self, logits, n=None):
-        """Entropy + selectable + block-quota select + bad flag for the first n windows (capturable)."""
+    def run(self, logits, n=None, keep_scores=False):
+        """Entropy + selectable + block-quota select + bad flag for the first n windows (capturable). With
+        keep_scores the fp32 scores are also left in `self.scores`."""
         n = self.batch if n is None else n
         _lib.require_gpu(logits)
         code, C, sb, sc, sn = self._layout(logits, n, self.n)
@@ -151,7 +152,8 @@ class EaseSelect:
             _lib.ptr(logits), code, C, sb, sc, sn, _lib.ptr(self.tokens), self.classes,
             _lib.ptr(self.last.view(torch.uint8)), n, Y, Z, X, self.block, _lib.ptr(self.k), _lib.ptr(self.pos),
             _lib.ptr(self.frac), _lib.ptr(self.n_total), _lib.ptr(self.committed),
-            _lib.ptr(self.chosen.view(torch.uint8)), _lib.ptr(self.bad.view(torch.uint8)), _lib.ptr(self.scores),
+            _lib.ptr(self.chosen.view(torch.uint8)), _lib.ptr(self.bad.view(torch.uint8)),
+            _lib.ptr(self.scores) if keep_scores else None,
             _lib.ptr(self.ws.buffer), self.ws.buffer.numel(), _lib.stream_of(logits)), 'svhip_ease_select')
 
     def mark(self, logits, eps, n=None):

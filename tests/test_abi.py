@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol(lib):
 def test_workspace_queries_and_argument_errors(lib):
     n = lib.svhip_quota_select_workspace_bytes(8, 256, 16, 16, 4)
     assert n >= 8 * 1024 * 16 + 8 * 8
-    assert lib.svhip_ease_select_workspace_bytes(8, 256, 16, 16, 4) >= n + 8 * 65536 * 4
+    assert lib.svhip_ease_select_workspace_bytes(8, 256, 16, 16, 4) >= 8 * 65536 * 4   # at least the voxel keys
     assert lib.svhip_quota_select_workspace_bytes(1, 256, 16, 16, 3) == 0          # unsupported block size
     assert b'unsupported' in lib.svhip_last_error()
     assert lib.svhip_quota_select_workspace_bytes(1, 256, 16, 12, 8) == 0          # 12 not divisible by 8
