@@ -194,6 +194,44 @@ def time_events(fn, reps, warm=3):
     return start.elapsed_time(end) / reps / 1e3   # seconds per call
 
 
+def time_graph(fn, reps, replays=5):
+    """Seconds per call of `fn` from HIP events around replays of one graph of `reps` back-to-back calls (no host
+    gaps between the launches), recorded on the stream the graph launches on."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / (reps * replays) / 1e3
+
+
+def profiled_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (a line
+    `traffic <kernel> <bytes>`), or None when there is none."""
+    path = os.path.join(ROOT, 'profiles', 'hbm_traffic_8slot.md')
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.strip().strip('`').split()
+            if len(parts) == 3 and parts[0] == 'traffic' and parts[1] == kernel:
+                return float(parts[2])
+    return None
+
+
 def measured_peaks(dev):
     import torch
     out = {}
@@ -287,13 +325,13 @@ def main():
     log(f'{ms_per_step:.3f} ms/step, bad={bad}')
     value = SLOTS * VOXELS / (STEPS_PER_WINDOW * ms_per_step / 1e3)
 
-    # Component timings with HIP events on the launching stream (the current stream).
-    t_layer = time_events(lambda: w.ctx.attend(0, w.q[1][0], out=w.o[0].transpose(1, 2)), 20)
+    # Component timings: HIP events around graphs of back-to-back launches on the launching stream.
+    t_layer = time_graph(lambda: w.ctx.attend(0, w.q[1][0], out=w.o[0].transpose(1, 2)), 20)
     w.sel.k.copy_(w.k_tab[0])
     w.sel.committed.copy_(w.com_tab[0])
     w.sel.frac.copy_(w.frac_tab[0])
     w.sel.tokens.fill_(CLASSES)
-    t_select = time_events(lambda: w.sel.run(w.logits[0]), 20)
+    t_select = time_graph(lambda: w.sel.run(w.logits[0]), 20)
     from streamvoxel_amd.sampling.entropy import entropy_batched
     ent_out = torch.empty(SLOTS, VOXELS, device=dev)
     t_entropy = time_events(lambda: entropy_batched(w.logits[0].view(SLOTS, VOXELS, CLASSES), 'voxel_major',
@@ -319,11 +357,13 @@ def main():
                     kv_lengths=w.lengths, kv_dtype=args.kv_dtype, window=list(SHAPE), classes=CLASSES, block=BLOCK,
                     steps_per_window=STEPS_PER_WINDOW, parallelism='single GPU (slots are independent)'),
         roofline=dict(kernel='xattn_fwd_kernel', bound='mfma', achieved=xattn_tflops, peak=PEAK_BF16_TFLOPS,
-                      unit='TFLOP/s', frac=xattn_tflops / PEAK_BF16_TFLOPS, traffic=None,
+                      unit='TFLOP/s', frac=xattn_tflops / PEAK_BF16_TFLOPS,
+                      traffic=profiled_traffic('xattn_fwd_kernel'),
                       flops_per_launch=w.flops_per_layer, avg_launch_us=t_layer * 1e6),
         roofline_select=dict(kernel='svhip_ease_select (entropy + apportion + in-block + fix)', bound='hbm',
                              achieved=select_gbs, peak=PEAK_HBM_GBS, unit='GB/s', frac=select_gbs / PEAK_HBM_GBS,
-                             bytes_per_call=w.select_bytes, avg_call_us=t_select * 1e6,
+                             traffic=profiled_traffic('ease_select'), bytes_per_call=w.select_bytes,
+                             avg_call_us=t_select * 1e6,
                              entropy_kernel_GBps=entropy_bytes / t_entropy / 1e9, entropy_us=t_entropy * 1e6),
         components=dict(xattn_ms_per_step=LAYERS * t_layer * 1e3, select_ms_per_step=t_select * 1e3,
                         selection_bad_flag_seen=bad),

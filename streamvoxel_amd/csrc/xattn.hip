@@ -4,10 +4,11 @@
 // 64-key blocks staged through LDS, double-buffered: the next block is in flight while the current one is
 // computed, one workgroup barrier per block.
 //
-// Per wave and key block (v_mfma_f32_32x32x16_bf16 throughout):
+// Per wave and key block (v_mfma_f32_32x32x16_bf16 throughout), in two 32-key halves that each run the whole
+// online-softmax step (a half's scores take 16 registers, which leaves room for three waves per SIMD):
 //   S^T[key, q] = K . Q^T         A = K rows from LDS, B = the wave's Q (registers, loaded once)
 //   P^T = exp2(S^T * scale*log2e - m)   online softmax; every lane owns one query column (q = lane % 32) and
-//                                       16 of every 32 keys, its partner lane (lane ^ 32) the other 16
+//                                       8 of every 16 keys, its partner lane (lane ^ 32) the other 8
 //   O^T[d, q] += V^T . P^T        A = V^T rows from LDS, B = P^T straight from the S^T accumulators
 // The C layout of a 32x32 MFMA gives lane l the rows 8*(i/4) + 4*(l/32) + i%4 of column l%32. K rows are
 // stored in LDS under the involution sigma (swap of the 4-row groups 1 and 2 of every 16 rows), so accumulator
@@ -16,21 +17,24 @@
 // Because O^T's columns are queries too, the per-query rescale and the final 1/l are lane-local.
 //
 // The softmax is VALU-bound at head_dim 64 (one exp per score against 2 x 64 MACs), so per score it costs one
-// max3 third, one fma (scale and max subtraction fused), one exp, half a bf16 pack and half a bf16 dot (the row
-// sum is taken over the packed bf16 P, the same values the second product consumes):
-//   * the stored running max m is only raised when a block's max exceeds it by more than kLazy (log2 units);
-//     otherwise P may reach 2^kLazy, harmless in fp32 sums and bf16 P, and the O / l rescale is skipped for the
-//     whole wave. O and l always share the same m, so O / l is unchanged.
+// fma (scale and max subtraction fused), one exp, half a bf16 pack and half a bf16 dot (the row sum is taken over
+// the packed bf16 P, the same values the second product consumes), and no max:
+//   * P is formed against the running max m as it stands. The half's row sum tells whether m still bounds the
+//     half's scores: only a sum above 2^20 (or inf / NaN, as on the first half, where m is -inf) makes the wave
+//     take the half's max (16 three-input maxes and the partner's over v_permlane32_swap), raise m, rescale O
+//     and l and redo P. P may thus reach 2^20, harmless in fp32 sums and bf16 P; O and l always share m, so
+//     O / l does not depend on where m sits.
 //   * key masking runs only in the last, partial block; padding keys are staged as zeros.
-//   * the partner lane's block max comes over v_permlane32_swap, not an LDS round trip.
 //
-// Staging. LDS tiles hold 64 rows of 144 bytes (8 16-byte chunks + 16 bytes of padding, which keeps the 16-byte
-// operand reads conflict-free); a K row is one key's head_dim, a V^T row one head_dim element's 64 keys. bf16 K
-// and V^T of the padded [B,H,Kcap,*] layout with 16-byte aligned rows take global_load_lds_dwordx4, which moves
-// a full block straight into LDS without registers. Every other form goes through registers, prefetched one
-// block ahead: OCP e4m3fn K/V converted exactly to bf16 (v_cvt_scalef32_pk_bf16_fp8 with scale 1; the fp8 scales
-// are folded into the softmax scale (k_scale) and the output (v_scale)), row-major V transposed on the way, the
-// packed cu_seqlens layout, and the last partial block of a window.
+// Staging. An LDS tile holds 64 rows of 128 bytes, the eight 16-byte chunks of row r XOR-swizzled by (r / 2) % 8
+// so that the 16-byte operand reads are bank-conflict-free; a K row is one key's head_dim, a V^T row one
+// head_dim element's 64 keys. bf16 K and V^T of the padded [B,H,Kcap,*] layout with 16-byte aligned rows take
+// buffer_load_dwordx4 ... lds, which moves a full block straight into LDS without registers, addressed by a
+// per-lane offset fixed for the window plus a scalar block offset. Every other form goes through registers,
+// prefetched one block ahead: OCP e4m3fn K/V converted exactly to bf16 (v_cvt_scalef32_pk_bf16_fp8 with
+// scale 1; the fp8 scales are folded into the softmax scale (k_scale) and the output (v_scale)), row-major V
+// transposed on the way, the packed cu_seqlens layout. The last, partial block of a window is peeled out of the
+// loop and staged synchronously through registers, keys >= L as zeros.
 //
 // Workgroup order: windows are ranked by key count (longest first, ties by index) inside the kernel, so the
 // longest (window, head) pairs start first; consecutive workgroup ids go round robin to the 8 XCDs and all query
@@ -49,10 +53,10 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kQTile = 128;   // queries per workgroup
 constexpr int kKB = 64;       // keys per block
 constexpr int kDPad = 64;     // head_dim handled by the MFMA tiles (smaller head_dim is zero-padded)
-constexpr int kRow = 72;      // LDS row stride in bf16 elements (144 bytes: conflict-free 16-byte reads)
+constexpr int kRow = 64;      // LDS row stride in bf16 elements (128 bytes, 16-byte chunks XOR-swizzled)
 constexpr int kThreads = 256;
-constexpr int kSlots = kKB * kRow / 8;  // 16-byte slots of an LDS tile (64 rows x 9)
-constexpr float kLazy = 8.0f;  // log2-domain headroom before the running max is raised
+constexpr float kSumHigh = 1048576.0f;  // 2^20: a half's row sum above it makes the running max be raised
+constexpr float kFltMax = 3.40282347e38f;
 constexpr int kMaxRankWindows = 4096;
 
 struct XattnParams {
@@ -73,6 +77,11 @@ struct XattnParams {
   int q_tiles;
 };
 
+// Physical 16-byte chunk of logical chunk c in LDS row r. The 64 banks span two 128-byte rows and a 16-byte read
+// serves 16 lanes per cycle: 16 consecutive rows read at one logical chunk land on 16 different (row parity,
+// chunk) bank groups, so the operand reads (lane i of a group on row i) are conflict-free.
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
 // Row of key `key` (0..63) of a block inside the LDS K tile.
 __device__ __forceinline__ int sigma_row(int key) {
   const int y = key & 15;
@@ -92,7 +101,8 @@ __device__ __forceinline__ uint4 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
 }
 
 // v_max3_f32 without the operand canonicalisation the compiler adds around fmaxf (the MFMA results feeding it
-// are never signalling NaNs).
+// are never signalling NaNs). Inline asm: its operands must not be MFMA results the compiler has not yet waited
+// for (it inserts no wait states for inline asm).
 __device__ __forceinline__ float max3(float a, float b, float c) {
   float r;
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
@@ -175,36 +185,28 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT>& st, const XattnParams
   }
 }
 
-// Registers -> LDS (K rows under sigma; V as V^T [d][key]).
+// Registers -> LDS (K rows under sigma; V as V^T [d][key]; both swizzled).
 template <bool FP8, bool VT>
 __device__ __forceinline__ void stage_store(const Stage<FP8, VT>& st, uint16_t* sK, uint16_t* sV) {
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int c = threadIdx.x + kThreads * r;
     {
-      const int key = c >> 3, dc = c & 7;
-      *reinterpret_cast<uint4*>(sK + sigma_row(key) * kRow + dc * 8) = st.k[r];
+      const int R = sigma_row(c >> 3), dc = c & 7;
+      *reinterpret_cast<uint4*>(sK + R * kRow + swz(R, dc) * 8) = st.k[r];
     }
     if constexpr (VT) {
       const int d = c >> 3, kc = c & 7;
-      *reinterpret_cast<uint4*>(sV + d * kRow + kc * 8) = st.v[r];
+      *reinterpret_cast<uint4*>(sV + d * kRow + swz(d, kc) * 8) = st.v[r];
     } else {
       const int key = c >> 3, dc = c & 7;
       const uint32_t w[4] = {st.v[r].x, st.v[r].y, st.v[r].z, st.v[r].w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sV[(dc * 8 + e) * kRow + key] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+      for (int e = 0; e < 8; ++e) {
+        const int d = dc * 8 + e;
+        sV[d * kRow + swz(d, key >> 3) * 8 + (key & 7)] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+      }
     }
-  }
-}
-
-template <bool FP8, bool VT>
-__device__ __forceinline__ void stage_block(Stage<FP8, VT>& st, const XattnParams& p,
-                                            const typename Elem<FP8>::T* K, const typename Elem<FP8>::T* V, int L,
-                                            int kv0, int dchunks, bool vt_vec) {
-  if (kv0 + kKB <= L) {
-    stage_load<FP8, VT, false>(st, p, K, V, L, kv0, dchunks, vt_vec);
-  } else {
-    stage_load<FP8, VT, true>(st, p, K, V, L, kv0, dchunks, vt_vec);
   }
 }
 
@@ -219,34 +221,72 @@ __device__ __forceinline__ int window_length(const XattnParams& p, int64_t b) {
   return L < 0 ? 0 : static_cast<int>(L);
 }
 
-// Direct path (bf16 K and V^T, full block): global_load_lds_dwordx4 moves the block straight into LDS without
-// registers; each wave instruction fills 64 consecutive 16-byte slots of a tile (row R at slots 9 R .. 9 R + 8,
-// the ninth being padding), the 9 instructions of a tile spread over the 4 waves. Padding slots and chunks past
-// head_dim are not loaded (K's are zeroed once; V^T rows past head_dim only feed outputs that are never stored).
-__device__ __forceinline__ void stage_direct(const XattnParams& p, const uint16_t* K, const uint16_t* V, int kv0,
-                                             int dchunks, uint16_t* sK, uint16_t* sV) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// Direct path (bf16 K and V^T, full blocks): buffer_load_dwordx4 ... lds moves a block straight into LDS without
+// registers. Wave instruction j of a tile fills its rows 8 j .. 8 j + 7 (1024 consecutive bytes, lane l at
+// 16 l): row R = 8 j + l / 8, physical chunk l % 8, so the logical chunk c with swz(R, c) = l % 8. The 8
+// instructions of a tile go to the 4 waves two each. A lane's byte offsets from the (window, head) base depend only on the window, so
+// they are computed once; a block adds kv0 rows of K / columns of V^T through the scalar offset. The buffer
+// descriptors bound the reads to the window's full blocks (an out-of-range read returns zeros).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+struct DirectLanes {
+  __amdgpu_buffer_rsrc_t k_rsrc, v_rsrc;
+  uint32_t k[2];  // byte offsets of instructions w and w + 4 for the block at key 0
+  uint32_t v[2];
+  bool k_ok[2];   // the lane's K chunk lies inside head_dim
+  bool v_ok[2];   // the lane's V^T row lies inside head_dim
+};
+
+// Raw buffer descriptor word 3 for 32-bit-element untyped access.
+constexpr int kRsrcFlags = 0x00020000;
+
+__device__ __forceinline__ DirectLanes direct_lanes(const XattnParams& p, const uint16_t* K, const uint16_t* V,
+                                                    int dchunks, int nfull, int w) {
+  DirectLanes dl;
+  const int lane = threadIdx.x & 63;
+  const uint32_t k_bytes = static_cast<uint32_t>(((static_cast<int64_t>(nfull) * kKB - 1) * p.sk_k + p.D) * 2);
+  const uint32_t v_bytes = static_cast<uint32_t>(((p.D - 1) * p.sv_d + static_cast<int64_t>(nfull) * kKB) * 2);
+  dl.k_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(K), 0, k_bytes, kRsrcFlags);
+  dl.v_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(V), 0, v_bytes, kRsrcFlags);
 #pragma unroll
-  for (int i = w; i < kSlots / 64; i += kThreads / 64) {
-    const int slot = 64 * i + lane;
-    const int row = slot / 9, c = slot - 9 * (slot / 9);
-    if (c < dchunks) {
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(K + (kv0 + sigma_row(row)) * p.sk_k + c * 8),
-                                       reinterpret_cast<void*>(sK + 64 * 8 * i), 16, 0, 0);
+  for (int t = 0; t < 2; ++t) {
+    const int R = 8 * (w + 4 * t) + (lane >> 3);
+    const int c = swz(R, lane & 7);  // swz is an involution in c
+    dl.k[t] = static_cast<uint32_t>((sigma_row(R) * p.sk_k + 8 * c) * 2);
+    dl.v[t] = static_cast<uint32_t>((R * p.sv_d + 8 * c) * 2);
+    dl.k_ok[t] = c < dchunks;
+    dl.v_ok[t] = R < 8 * dchunks;
+  }
+  return dl;
+}
+
+// FULL_D: head_dim 64, every lane loads (no exec masking). w: the wave index (uniform).
+template <bool FULL_D>
+__device__ __forceinline__ void stage_direct(const DirectLanes& dl, uint32_t k_soff, uint32_t v_soff, int w,
+                                             uint16_t* sK, uint16_t* sV) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int j = w + 4 * t;
+    if (FULL_D || dl.k_ok[t]) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dl.k_rsrc, (lds_ptr_t)(sK + 512 * j), 16, dl.k[t],
+                                               k_soff, 0, 0);
     }
-    if (row < 8 * dchunks && c < 8) {
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(V + row * p.sv_d + kv0 + 8 * c),
-                                       reinterpret_cast<void*>(sV + 64 * 8 * i), 16, 0, 0);
+    if (FULL_D || dl.v_ok[t]) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dl.v_rsrc, (lds_ptr_t)(sV + 512 * j), 16, dl.v[t],
+                                               v_soff, 0, 0);
     }
   }
 }
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// DIRECT: bf16 K and V^T of the padded layout with 16-byte aligned rows (chosen on the host); full blocks are
-// staged with direct loads.
-template <bool FP8, bool VT, bool DIRECT>
+// STAGING: kRegister (registers for every block), kDirect (direct loads for full blocks, any head_dim),
+// kDirect64 (the same at head_dim 64). The last, partial block of a window always goes through registers.
+enum Staging { kRegister = 0, kDirect = 1, kDirect64 = 2 };
+
+template <bool FP8, bool VT, int STAGING>
 __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
+  constexpr bool DIRECT = STAGING != kRegister;
   // Four distinct LDS objects (not one indexed array): the compiler can then tell the direct loads into one
   // buffer from the operand reads of the other and does not wait for the loads in flight before those reads.
   __shared__ __attribute__((aligned(16))) uint16_t sK0[kKB * kRow], sK1[kKB * kRow];
@@ -285,7 +325,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   }
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 31;  // query column within the wave
   const int hh = lane >> 5;   // lane half
   const int64_t q = static_cast<int64_t>(qt) * kQTile + w * 32 + col;
@@ -327,146 +367,198 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   const int dchunks = static_cast<int>(p.D / 8);
   // V^T rows allow vector loads when every 8-key run starts aligned (the base, the row stride and the offset).
   const bool vt_vec = VT && ((reinterpret_cast<uintptr_t>(V) & (FP8 ? 7 : 15)) == 0) && (p.sv_d % 8 == 0);
-  const int nblocks = (L + kKB - 1) / kKB;
+  const int nfull = L / kKB;           // full key blocks
+  const bool tail = nfull * kKB < L;   // plus one partial block
 
-  if (DIRECT && dchunks < 8) {
-    // Chunks past head_dim of both K tiles are never loaded by the direct path; they must hold zeros.
-    for (int i = threadIdx.x; i < kSlots; i += kThreads) {
-      const int c = i - 9 * (i / 9);
-      if (c >= dchunks && c < 8) {
-        *reinterpret_cast<uint4*>(sK0 + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(sK1 + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
+  DirectLanes dl;
+  if constexpr (DIRECT) {
+    dl = direct_lanes(p, reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V), dchunks, nfull,
+                      w);
+    if (STAGING == kDirect && dchunks < 8) {
+      // Chunks past head_dim of both K tiles are never loaded by direct loads; they must hold zeros.
+      for (int i = threadIdx.x; i < kKB * 8; i += kThreads) {
+        const int R = i >> 3, c = i & 7;
+        if (c >= dchunks) {
+          *reinterpret_cast<uint4*>(sK0 + R * kRow + swz(R, c) * 8) = make_uint4(0u, 0u, 0u, 0u);
+          *reinterpret_cast<uint4*>(sK1 + R * kRow + swz(R, c) * 8) = make_uint4(0u, 0u, 0u, 0u);
+        }
       }
     }
   }
+
+  // Operand reads: lane (col, hh) takes logical chunk 2 s + hh of rows col and 32 + col of a tile; the two rows
+  // share the swizzle, so four byte offsets serve K and V^T of both buffers.
+  uint32_t rd[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) rd[s] = static_cast<uint32_t>(col * kRow * 2 + swz(col, 2 * s + hh) * 16);
 
   f32x16_t o0 = {0}, o1 = {0};  // O^T tiles: d in [0,32) and [32,64)
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
   float l0 = 0.f, l1 = 0.f;     // row-sum partials of this lane's keys
 
-  // Stages block `blk` into (sK, sV): direct loads for a full block on the direct path (complete at the next
-  // vmem wait), registers otherwise (prefetched into `st` when `st_ready`, else loaded here).
+  // Full block `blk` into (sK, sV): issued now, complete at the next vmem wait (direct) or at `stage_commit`
+  // (registers, prefetched into `st`).
   Stage<FP8, VT> st;
-  auto stage_now = [&](int blk, uint16_t* sK, uint16_t* sV) {
-    const int kv0 = blk * kKB;
-    if (DIRECT && kv0 + kKB <= L) {
-      stage_direct(p, reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V), kv0, dchunks, sK,
-                   sV);
+  auto stage_issue = [&](int blk, uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
+    if constexpr (DIRECT) {
+      const int kv0 = blk * kKB;
+      stage_direct<STAGING == kDirect64>(dl, static_cast<uint32_t>(kv0 * p.sk_k * 2), static_cast<uint32_t>(kv0 * 2),
+                                         w, sK, sV);
     } else {
-      Stage<FP8, VT> tmp;
-      stage_block<FP8, VT>(tmp, p, K, V, L, kv0, dchunks, vt_vec);
-      stage_store<FP8, VT>(tmp, sK, sV);
+      stage_load<FP8, VT, false>(st, p, K, V, L, blk * kKB, dchunks, vt_vec);
     }
   };
-  stage_now(0, sK0, sV0);
-  wait_vmem();
-  __syncthreads();
+  auto stage_commit = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
+    if constexpr (!DIRECT) stage_store<FP8, VT>(st, sK, sV);
+  };
+  // The partial block, synchronously through registers.
+  auto stage_tail = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
+    Stage<FP8, VT> tmp;
+    stage_load<FP8, VT, true>(tmp, p, K, V, L, nfull * kKB, dchunks, vt_vec);
+    stage_store<FP8, VT>(tmp, sK, sV);
+  };
 
   const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
-  auto iteration = [&](int blk, const uint16_t* Ks, const uint16_t* Vt, uint16_t* nK, uint16_t* nV) {
-    const bool more = blk + 1 < nblocks;
-    const int kv_next = (blk + 1) * kKB;
-    // Next block: direct loads now (full blocks of the direct path), register prefetch now (register path), or
-    // a synchronous register staging after the compute (the last, partial block of the direct path).
-    const bool next_direct = DIRECT && more && kv_next + kKB <= L;
-    if (next_direct) {
-      stage_direct(p, reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V), kv_next, dchunks,
-                   nK, nV);
-    } else if (!DIRECT && more) {
-      stage_block<FP8, VT>(st, p, K, V, L, kv_next, dchunks, vt_vec);
-    }
-
-    // S^T for the two 32-key tiles.
-    f32x16_t s0 = {0}, s1 = {0};
+  // One key block from (Ks, Vt), as two 32-key halves that each run the whole online-softmax step (scores,
+  // running max, exponentials, second product): a half's scores take 16 registers, which keeps four waves per
+  // SIMD resident. MASKED: the partial block (keys >= L masked out).
+  auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vt, int kv0) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked)::value;
+    const char* kp = reinterpret_cast<const char*>(Ks);
+    const char* vp = reinterpret_cast<const char*>(Vt);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(Ks + col * kRow + 16 * s + 8 * hh);
-      const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(Ks + (32 + col) * kRow + 16 * s + 8 * hh);
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[s], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[s], s1, 0, 0, 0);
-    }
-    const int kv0 = blk * kKB;
-    if (kv0 + kKB > L) {
-      // Entry i of tile t is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8).
+    for (int t = 0; t < 2; ++t) {
+      // S^T of keys 32 t .. 32 t + 31 (LDS rows 32 t + col).
+      f32x16_t s = {0};
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kin = (i < 8) ? (8 * hh + i) : (16 + 8 * hh + (i - 8));
-        if (kv0 + kin >= L) s0[i] = -INFINITY;
-        if (kv0 + 32 + kin >= L) s1[i] = -INFINITY;
+      for (int k = 0; k < 4; ++k) {
+        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(kp + rd[k] + t * (32 * kRow * 2));
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], s, 0, 0, 0);
       }
-    }
-    // Block max of the raw scores (scale > 0, so it commutes with the scaling): 16 three-input maxes, and the
-    // partner lane's over v_permlane32_swap, which gives (x[l % 32], x[l % 32 + 32]) in every lane.
-    float ma = max3(s0[0], s0[1], s0[2]);
-    float mb = max3(s1[0], s1[1], s1[2]);
+      if constexpr (MASKED) {
+        // Entry i is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8).
 #pragma unroll
-    for (int i = 3; i < 15; i += 2) {
-      ma = max3(ma, s0[i], s0[i + 1]);
-      mb = max3(mb, s1[i], s1[i + 1]);
-    }
-    float mr = max3(ma, s0[15], mb);
-    mr = max3(mr, s1[15], s1[15]);
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mr), __float_as_int(mr), false, false);
-    mr = max3(__int_as_float(sw[0]), __int_as_float(sw[1]), __int_as_float(sw[1]));
-    const float cand = mr * sl2;
-    const bool raise = cand > m + kLazy;
-    if (__builtin_amdgcn_ballot_w64(raise) != 0ull) {
-      const float mn = raise ? cand : m;
-      const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 1 where m stays; 0 on the first block
-      m = mn;
-      l0 *= alpha;
-      l1 *= alpha;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        o0[i] *= alpha;
-        o1[i] *= alpha;
-      }
-    }
-    const float neg_m = -m;
-    // P^T as B operands: k-step (tile t, half s) = entries 16 t + 8 s + 0..7; the row sum over the packed bf16.
-    bf16x8_t pb[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const f32x16_t& src = (ks < 2) ? s0 : s1;
-      const int base = 8 * (ks & 1);
-      bf16x8_t v;
-#pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        f32x2_t two = {__builtin_amdgcn_exp2f(__builtin_fmaf(src[base + j], sl2, neg_m)),
-                       __builtin_amdgcn_exp2f(__builtin_fmaf(src[base + j + 1], sl2, neg_m))};
-        const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
-        if (j & 2) {
-          l1 = __builtin_amdgcn_fdot2_f32_bf16(c, ones, l1, false);
-        } else {
-          l0 = __builtin_amdgcn_fdot2_f32_bf16(c, ones, l0, false);
+        for (int i = 0; i < 16; ++i) {
+          const int kin = (i < 8) ? (8 * hh + i) : (16 + 8 * hh + (i - 8));
+          if (kv0 + 32 * t + kin >= L) s[i] = -INFINITY;
         }
-        v[j] = c[0];
-        v[j + 1] = c[1];
       }
-      pb[ks] = v;
-    }
-    // O^T += V^T . P^T ; k-step ks covers keys 16 ks + 8 hh + 0..7 of the block.
+      // P^T = exp2(S^T * scale*log2e - m) against the running max m as it stands, as B operands: k-step ks (keys
+      // 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7. The row sum is taken over the packed bf16 P, the values
+      // the second product consumes.
+      bf16x8_t pb[2];
+      float lb0, lb1;
+      auto exps = [&](float neg_m) __attribute__((always_inline)) {
+        lb0 = 0.f;
+        lb1 = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(Vt + col * kRow + 16 * ks + 8 * hh);
-      const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(Vt + (32 + col) * kRow + 16 * ks + 8 * hh);
-      o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pb[ks], o0, 0, 0, 0);
-      o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pb[ks], o1, 0, 0, 0);
-    }
-    if (more && !next_direct) {
-      if constexpr (DIRECT) {
-        stage_now(blk + 1, nK, nV);
-      } else {
-        stage_store<FP8, VT>(st, nK, nV);
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {
+            f32x2_t two = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j], sl2, neg_m)),
+                           __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j + 1], sl2, neg_m))};
+            const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
+            if (j & 2) {
+              lb1 = __builtin_amdgcn_fdot2_f32_bf16(c, ones, lb1, false);
+            } else {
+              lb0 = __builtin_amdgcn_fdot2_f32_bf16(c, ones, lb0, false);
+            }
+            pb[ks][j] = c[0];
+            pb[ks][j + 1] = c[1];
+          }
+        }
+      };
+      exps(-m);
+      // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN, as before
+      // the first half, where m is -inf) some score passed m by about 20 (log2 units). Only then is the half's
+      // max taken, m raised, O and l rescaled and P redone; O and l always share m, so O / l does not depend on
+      // where m sits.
+      if (__builtin_amdgcn_ballot_w64(!(lb0 + lb1 <= kSumHigh)) != 0ull) {
+        // Max of the raw scores (scale > 0, so it commutes with the scaling). The chain opens with a
+        // compiler-visible v_med3_f32 (med3(a, b, FLT_MAX) = max(a, b) for scores below +inf), before which the
+        // compiler inserts the wait states a VALU read of an MFMA result needs; the inline v_max3_f32 that follow
+        // (the compiler does not check inline asm for that hazard) read the same, by then complete,
+        // accumulator. The partner lane's max comes over v_permlane32_swap, which gives (x[l % 32],
+        // x[l % 32 + 32]) in every lane. Every query has a key below L in the first half, so m is finite after
+        // it.
+        float mr = __builtin_amdgcn_fmed3f(s[0], s[1], kFltMax);
+#pragma unroll
+        for (int i = 2; i < 16; i += 2) mr = max3(mr, s[i], s[i + 1]);
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mr), __float_as_int(mr), false, false);
+        mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
+        const float cand = mr * sl2;
+        const float mn = cand > m ? cand : m;
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first half
+        m = mn;
+        l0 *= alpha;
+        l1 *= alpha;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          o0[i] *= alpha;
+          o1[i] *= alpha;
+        }
+        exps(-m);
+      }
+      l0 += lb0;
+      l1 += lb1;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        // O^T += V^T . P^T for this k-step: V^T columns 32 t + 16 ks + 8 hh + 0..7 are logical chunk 2 (2 t + ks) + hh.
+        const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(vp + rd[2 * t + ks]);
+        const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(vp + rd[2 * t + ks] + 32 * kRow * 2);
+        o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pb[ks], o0, 0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pb[ks], o1, 0, 0, 0);
       }
     }
+  };
+  using Full = std::false_type;
+  using Partial = std::true_type;
+
+  // Full block blk from (Ks, Vt) while full block blk + 1 is staged into (nK, nV).
+  auto full_step = [&](int blk, const uint16_t* Ks, const uint16_t* Vt, uint16_t* nK, uint16_t* nV) __attribute__((always_inline)) {
+    stage_issue(blk + 1, nK, nV);
+    compute(Full{}, Ks, Vt, blk * kKB);
+    stage_commit(nK, nV);
     wait_vmem();
     __syncthreads();
   };
-  for (int blk = 0; blk < nblocks; blk += 2) {
-    iteration(blk, sK0, sV0, sK1, sV1);
-    if (blk + 1 < nblocks) iteration(blk + 1, sK1, sV1, sK0, sV0);
+
+  if (nfull > 0) {
+    stage_issue(0, sK0, sV0);
+    stage_commit(sK0, sV0);
+  } else {
+    stage_tail(sK0, sV0);
+  }
+  wait_vmem();
+  __syncthreads();
+  int blk = 0;
+  for (; blk + 2 < nfull; blk += 2) {
+    full_step(blk, sK0, sV0, sK1, sV1);
+    full_step(blk + 1, sK1, sV1, sK0, sV0);
+  }
+  if (blk + 1 < nfull) {
+    full_step(blk, sK0, sV0, sK1, sV1);
+    ++blk;
+  }
+  // blk is the last full block (or 0 with no full block); its tiles are the ones of its parity.
+  {
+    const bool odd = blk & 1;
+    uint16_t* cK = odd ? sK1 : sK0;
+    uint16_t* cV = odd ? sV1 : sV0;
+    uint16_t* nK = odd ? sK0 : sK1;
+    uint16_t* nV = odd ? sV0 : sV1;
+    if (nfull > 0) {
+      compute(Full{}, cK, cV, blk * kKB);
+      if (tail) {
+        stage_tail(nK, nV);
+        wait_vmem();
+        __syncthreads();
+        compute(Partial{}, nK, nV, nfull * kKB);
+      }
+    } else {
+      compute(Partial{}, cK, cV, 0);
+    }
   }
 
   float lsum = l0 + l1;
@@ -573,23 +665,26 @@ extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void
   const int64_t grid = static_cast<int64_t>(p.q_tiles) * H * B;
   SVHIP_REQUIRE(grid < (1ll << 31), "%s: grid too large", name);
   // Direct-to-LDS staging: bf16 K and V^T of the padded layout whose rows (and every 8-key run of V^T) start on
-  // 16-byte boundaries.
+  // 16-byte boundaries, whose byte offsets from a (window, head) base fit 32 bits.
   const bool direct = !fp8 && vt && !cu_seqlens && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_d % 8 == 0 &&
-                      sv_h % 8 == 0 && sv_b % 8 == 0;
+                      sv_h % 8 == 0 && sv_b % 8 == 0 && (kv_cap * sk_k + D) * 2 < (1ll << 32) &&
+                      (D * sv_d + kv_cap) * 2 < (1ll << 32);
   hipStream_t s = as_stream(stream);
   const unsigned g = static_cast<unsigned>(grid);
   if (fp8) {
     if (vt) {
-      xattn_fwd_kernel<true, true, false><<<g, kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<true, true, kRegister><<<g, kThreads, 0, s>>>(p);
     } else {
-      xattn_fwd_kernel<true, false, false><<<g, kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<true, false, kRegister><<<g, kThreads, 0, s>>>(p);
     }
+  } else if (direct && D == kDPad) {
+    xattn_fwd_kernel<false, true, kDirect64><<<g, kThreads, 0, s>>>(p);
   } else if (direct) {
-    xattn_fwd_kernel<false, true, true><<<g, kThreads, 0, s>>>(p);
+    xattn_fwd_kernel<false, true, kDirect><<<g, kThreads, 0, s>>>(p);
   } else if (vt) {
-    xattn_fwd_kernel<false, true, false><<<g, kThreads, 0, s>>>(p);
+    xattn_fwd_kernel<false, true, kRegister><<<g, kThreads, 0, s>>>(p);
   } else {
-    xattn_fwd_kernel<false, false, false><<<g, kThreads, 0, s>>>(p);
+    xattn_fwd_kernel<false, false, kRegister><<<g, kThreads, 0, s>>>(p);
   }
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;

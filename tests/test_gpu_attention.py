@@ -207,3 +207,25 @@ def test_transposed_v_padded_layout_fast_path(dev, D):
     torch.cuda.synchronize()
     check(out_direct, ref, BF16_ATOL, BF16_RTOL)
     assert torch.equal(out_direct, out_rows)
+
+
+@pytest.mark.parametrize('transposed', [True, False])
+def test_score_scale_jumps_between_key_halves(dev, transposed):
+    """Score magnitudes that jump up and down between 32-key halves (K rows scaled by 1 .. 90 and down to 1e-3):
+    the running max must be raised mid-window (after lower halves) and hold through much lower halves, on the
+    direct (V^T) and the register-staged path; the windows end inside a half, on a half and inside a block."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, kcap, D = 3, 2, 96, 640, 64
+    lengths = [640, 333, 47]
+    _case(f'xattn score jumps transposed={transposed} lengths={lengths}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=29)
+    factors = torch.tensor([1.0, 30.0, 0.01, 90.0, 2.0, 0.3, 60.0, 0.001])
+    half = torch.arange(kcap) // 32
+    k = (k.float() * factors[half % 8][None, None, :, None]).to(torch.bfloat16)
+    ref = A.cross_attention(q, k, v, lengths)
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    vv = v.transpose(2, 3).contiguous().to(dev).transpose(2, 3) if transposed else v.to(dev)
+    out = attention(q.to(dev), k.to(dev), vv, lengths=lt)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    check(out, ref, BF16_ATOL, BF16_RTOL)
