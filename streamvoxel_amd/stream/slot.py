@@ -1,0 +1,342 @@
+"""Low-entropy-last window slots on the HIP selection kernels.
+
+Reference counterparts: `ForwardBudget` and `LowEntropyLastSlot` (streamvoxel/stream/slot.py:12-176),
+`FastLowEntropyLastSlot`, `SelectGraphs` and `consume_batch` (streamvoxel/stream/fast_ops.py:481-642). The
+constructors, methods, phases, host records and random streams are the reference's: the block order is
+`randperm(blocks)` on a generator seeded `seed + 9173`, and the only draws on the sample generator are the
+categorical samples of the solid steps, one per chosen voxel in ascending flat (YZX) order. A trajectory therefore
+equals the reference's on the same device and torch build whenever the selection masks are equal.
+
+The device work of a window:
+  * marking forward: `svhip_air_prob` and `svhip_lel_update` (column mode) into the deferred mask, one host read
+    of its count (the reference's `int(last.sum())`, stream/slot.py:130);
+  * solid forward: `svhip_ease_select` (entropy, selectable = unfilled & not deferred, block-quota selection, the
+    `bad` flag) into static buffers, capturable in a graph; then the eager tail the reference keeps in torch
+    (`nonzero_static` -> softmax -> multinomial -> `index_copy_`, fast_ops.py:548-553) and one pinned D2H copy;
+  * finish: the deferred voxels are written as `air_token`.
+"""
+from __future__ import annotations
+
+import torch
+
+from streamvoxel_amd import _lib
+from streamvoxel_amd.sampling.block_quota import QuotaWorkspace, block_view
+from streamvoxel_amd.sampling.low_entropy_last import low_entropy_last_quotas
+from streamvoxel_amd.sampling.schedule import actual_time
+
+ORDER_SEED_OFFSET = 9173
+
+
+class ForwardBudget:
+    """Forward counting of one window (stream/slot.py:12-47): the marking forward, then one forward per solid quota.
+    `arm(total)` sets the whole-window count including the marking forward; `forward()` returns True on the forward
+    that finishes the window."""
+
+    def __init__(self):
+        self.phase = 'idle'
+        self.solid = 0
+        self.left = 0
+        self.nfe = 0
+
+    def arm(self, total):
+        total = int(total)
+        if total < 1:
+            raise ValueError('A window needs at least the marking forward')
+        self.phase = 'marking'
+        self.solid = total - 1
+        self.left = 0
+        self.nfe = 0
+
+    def forward(self):
+        if self.phase == 'idle':
+            return False
+        self.nfe += 1
+        if self.phase == 'marking':
+            self.phase = 'solid'
+            self.left = self.solid
+        else:
+            self.left -= 1
+        if self.left == 0:
+            self.phase = 'idle'
+            return True
+        return False
+
+
+def _class_major(logits, classes, total):
+    """(tensor, dtype code, stride_c, stride_n) of [C, Y, Z, X] logits as the kernels read them ([C, N] with any
+    class stride). Logits that do not flatten without a copy, or in another float type, are made so on the device."""
+    if logits.dtype not in (torch.float32, torch.bfloat16):
+        logits = logits.float()
+    x = logits.reshape(classes, total)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    return x, _lib.dtype_code(x.dtype), x.stride(0), x.stride(1)
+
+
+class LowEntropyLastSlot:
+    """One window of `shape` ([Y,Z,X]) inside a batched forward (stream/slot.py:50-176, with the solid steps of
+    `FastLowEntropyLastSlot`, fast_ops.py:481-581). `entropy` names the score kernel; only 'hip' exists here.
+    `keep_scores=True` also leaves each solid step's fp32 scores in `self.scores` (for checking)."""
+
+    def __init__(self, shape, classes, air_ids, air_token, last_eps, block_size, device, entropy='hip',
+                 keep_scores=False):
+        if entropy != 'hip':
+            raise ValueError("entropy must be 'hip' (the HIP entropy kernel)")
+        self.shape = tuple(int(s) for s in shape)
+        if len(self.shape) != 3:
+            raise ValueError('shape is [Y, Z, X]')
+        self.total = self.shape[0] * self.shape[1] * self.shape[2]
+        self.classes = int(classes)
+        self.air_ids = tuple(int(a) for a in air_ids)
+        self.air_token = int(air_token)
+        self.last_eps = float(last_eps)
+        self.block_size = int(block_size)
+        self.device = torch.device(device)
+        if self.device.type != 'cuda':
+            raise RuntimeError('LowEntropyLastSlot runs on the GPU; there is no CPU path')
+        b = self.block_size
+        if any(s % b for s in self.shape):
+            raise ValueError(f'shape {self.shape} is not a multiple of block_size {b}')
+        self.entropy_name = entropy
+        self.phase = 'idle'
+        self.target = self.seed = self.cap = None
+        self.last = None
+        self.quotas = None
+        self.solid_calls = self.actual = self.nfe = self.last_count = 0
+        self.order = self.generator = None
+        self.step_map = torch.zeros(self.shape, dtype=torch.int16)
+        self.values = torch.full(self.shape, -1, dtype=torch.int16)
+        blocks = self.total // b ** 3
+        dev = self.device
+        # Static buffers at fixed addresses, so a captured `select` stays valid across windows.
+        self.last_static = torch.zeros(self.shape, dtype=torch.bool, device=dev)
+        self.n_total = torch.zeros(blocks, dtype=torch.int64, device=dev)
+        self.pos = torch.zeros(blocks, dtype=torch.int64, device=dev)
+        self.k = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.committed = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.frac = torch.zeros(1, dtype=torch.float64, device=dev)
+        self.chosen = torch.zeros(self.shape, dtype=torch.bool, device=dev)
+        self.bad = torch.zeros(1, dtype=torch.bool, device=dev)
+        self.scores = torch.zeros(self.shape, dtype=torch.float32, device=dev) if keep_scores else None
+        self.air_index = torch.as_tensor(self.air_ids, dtype=torch.int32, device=dev)
+        self.air_p = torch.zeros(self.shape, dtype=torch.float32, device=dev)
+        self.workspace = QuotaWorkspace(1, self.shape, b, dev, fused=True)
+        self._bound = False
+        self._host = torch.empty(2 * self.total + 1, dtype=torch.int64, pin_memory=True)
+
+    @property
+    def idle(self):
+        return self.phase == 'idle'
+
+    def arm(self, seed, cap, target):
+        """stream/slot.py:86-103."""
+        self.phase = 'marking'
+        self.seed = int(seed)
+        self.cap = int(cap)
+        self.target = tuple(target)
+        self.nfe = self.actual = self.solid_calls = self.last_count = 0
+        self.quotas = None
+        self.last = torch.zeros(self.shape, dtype=torch.bool, device=self.device)
+        blocks = self.total // self.block_size ** 3
+        order_rng = torch.Generator(device=self.device).manual_seed(self.seed + ORDER_SEED_OFFSET)
+        self.order = torch.randperm(blocks, device=self.device, generator=order_rng)
+        self.generator = torch.Generator(device=self.device).manual_seed(self.seed)
+        self.step_map = torch.zeros(self.shape, dtype=torch.int16)
+        self.values = torch.full(self.shape, -1, dtype=torch.int16)
+        self._bound = False
+
+    def drop(self):
+        self.phase = 'idle'
+        self.target = None
+        self.quotas = None
+
+    def time(self, tokens=None):
+        """Masked fraction mapped to model time; solid steps commit exactly their quota, so no device read."""
+        if self.phase == 'idle':
+            return 1.0
+        committed = sum(self.quotas[:self.solid_calls]) if self.quotas else 0
+        return actual_time((self.total - committed) / self.total)
+
+    def stageable(self):
+        return self.phase == 'solid' and self.quotas is not None and self.solid_calls < len(self.quotas)
+
+    # -- marking ---------------------------------------------------------------------------------------------------
+
+    def _mark(self, logits, tokens):
+        """The marking forward (stream/slot.py:124-135): air probability, then the top run of clean voxels of every
+        (z, x) column joins the deferred set."""
+        x, code, sc, sn = _class_major(logits, self.classes, self.total)
+        lib = _lib.load()
+        stream = _lib.stream_of(x)
+        _lib.check(lib.svhip_air_prob(_lib.ptr(x), code, 1, self.classes, self.total, 0, sc, sn,
+                                      _lib.ptr(self.air_index), int(self.air_index.numel()),
+                                      _lib.ptr(self.air_p), stream), 'svhip_air_prob')
+        Y, Z, X = self.shape
+        _lib.check(lib.svhip_lel_update(_lib.ptr(self.last.view(torch.uint8)), None, _lib.ptr(self.air_p), None,
+                                        self.last_eps, _lib.SVHIP_LEL_COLUMN, 1, Y, Z, X, stream),
+                   'svhip_lel_update')
+        self.last_count = int(self.last.sum())
+        self.quotas = low_entropy_last_quotas(self.total, self.cap, self.last_count, 'quartercos')
+        self.phase = 'solid'
+        self.solid_calls = 0
+
+    # -- solid steps -----------------------------------------------------------------------------------------------
+
+    def prepare(self):
+        """Per-step scalars (device fills, no H2D copy) and, once per window, the deferred mask and the block
+        constants (fast_ops.py:519-532). Returns k."""
+        k = self.quotas[self.solid_calls]
+        committed = sum(self.quotas[:self.solid_calls])
+        if not self._bound:
+            self.last_static.copy_(self.last)
+            self.n_total.copy_(block_view((~self.last).contiguous(), self.block_size).sum(1))
+            self.pos[self.order] = torch.arange(len(self.order), device=self.device)
+            self._bound = True
+        self.k.fill_(k)
+        self.committed.fill_(committed)
+        self.frac.fill_((committed + k) / (self.total - self.last_count))
+        return k
+
+    def select(self, logits, tokens):
+        """Graph-capturable (fast_ops.py:534-540): reads logits [C,Y,Z,X], tokens [Y,Z,X] int64 and the static
+        buffers; writes `chosen` and `bad` (and `scores` when kept). One fused kernel sequence, no host sync."""
+        _lib.require_gpu(logits, tokens)
+        if tokens.dtype != torch.int64 or tokens.shape != self.shape or not tokens.is_contiguous():
+            raise ValueError('tokens must be a contiguous int64 [Y, Z, X] buffer')
+        x, code, sc, sn = _class_major(logits, self.classes, self.total)
+        Y, Z, X = self.shape
+        lib = _lib.load()
+        _lib.check(lib.svhip_ease_select(
+            _lib.ptr(x), code, self.classes, self.classes * self.total, sc, sn, _lib.ptr(tokens), self.classes,
+            _lib.ptr(self.last_static.view(torch.uint8)), 1, Y, Z, X, self.block_size, _lib.ptr(self.k),
+            _lib.ptr(self.pos), _lib.ptr(self.frac), _lib.ptr(self.n_total), _lib.ptr(self.committed),
+            _lib.ptr(self.chosen.view(torch.uint8)), _lib.ptr(self.bad.view(torch.uint8)), _lib.ptr(self.scores),
+            _lib.ptr(self.workspace.buffer), self.workspace.buffer.numel(), _lib.stream_of(x)), 'svhip_ease_select')
+
+    def stage(self, logits, tokens, graph=None):
+        """Selection (eager, or a replay of `graph`, a captured `select`), then the eager tail; no host wait.
+        Returns the handle `collect` takes (fast_ops.py:542-558)."""
+        k = self.prepare()
+        if graph is None:
+            self.select(logits, tokens)
+        else:
+            graph.replay()
+        index = torch.nonzero_static(self.chosen.reshape(-1), size=k).squeeze(1)
+        probabilities = logits.reshape(self.classes, -1).index_select(1, index).t().contiguous().float().softmax(-1)
+        values = torch.multinomial(probabilities, 1, generator=self.generator).squeeze(-1)
+        tokens.view(-1).index_copy_(0, index, values)
+        host = self._host[:2 * k + 1]
+        host.copy_(torch.cat((index, values, self.bad.long())), non_blocking=True)
+        event = torch.cuda.Event()
+        event.record()
+        return k, host, event, tokens
+
+    def collect(self, staged):
+        """Wait for the step's copy and do the host bookkeeping (fast_ops.py:560-575)."""
+        k, host, event, tokens = staged
+        event.synchronize()
+        if int(host[2 * k]):
+            raise AssertionError('low-entropy-last solid step did not meet its quota')
+        positions = host[:k].clone()
+        values_cpu = host[k:2 * k].to(torch.int16)
+        self.solid_calls += 1
+        self.actual += 1
+        self.nfe += 1
+        self.step_map.reshape(-1)[positions] = self.nfe
+        self.values.reshape(-1)[positions] = values_cpu
+        commit = dict(positions=positions.numpy().astype('int32'), values=values_cpu.numpy(), step=int(self.nfe))
+        if self.solid_calls >= len(self.quotas):
+            return self._finish(tokens), commit
+        return None, commit
+
+    def consume(self, logits, tokens):
+        """One forward for this slot (stream/slot.py:117-164). `tokens` [Y,Z,X] int64 is updated in place, `logits`
+        is [C,Y,Z,X]. Returns (finish record or None, commit or None)."""
+        if self.phase == 'idle':
+            return None, None
+        if self.phase == 'marking':
+            self.nfe += 1
+            self._mark(logits, tokens)
+            if not self.quotas:
+                return self._finish(tokens), None
+            return None, None
+        if not self.stageable():
+            return self._finish(tokens), None
+        return self.collect(self.stage(logits, tokens))
+
+    def _finish(self, tokens):
+        """stream/slot.py:166-176: the deferred voxels become `air_token`; the window record."""
+        tokens[self.last] = self.air_token
+        last_cpu = self.last.cpu()
+        self.step_map[last_cpu] = self.nfe
+        self.values[last_cpu] = self.air_token
+        record = dict(target=self.target, seed=self.seed, cap=self.cap, nfe=int(self.nfe), actual=int(self.actual),
+                      last_count=int(self.last_count), last_frac=float(self.last_count) / self.total,
+                      step_map=self.step_map.clone(), values=self.values.clone())
+        self.phase = 'idle'
+        self.target = None
+        return record
+
+
+# The solid steps above already run the fast (staged, capturable) path; the reference's name for that class.
+FastLowEntropyLastSlot = LowEntropyLastSlot
+
+
+class SelectGraphs:
+    """One captured `select` per (bucket, slot) over an engine's static outputs and token rows
+    (fast_ops.py:584-623). `engine` provides `device`, `graphs` (non-empty once captured), `outputs`
+    ({bucket size: logits [size, C, Y, Z, X]}) and `tokens` ([slots, Y, Z, X] int64). `lookup(logits)` returns the
+    bucket whose output tensor `logits` is, or None (eager logits then select eagerly)."""
+
+    def __init__(self, engine, slots):
+        self.engine, self.slots = engine, slots
+        self.graphs = {}
+        if not getattr(engine, 'graphs', None):
+            return
+        device = engine.device
+        current = torch.cuda.current_stream(device)
+        warm = torch.cuda.Stream(device=device)
+        warm.wait_stream(current)
+        with torch.cuda.stream(warm), torch.inference_mode():
+            for size, out in engine.outputs.items():
+                for i in range(size):
+                    slots[i].select(out[i], engine.tokens[i])
+        current.wait_stream(warm)
+        torch.cuda.synchronize(device)
+        stream = torch.cuda.Stream(device=device)
+        pool = torch.cuda.graph_pool_handle()
+        with torch.inference_mode():
+            for size, out in sorted(engine.outputs.items()):
+                for i in range(size):
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, pool=pool, stream=stream, capture_error_mode='thread_local'):
+                        slots[i].select(out[i], engine.tokens[i])
+                    self.graphs[size, i] = graph
+        for slot in slots:
+            slot.chosen.zero_()
+            slot.bad.zero_()
+
+    def lookup(self, logits):
+        for size, out in self.engine.outputs.items():
+            if logits.data_ptr() == out.data_ptr() and len(logits) == len(out):
+                return size
+        return None
+
+
+def consume_batch(slots, logits, tokens, count, graphs=None):
+    """`[slot.consume(logits[i], tokens[i]) for i < count]` with every staged solid step enqueued before the first
+    host wait (fast_ops.py:626-642). Returns {index: (finished, commit)} for the non-idle slots."""
+    size = graphs.lookup(logits) if graphs is not None else None
+    staged, results = {}, {}
+    for index in range(count):
+        slot = slots[index]
+        if slot.idle:
+            continue
+        if slot.stageable():
+            graph = graphs.graphs.get((size, index)) if size is not None else None
+            staged[index] = slot.stage(logits[index], tokens[index], graph)
+        else:
+            results[index] = slot.consume(logits[index], tokens[index])
+    for index, item in staged.items():
+        results[index] = slots[index].collect(item)
+    return dict(sorted(results.items()))
