@@ -125,6 +125,40 @@ int svhip_xattn_fwd(const void* q, const void* k, const void* v, void* o, int kv
                     int64_t sk_h, int64_t sk_k, int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d,
                     int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream);
 
+/*
+ * AxialRoPE of bf16 activations: x [B,H,N,D] (element (b,h,n,d) at b*sx_b + h*sx_h + n*sx_n + d) -> out (same
+ * shape, own strides; out may equal x). D, a multiple of 6, splits into three axes of D/3; in axis t the pair
+ * (x[2i], x[2i+1]) (i < D/6 within the axis) turns by phase = positions[b,n,t] * freq[i] (fp32, positions element
+ * (b,n,t) at b*sp_b + n*sp_n + t). sin/cos are rounded to bf16 and every product and sum to bf16, in the order of
+ * the reference module. freq: fp32 [D/6], the module's `frequencies` buffer (base^(-2i/(D/3))).
+ * Replaces: AxialRoPE.forward (streamvoxel/models/unconditional_md4.py:18-24) as used by cross_query and local_kv
+ * (streamvoxel/stream/fast_ops.py:90-101) and RotaryCrossAttention.encode_kv
+ * (streamvoxel/models/streaming_controlnet.py:31-35).
+ */
+int svhip_axial_rope(const void* x, void* out, const float* positions, const float* freq, int64_t B, int64_t H,
+                     int64_t N, int64_t D, int64_t sx_b, int64_t sx_h, int64_t sx_n, int64_t so_b, int64_t so_h,
+                     int64_t so_n, int64_t sp_b, int64_t sp_n, void* stream);
+
+/*
+ * One window of the cached cross-attention context: keys [0, P) from the prefix bank (bf16 [H,P,D], rows
+ * spk_l / spv_l apart, heads spk_h / spv_h apart; already rotated), keys [P, P+L) from the local projection (bf16
+ * [H,L,D]; K rotated by AxialRoPE at positions [L,3] fp32 (rows sp_l apart) when positions is not NULL, with freq
+ * as for svhip_axial_rope), zeros for keys [P+L, kv_cap). Written to the window's cache: K element (h,j,d) at
+ * h*sck_h + j*sck_k + d; V at h*scv_h + j*scv_k + d*scv_d with scv_d == 1 (rows) or scv_k == 1 (transposed, keys
+ * contiguous). kv_dtype SVHIP_BF16, or SVHIP_FP8_E4M3: per-head scales k_scale/v_scale [H] = max(amax/448, 1e-12)
+ * over the window's keys are written and the codes are round-to-nearest-even e4m3fn of x / scale; the e4m3 form
+ * needs a workspace of svhip_kv_write_workspace_bytes(H, kv_cap) bytes.
+ * Replaces: FastSlotForward.encode + _write (streamvoxel/stream/fast_ops.py:228-250, local_kv :90-95) and the
+ * per-head amax/448 e4m3 quantisation of the cached K/V (scripts/bench_ops.py:506-522).
+ */
+size_t svhip_kv_write_workspace_bytes(int64_t H, int64_t kv_cap);
+int svhip_kv_write(const void* prefix_k, const void* prefix_v, int64_t P, int64_t spk_h, int64_t spk_l,
+                   int64_t spv_h, int64_t spv_l, const void* local_k, const void* local_v, int64_t L, int64_t slk_h,
+                   int64_t slk_l, int64_t slv_h, int64_t slv_l, const float* positions, int64_t sp_l,
+                   const float* freq, int64_t H, int64_t D, void* cache_k, int64_t sck_h, int64_t sck_k,
+                   void* cache_v, int64_t scv_h, int64_t scv_k, int64_t scv_d, int64_t kv_cap, int kv_dtype,
+                   float* k_scale, float* v_scale, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

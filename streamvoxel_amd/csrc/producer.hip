@@ -1,0 +1,344 @@
+// Producers of the cross-attention operands.
+//
+//  * svhip_axial_rope: AxialRoPE (models/unconditional_md4.py:10-24) on bf16 activations. head_dim D splits into
+//    three axes of D/3; inside an axis the adjacent pairs (a, b) = (x[2i], x[2i+1]) turn by the phase
+//    pos[axis] * freq[i]. The arithmetic follows the reference under bf16 autocast step by step: the phase is one
+//    fp32 product, sin and cos are fp32 and rounded to bf16, and each product and each sum of
+//    (a cos - b sin, a sin + b cos) is rounded to bf16 (fp32 operation, then round to nearest even).
+//  * svhip_kv_write: one window of the cached context (stream/fast_ops.py:228-250): keys [0, P) from the prefix
+//    bank (already rotated), keys [P, P + L) from the local projection (K rotated at the local positions when
+//    positions are given), zeros up to the capacity; K as rows [H, Kcap, D], V as rows or transposed
+//    [H, D, Kcap]. bf16, or OCP e4m3fn with per-head scales amax / 448 (clamped below at 1e-12) over the window's
+//    keys and codes round-to-nearest-even of x / scale.
+//
+// HBM-bound, once per window (K/V) or once per layer and step (Q); one thread per bf16 pair.
+#include "common.hpp"
+
+namespace svhip {
+
+constexpr int kTileKeys = 64;
+constexpr int kProducerThreads = 256;
+constexpr int kMaxHeadDim = 128;
+
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float bf16_round(float f) { return bf16_bits_to_float(bf16_rne(f)); }
+
+// OCP e4m3fn (bias 7, 3 mantissa bits, no infinities, S.1111.111 = NaN, largest finite 448, quantum 2^-9 below
+// 2^-6), round to nearest even. Magnitudes above 464 (half way between 448 and the NaN code's 480) and NaN give
+// the NaN code.
+__device__ __forceinline__ uint8_t e4m3fn_rne(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint8_t sign = static_cast<uint8_t>((u >> 24) & 0x80u);
+  const float a = __uint_as_float(u & 0x7fffffffu);
+  if (!(a <= 464.0f)) return sign | 0x7fu;
+  if (a < 0.015625f) {
+    // Subnormal range (and the rounding up into 2^-6): m * 2^-9, m = rne(a * 512) in 0..8; m = 8 is the smallest
+    // normal, whose code (exponent 1, mantissa 0) is 8 as well.
+    return sign | static_cast<uint8_t>(__builtin_rintf(a * 512.0f));
+  }
+  const uint32_t au = u & 0x7fffffffu;
+  int e = static_cast<int>(au >> 23) - 127;  // -6 .. 8
+  const uint32_t mant = au & 0x7fffffu;
+  uint32_t m = mant >> 20;
+  const uint32_t rest = mant & 0xfffffu;
+  if (rest > 0x80000u || (rest == 0x80000u && (m & 1u))) ++m;
+  if (m == 8u) {
+    m = 0u;
+    ++e;
+  }
+  return sign | static_cast<uint8_t>(((e + 7) << 3) | static_cast<int>(m));
+}
+
+// One rotated pair: (a, b) at phase p.
+__device__ __forceinline__ void rope_pair(float a, float b, float p, float& ra, float& rb) {
+  const float s = bf16_round(sinf(p));
+  const float c = bf16_round(cosf(p));
+  ra = bf16_round(bf16_round(a * c) - bf16_round(b * s));
+  rb = bf16_round(bf16_round(a * s) + bf16_round(b * c));
+}
+
+__device__ __forceinline__ void unpack2(uint32_t w, float& a, float& b) {
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return static_cast<uint32_t>(bf16_rne(a)) | (static_cast<uint32_t>(bf16_rne(b)) << 16);
+}
+
+struct RopeArgs {
+  const uint16_t* x;
+  uint16_t* out;
+  const float* pos;
+  const float* freq;
+  int64_t B, H, N, D;
+  int64_t sxb, sxh, sxn;
+  int64_t sob, soh, son;
+  int64_t spb, spn;
+};
+
+__global__ __launch_bounds__(kProducerThreads) void axial_rope_kernel(RopeArgs a) {
+  const int64_t pairs = a.D / 2;
+  const int64_t per_axis = a.D / 6;  // pairs per axis = number of frequencies
+  const int64_t total = a.B * a.H * a.N * pairs;
+  for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t pr = t % pairs;
+    int64_t r = t / pairs;
+    const int64_t n = r % a.N;
+    r /= a.N;
+    const int64_t h = r % a.H;
+    const int64_t b = r / a.H;
+    const int64_t axis = pr / per_axis, i = pr - axis * per_axis;
+    const float phase = a.pos[b * a.spb + n * a.spn + axis] * a.freq[i];
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(a.x + b * a.sxb + h * a.sxh + n * a.sxn + 2 * pr);
+    float x0, x1, r0, r1;
+    unpack2(w, x0, x1);
+    rope_pair(x0, x1, phase, r0, r1);
+    *reinterpret_cast<uint32_t*>(a.out + b * a.sob + h * a.soh + n * a.son + 2 * pr) = pack2(r0, r1);
+  }
+}
+
+struct KvArgs {
+  const uint16_t *pk, *pv;  // prefix [H, P, D]
+  int64_t P, spk_h, spk_l, spv_h, spv_l;
+  const uint16_t *lk, *lv;  // local [H, L, D]
+  int64_t L, slk_h, slk_l, slv_h, slv_l;
+  const float* pos;  // [L, 3] or null
+  int64_t sp_l;
+  const float* freq;
+  int64_t H, D, kcap;
+  void* ck;
+  int64_t sck_h, sck_k;
+  void* cv;
+  int64_t scv_h, scv_k, scv_d;
+  float *k_scale, *v_scale;  // [H] (e4m3)
+  float* partial;            // [H, tiles, 2] (e4m3)
+  int64_t tiles;
+};
+
+// K and V pair `pr` of key j of head h (zeros past the window's keys; local K rotated when positions are given).
+__device__ __forceinline__ void load_pair(const KvArgs& a, int64_t h, int64_t j, int64_t pr, float& k0, float& k1,
+                                          float& v0, float& v1) {
+  k0 = k1 = v0 = v1 = 0.f;
+  if (j < a.P) {
+    unpack2(*reinterpret_cast<const uint32_t*>(a.pk + h * a.spk_h + j * a.spk_l + 2 * pr), k0, k1);
+    unpack2(*reinterpret_cast<const uint32_t*>(a.pv + h * a.spv_h + j * a.spv_l + 2 * pr), v0, v1);
+  } else if (j < a.P + a.L) {
+    const int64_t l = j - a.P;
+    unpack2(*reinterpret_cast<const uint32_t*>(a.lk + h * a.slk_h + l * a.slk_l + 2 * pr), k0, k1);
+    unpack2(*reinterpret_cast<const uint32_t*>(a.lv + h * a.slv_h + l * a.slv_l + 2 * pr), v0, v1);
+    if (a.pos) {
+      const int64_t per_axis = a.D / 6;
+      const int64_t axis = pr / per_axis, i = pr - axis * per_axis;
+      float r0, r1;
+      rope_pair(k0, k1, a.pos[l * a.sp_l + axis] * a.freq[i], r0, r1);
+      k0 = r0;
+      k1 = r1;
+    }
+  }
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < kProducerThreads / 64; ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+// e4m3 only: per (head, 64-key tile) max |K| and max |V| of the window's keys.
+__global__ __launch_bounds__(kProducerThreads) void kv_stats_kernel(KvArgs a) {
+  __shared__ float red[kProducerThreads / 64];
+  const int64_t h = blockIdx.y, tile = blockIdx.x;
+  const int64_t pairs = a.D / 2;
+  float mk = 0.f, mv = 0.f;
+  for (int64_t e = threadIdx.x; e < kTileKeys * pairs; e += kProducerThreads) {
+    const int64_t j = tile * kTileKeys + e / pairs;
+    if (j >= a.P + a.L) continue;
+    float k0, k1, v0, v1;
+    load_pair(a, h, j, e % pairs, k0, k1, v0, v1);
+    mk = fmaxf(mk, fmaxf(fabsf(k0), fabsf(k1)));
+    mv = fmaxf(mv, fmaxf(fabsf(v0), fabsf(v1)));
+  }
+  mk = block_max(mk, red);
+  mv = block_max(mv, red);
+  if (threadIdx.x == 0) {
+    a.partial[(h * a.tiles + tile) * 2] = mk;
+    a.partial[(h * a.tiles + tile) * 2 + 1] = mv;
+  }
+}
+
+template <bool FP8, bool VT>
+__global__ __launch_bounds__(kProducerThreads) void kv_write_kernel(KvArgs a) {
+  __shared__ float red[kProducerThreads / 64];
+  // V^T staging: [d][key] of one tile, in output element bytes.
+  __shared__ __attribute__((aligned(16))) uint8_t sv[kMaxHeadDim * kTileKeys * (FP8 ? 1 : 2)];
+  const int64_t h = blockIdx.y, tile = blockIdx.x;
+  const int64_t pairs = a.D / 2;
+  float sk = 1.f, svs = 1.f;  // e4m3 scales of K and V
+  if constexpr (FP8) {
+    float mk = 0.f, mv = 0.f;
+    for (int64_t t = threadIdx.x; t < a.tiles; t += kProducerThreads) {
+      mk = fmaxf(mk, a.partial[(h * a.tiles + t) * 2]);
+      mv = fmaxf(mv, a.partial[(h * a.tiles + t) * 2 + 1]);
+    }
+    mk = block_max(mk, red);
+    mv = block_max(mv, red);
+    sk = fmaxf(__fdiv_rn(mk, 448.0f), 1e-12f);
+    svs = fmaxf(__fdiv_rn(mv, 448.0f), 1e-12f);
+    if (tile == 0 && threadIdx.x == 0) {
+      a.k_scale[h] = sk;
+      a.v_scale[h] = svs;
+    }
+  }
+  for (int64_t e = threadIdx.x; e < kTileKeys * pairs; e += kProducerThreads) {
+    const int64_t key = e / pairs, pr = e % pairs;
+    const int64_t j = tile * kTileKeys + key;
+    if (j >= a.kcap) continue;
+    float k0, k1, v0, v1;
+    load_pair(a, h, j, pr, k0, k1, v0, v1);
+    const int64_t kofs = h * a.sck_h + j * a.sck_k + 2 * pr;
+    if constexpr (FP8) {
+      const uint16_t kc = static_cast<uint16_t>(e4m3fn_rne(__fdiv_rn(k0, sk))) |
+                          static_cast<uint16_t>(static_cast<uint16_t>(e4m3fn_rne(__fdiv_rn(k1, sk))) << 8);
+      *reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(a.ck) + kofs) = kc;
+      const uint8_t c0 = e4m3fn_rne(__fdiv_rn(v0, svs)), c1 = e4m3fn_rne(__fdiv_rn(v1, svs));
+      if constexpr (VT) {
+        sv[(2 * pr) * kTileKeys + key] = c0;
+        sv[(2 * pr + 1) * kTileKeys + key] = c1;
+      } else {
+        *reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(a.cv) + h * a.scv_h + j * a.scv_k + 2 * pr) =
+            static_cast<uint16_t>(c0) | static_cast<uint16_t>(static_cast<uint16_t>(c1) << 8);
+      }
+    } else {
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.ck) + kofs) = pack2(k0, k1);
+      if constexpr (VT) {
+        uint16_t* s16 = reinterpret_cast<uint16_t*>(sv);
+        s16[(2 * pr) * kTileKeys + key] = bf16_rne(v0);
+        s16[(2 * pr + 1) * kTileKeys + key] = bf16_rne(v1);
+      } else {
+        *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.cv) + h * a.scv_h + j * a.scv_k + 2 * pr) =
+            pack2(v0, v1);
+      }
+    }
+  }
+  if constexpr (VT) {
+    __syncthreads();
+    // Rows of the transposed tile: consecutive threads write consecutive keys of one head_dim element.
+    for (int64_t e = threadIdx.x; e < a.D * kTileKeys; e += kProducerThreads) {
+      const int64_t d = e / kTileKeys, key = e % kTileKeys;
+      const int64_t j = tile * kTileKeys + key;
+      if (j >= a.kcap) continue;
+      const int64_t vofs = h * a.scv_h + d * a.scv_d + j;
+      if constexpr (FP8) {
+        static_cast<uint8_t*>(a.cv)[vofs] = sv[d * kTileKeys + key];
+      } else {
+        static_cast<uint16_t*>(a.cv)[vofs] = reinterpret_cast<const uint16_t*>(sv)[d * kTileKeys + key];
+      }
+    }
+  }
+}
+
+}  // namespace svhip
+
+using namespace svhip;
+
+extern "C" int svhip_axial_rope(const void* x, void* out, const float* positions, const float* freq, int64_t B,
+                                int64_t H, int64_t N, int64_t D, int64_t sx_b, int64_t sx_h, int64_t sx_n,
+                                int64_t so_b, int64_t so_h, int64_t so_n, int64_t sp_b, int64_t sp_n, void* stream) {
+  const char* name = "svhip_axial_rope";
+  clear_error();
+  SVHIP_REQUIRE(x && out && positions && freq, "%s: null pointer", name);
+  SVHIP_REQUIRE(B >= 0 && H >= 0 && N >= 0, "%s: bad sizes", name);
+  SVHIP_REQUIRE(D >= 6 && D % 6 == 0, "%s: head_dim %lld must be a positive multiple of 6 (three even axes)", name,
+                (long long)D);
+  SVHIP_REQUIRE(reinterpret_cast<uintptr_t>(x) % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 4 == 0 &&
+                    sx_b % 2 == 0 && sx_h % 2 == 0 && sx_n % 2 == 0 && so_b % 2 == 0 && so_h % 2 == 0 &&
+                    so_n % 2 == 0,
+                "%s: rows must start on 4-byte boundaries (head_dim contiguous)", name);
+  const int64_t total = B * H * N * (D / 2);
+  if (total == 0) return SVHIP_OK;
+  RopeArgs a{static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), positions, freq, B, H, N, D,
+             sx_b, sx_h, sx_n, so_b, so_h, so_n, sp_b, sp_n};
+  int64_t grid = cdiv(total, kProducerThreads);
+  if (grid > 65536) grid = 65536;
+  axial_rope_kernel<<<static_cast<unsigned>(grid), kProducerThreads, 0, as_stream(stream)>>>(a);
+  SVHIP_LAUNCHED(name);
+  return SVHIP_OK;
+}
+
+extern "C" size_t svhip_kv_write_workspace_bytes(int64_t H, int64_t kv_cap) {
+  if (H <= 0 || kv_cap < 0) return 0;
+  return static_cast<size_t>(H * cdiv(kv_cap, kTileKeys) * 2) * sizeof(float);
+}
+
+extern "C" int svhip_kv_write(const void* prefix_k, const void* prefix_v, int64_t P, int64_t spk_h, int64_t spk_l,
+                              int64_t spv_h, int64_t spv_l, const void* local_k, const void* local_v, int64_t L,
+                              int64_t slk_h, int64_t slk_l, int64_t slv_h, int64_t slv_l, const float* positions,
+                              int64_t sp_l, const float* freq, int64_t H, int64_t D, void* cache_k, int64_t sck_h,
+                              int64_t sck_k, void* cache_v, int64_t scv_h, int64_t scv_k, int64_t scv_d,
+                              int64_t kv_cap, int kv_dtype, float* k_scale, float* v_scale, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  const char* name = "svhip_kv_write";
+  clear_error();
+  SVHIP_REQUIRE(cache_k && cache_v, "%s: null cache pointer", name);
+  SVHIP_REQUIRE(H >= 1 && D >= 2 && D % 2 == 0 && D <= kMaxHeadDim, "%s: head_dim %lld unsupported (even, <= %d)",
+                name, (long long)D, kMaxHeadDim);
+  SVHIP_REQUIRE(P >= 0 && L >= 0 && kv_cap >= 0 && P + L <= kv_cap, "%s: %lld + %lld keys exceed the capacity %lld",
+                name, (long long)P, (long long)L, (long long)kv_cap);
+  SVHIP_REQUIRE(P == 0 || (prefix_k && prefix_v), "%s: null prefix pointer", name);
+  SVHIP_REQUIRE(L == 0 || (local_k && local_v), "%s: null local pointer", name);
+  SVHIP_REQUIRE(!positions || (freq && D % 6 == 0), "%s: rotation needs frequencies and head_dim a multiple of 6",
+                name);
+  SVHIP_REQUIRE(kv_dtype == SVHIP_BF16 || kv_dtype == SVHIP_FP8_E4M3, "%s: kv dtype %d unsupported", name, kv_dtype);
+  const bool fp8 = kv_dtype == SVHIP_FP8_E4M3;
+  SVHIP_REQUIRE(scv_d == 1 || scv_k == 1, "%s: V needs a unit stride along head_dim or keys", name);
+  const bool vt = scv_k == 1 && scv_d != 1;
+  // 4-byte (bf16) / 2-byte (e4m3) pair accesses.
+  auto even = [](const void* p, int64_t a, int64_t b) {
+    return reinterpret_cast<uintptr_t>(p) % 4 == 0 && a % 2 == 0 && b % 2 == 0;
+  };
+  SVHIP_REQUIRE(P == 0 || (even(prefix_k, spk_h, spk_l) && even(prefix_v, spv_h, spv_l)),
+                "%s: prefix rows must start on 4-byte boundaries", name);
+  SVHIP_REQUIRE(L == 0 || (even(local_k, slk_h, slk_l) && even(local_v, slv_h, slv_l)),
+                "%s: local rows must start on 4-byte boundaries", name);
+  SVHIP_REQUIRE(even(cache_k, sck_h, sck_k) && (vt || even(cache_v, scv_h, scv_k)),
+                "%s: cache rows must start on pair boundaries", name);
+  const int64_t tiles = cdiv(kv_cap, kTileKeys);
+  if (tiles == 0) return SVHIP_OK;
+  if (fp8) {
+    SVHIP_REQUIRE(k_scale && v_scale, "%s: e4m3 needs k_scale and v_scale outputs", name);
+    SVHIP_REQUIRE(workspace && workspace_bytes >= svhip_kv_write_workspace_bytes(H, kv_cap),
+                  "%s: workspace too small (%zu < %zu bytes)", name, workspace_bytes,
+                  svhip_kv_write_workspace_bytes(H, kv_cap));
+  }
+  KvArgs a{static_cast<const uint16_t*>(prefix_k), static_cast<const uint16_t*>(prefix_v), P, spk_h, spk_l, spv_h,
+           spv_l, static_cast<const uint16_t*>(local_k), static_cast<const uint16_t*>(local_v), L, slk_h, slk_l,
+           slv_h, slv_l, positions, sp_l, freq, H, D, kv_cap, cache_k, sck_h, sck_k, cache_v, scv_h, scv_k, scv_d,
+           k_scale, v_scale, static_cast<float*>(workspace), tiles};
+  SVHIP_REQUIRE(tiles < 65536 && H < 65536, "%s: grid too large", name);
+  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(H));
+  hipStream_t s = as_stream(stream);
+  if (fp8) {
+    kv_stats_kernel<<<grid, kProducerThreads, 0, s>>>(a);
+    if (vt) {
+      kv_write_kernel<true, true><<<grid, kProducerThreads, 0, s>>>(a);
+    } else {
+      kv_write_kernel<true, false><<<grid, kProducerThreads, 0, s>>>(a);
+    }
+  } else if (vt) {
+    kv_write_kernel<false, true><<<grid, kProducerThreads, 0, s>>>(a);
+  } else {
+    kv_write_kernel<false, false><<<grid, kProducerThreads, 0, s>>>(a);
+  }
+  SVHIP_LAUNCHED(name);
+  return SVHIP_OK;
+}

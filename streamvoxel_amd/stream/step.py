@@ -42,31 +42,63 @@ class CachedContext:
             self.v_scale = [torch.ones(batch, heads, dtype=torch.float32, device=device) for _ in range(layers)]
         else:
             self.k_scale = self.v_scale = [None] * layers
+        self._kv_ws = None
 
-    def write(self, layer, index, key, value):
-        """key, value [H, L, D] (any float dtype) for window `index` of `layer`; host-side length only."""
-        L = key.shape[1]
-        if L > self.kv_cap:
-            raise ValueError('Condition exceeds the slot capacity')
-        k, vt = self.k[layer], self.vt[layer]
-        if self.kv_dtype == 'fp8':
-            ks = torch.clamp(key.float().abs().amax(dim=(1, 2)) / 448.0, min=1e-12)
-            vs = torch.clamp(value.float().abs().amax(dim=(1, 2)) / 448.0, min=1e-12)
-            self.k_scale[layer][index].copy_(ks)
-            self.v_scale[layer][index].copy_(vs)
-            key = (key.float() / ks[:, None, None]).to(torch.float8_e4m3fn)
-            value = (value.float() / vs[:, None, None]).to(torch.float8_e4m3fn)
-            k[index, :, :L].view(torch.uint8).copy_(key.view(torch.uint8))
-            vt[index, :, :, :L].view(torch.uint8).copy_(value.view(torch.uint8).transpose(1, 2))
-            k[index, :, L:].view(torch.uint8).zero_()
-            vt[index, :, :, L:].view(torch.uint8).zero_()
+    def write(self, layer, index, key, value, prefix=None, positions=None, frequencies=None):
+        """Window `index` of `layer` (FastSlotForward.encode + _write, fast_ops.py:228-250) in one `svhip_kv_write`:
+        keys [0, P) from `prefix` = (prefix_k, prefix_v) [H, P, D] (already rotated, optional), keys [P, P + L)
+        from key, value [H, L, D] (the local projections; K rotated by AxialRoPE at fp32 positions [L, 3] with the
+        fp32 `frequencies` buffer when given), zeros after; an e4m3 cache also gets its per-(window, head) scales.
+        Inputs are taken as bf16 (the reference's autocast dtype). The window's length is set on the host when the
+        last layer is written or the length changes."""
+        dev = self.k[layer].device
+        rows = lambda t: t.to(device=dev, dtype=torch.bfloat16) if t.stride(-1) == 1 else (
+            t.to(device=dev, dtype=torch.bfloat16).contiguous())
+        key, value = rows(key), rows(value)
+        _lib.require_gpu(key, value)
+        H, L, D = key.shape
+        if H != self.heads or D != self.head_dim or value.shape != key.shape:
+            raise ValueError('key / value must be [heads, L, head_dim] like the cache')
+        if prefix is not None:
+            pk, pv = rows(prefix[0]), rows(prefix[1])
+            if pk.shape[0] != H or pk.shape[2] != D or pv.shape != pk.shape:
+                raise ValueError('prefix K / V must be [heads, P, head_dim]')
+            P = pk.shape[1]
         else:
-            k[index, :, :L].copy_(key)
-            vt[index, :, :, :L].copy_(value.transpose(1, 2))
-            k[index, :, L:].zero_()
-            vt[index, :, :, L:].zero_()
-        if layer == self.layers - 1 or self.host_lengths[index] != L:
-            self.set_length(index, L)
+            pk = pv = None
+            P = 0
+        if P + L > self.kv_cap:
+            raise ValueError('Condition exceeds the slot capacity')
+        pos = freq = None
+        if positions is not None:
+            if frequencies is None:
+                raise ValueError('rotating the local keys needs the AxialRoPE frequencies')
+            pos = positions.to(device=dev, dtype=torch.float32).contiguous()
+            freq = frequencies.to(device=dev, dtype=torch.float32).contiguous()
+            if pos.shape != (L, 3):
+                raise ValueError('positions must be [L, 3]')
+        k, vt = self.k[layer][index], self.vt[layer][index]          # [H, Kcap, D], [H, D, Kcap]
+        fp8 = self.kv_dtype == 'fp8'
+        code = _lib.SVHIP_FP8_E4M3 if fp8 else _lib.SVHIP_BF16
+        kc, vc = (k.view(torch.uint8), vt.view(torch.uint8)) if fp8 else (k, vt)
+        lib = _lib.load()
+        ws = None
+        if fp8:
+            nbytes = int(lib.svhip_kv_write_workspace_bytes(H, self.kv_cap))
+            if self._kv_ws is None or self._kv_ws.numel() < nbytes:
+                self._kv_ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            ws = self._kv_ws
+        ks = self.k_scale[layer][index] if fp8 else None
+        vs = self.v_scale[layer][index] if fp8 else None
+        _lib.check(lib.svhip_kv_write(
+            _lib.ptr(pk), _lib.ptr(pv), P, pk.stride(0) if P else 0, pk.stride(1) if P else 0,
+            pv.stride(0) if P else 0, pv.stride(1) if P else 0, _lib.ptr(key), _lib.ptr(value), L, key.stride(0),
+            key.stride(1), value.stride(0), value.stride(1), _lib.ptr(pos), 3, _lib.ptr(freq), H, D, _lib.ptr(kc),
+            kc.stride(0), kc.stride(1), _lib.ptr(vc), vc.stride(0), vc.stride(2), vc.stride(1), self.kv_cap, code,
+            _lib.ptr(ks), _lib.ptr(vs), _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_of(key)),
+            'svhip_kv_write')
+        if layer == self.layers - 1 or self.host_lengths[index] != P + L:
+            self.set_length(index, P + L)
 
     def set_length(self, index, length):
         self.host_lengths[index] = int(length)

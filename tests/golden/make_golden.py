@@ -2,14 +2,16 @@
 
 Run in the build container only (the reference checkout is not present where the tests run):
 
-    python tests/golden/make_golden.py /root/reference
+    python tests/golden/make_golden.py /root/reference [sampling|rope]
 
 It imports the reference's pure-torch sampling functions and slot state machine, on the CPU, for the functions that
 closed forms, brute force and invariants do not pin literally:
   * block_quota_select (streamvoxel/sampling/block_quota.py:20-38) - which voxels, not just how many;
   * counts / low_entropy_last_quotas (streamvoxel/sampling/schedule.py:32-38, low_entropy_last.py:20-33);
   * low_entropy_last_update (streamvoxel/sampling/low_entropy_last.py:8-17) at the fp32 threshold;
-  * LowEntropyLastSlot trajectories (streamvoxel/stream/slot.py:50-176).
+  * LowEntropyLastSlot trajectories (streamvoxel/stream/slot.py:50-176);
+  * AxialRoPE (streamvoxel/models/unconditional_md4.py:10-24) on bf16 activations - the exact bf16 bits, which
+    depend on the module's rounding order.
 Only data is written (inputs and expected outputs); no reference source is copied.
 """
 from __future__ import annotations
@@ -182,21 +184,46 @@ def slot_cases(LowEntropyLastSlot):
         json.dump(meta, f, indent=1)
 
 
-def main(reference):
+def rope_cases(AxialRoPE):
+    """bf16 activations [B,H,N,D] at fp32 patch-centre positions (multiples of 1/8 up to ~300, as the condition
+    builder produces), through the reference module on the CPU."""
+    arrays, meta = {}, []
+    for case, (B, H, N, D, seed) in enumerate([(2, 3, 40, 48, 5), (1, 2, 33, 24, 6), (1, 1, 64, 96, 7)]):
+        g = torch.Generator().manual_seed(seed)
+        x = torch.randn(B, H, N, D, generator=g).to(torch.bfloat16)
+        positions = torch.randint(-64, 2400, (B, N, 3), generator=g).float() / 8
+        module = AxialRoPE(D)
+        out = module(x, positions)
+        name = 'case%d' % case
+        arrays[name + '/x'] = x.view(torch.int16).numpy()
+        arrays[name + '/positions'] = positions.numpy()
+        arrays[name + '/frequencies'] = module.frequencies.numpy()
+        arrays[name + '/out'] = out.view(torch.int16).numpy()
+        meta.append(dict(name=name, shape=[B, H, N, D], seed=seed))
+    np.savez_compressed(os.path.join(HERE, 'axial_rope.npz'), **arrays)
+    with open(os.path.join(HERE, 'axial_rope.json'), 'w') as f:
+        json.dump(meta, f, indent=1)
+
+
+def main(reference, only=None):
     sys.path.insert(0, reference)
     from streamvoxel.sampling.block_quota import block_quota_select, block_view
     from streamvoxel.sampling.low_entropy_last import low_entropy_last_quotas, low_entropy_last_update
     from streamvoxel.sampling.schedule import actual_time, counts
     from streamvoxel.stream.slot import LowEntropyLastSlot
+    from streamvoxel.models.unconditional_md4 import AxialRoPE
     torch.set_num_threads(1)
-    quota_cases(block_view, block_quota_select)
-    schedule_cases(counts, low_entropy_last_quotas, actual_time)
-    lel_cases(low_entropy_last_update)
-    slot_cases(LowEntropyLastSlot)
+    if only in (None, 'sampling'):
+        quota_cases(block_view, block_quota_select)
+        schedule_cases(counts, low_entropy_last_quotas, actual_time)
+        lel_cases(low_entropy_last_update)
+        slot_cases(LowEntropyLastSlot)
+    if only in (None, 'rope'):
+        rope_cases(AxialRoPE)
     with open(os.path.join(HERE, 'provenance.json'), 'w') as f:
         json.dump(dict(torch=torch.__version__, numpy=np.__version__, reference=reference,
                        script='tests/golden/make_golden.py'), f, indent=1)
 
 
 if __name__ == '__main__':
-    main(sys.argv[1] if len(sys.argv) > 1 else '/root/reference')
+    main(sys.argv[1] if len(sys.argv) > 1 else '/root/reference', sys.argv[2] if len(sys.argv) > 2 else None)
