@@ -17,8 +17,8 @@
 // Because O^T's columns are queries too, the per-query rescale and the final 1/l are lane-local.
 //
 // The softmax is VALU-bound at head_dim 64 (one exp per score against 2 x 64 MACs), so per score it costs one
-// fma (scale and max subtraction fused), one exp, half a bf16 pack and half a bf16 dot (the row sum is taken over
-// the packed bf16 P, the same values the second product consumes), and no max:
+// fma (scale and max subtraction fused), one exp, half a bf16 pack and one fp32 add (the row sum; v_dot2c_f32_bf16
+// over the packed P would need half the instructions but does not co-execute with the matrix cores), and no max:
 //   * P is formed against the running max m as it stands. The half's row sum tells whether m still bounds the
 //     half's scores: only a sum above 2^20 (or inf / NaN, as on the first half, where m is -inf) makes the wave
 //     take the half's max (16 three-input maxes and the partner's over v_permlane32_swap), raise m, rescale O
@@ -58,6 +58,7 @@ constexpr int kThreads = 256;
 constexpr float kSumHigh = 1048576.0f;  // 2^20: a half's row sum above it makes the running max be raised
 constexpr float kFltMax = 3.40282347e38f;
 constexpr int kMaxRankWindows = 4096;
+constexpr int kCusPerXcd = 32;  // MI355X: 8 XCDs x 32 CUs
 
 struct XattnParams {
   const void* q;
@@ -294,14 +295,24 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   __shared__ int s_window;
 
   // Workgroup -> (rank, head, query tile): XCD x (= id % 8) takes the (rank, head) units x, x + 8, ... with all
-  // query tiles of a unit back to back. rank 0 is the window with the most keys.
+  // query tiles of a unit back to back. rank 0 is the window with the most keys. An XCD hands its k-th workgroup
+  // to its CU k % 32, so every CU holds one unit's tile from each round of 32 and the rounds go from the longest
+  // units to the shortest; odd rounds take their units in reverse, pairing a CU's long tile of one round with a
+  // short one of the next (a permutation: any placement stays correct, this one only balances the CUs).
   const int64_t wg = blockIdx.x;
   int qt;
   int64_t unit;
   if ((p.B * p.H) % 8 == 0) {
     const int64_t seq = wg >> 3;
     qt = static_cast<int>(seq % p.q_tiles);
-    unit = (wg & 7) + 8 * (seq / p.q_tiles);
+    int64_t k = seq / p.q_tiles;  // the XCD's unit index
+    const int64_t per_round = kCusPerXcd / p.q_tiles;
+    if (kCusPerXcd % p.q_tiles == 0 && per_round > 1) {
+      const int64_t round = k / per_round;
+      const int64_t full_rounds = (p.B * p.H / 8) / per_round;
+      if ((round & 1) && round < full_rounds) k = round * per_round + (per_round - 1 - (k - round * per_round));
+    }
+    unit = (wg & 7) + 8 * k;
   } else {
     qt = static_cast<int>(wg % p.q_tiles);
     unit = wg / p.q_tiles;
@@ -418,7 +429,6 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
     stage_store<FP8, VT>(tmp, sK, sV);
   };
 
-  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
   // One key block from (Ks, Vt), as two 32-key halves that each run the whole online-softmax step (scores,
   // running max, exponentials, second product): a half's scores take 16 registers, which keeps four waves per
@@ -445,8 +455,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
         }
       }
       // P^T = exp2(S^T * scale*log2e - m) against the running max m as it stands, as B operands: k-step ks (keys
-      // 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7. The row sum is taken over the packed bf16 P, the values
-      // the second product consumes.
+      // 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7. The row sum is taken over the fp32 P.
       bf16x8_t pb[2];
       float lb0, lb1;
       auto exps = [&](float neg_m) __attribute__((always_inline)) {
@@ -459,10 +468,13 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
             f32x2_t two = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j], sl2, neg_m)),
                            __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j + 1], sl2, neg_m))};
             const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
+            // Row sum in fp32 adds: v_dot2c_f32_bf16 (the packed alternative) does not co-execute with the
+            // matrix cores on gfx950, and the plain adds do.
+            const float pair = two[0] + two[1];
             if (j & 2) {
-              lb1 = __builtin_amdgcn_fdot2_f32_bf16(c, ones, lb1, false);
+              lb1 += pair;
             } else {
-              lb0 = __builtin_amdgcn_fdot2_f32_bf16(c, ones, lb0, false);
+              lb0 += pair;
             }
             pb[ks][j] = c[0];
             pb[ks][j + 1] = c[1];
