@@ -405,7 +405,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
 
   f32x16_t o0 = {0}, o1 = {0};  // O^T tiles: d in [0,32) and [32,64)
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
-  float l0 = 0.f, l1 = 0.f;     // row-sum partials of this lane's keys
+  float l = 0.f;                // row-sum partial of this lane's keys
 
   // Full block `blk` into (sK, sV): issued now, complete at the next vmem wait (direct) or at `stage_commit`
   // (registers, prefetched into `st`).
@@ -457,10 +457,9 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
       // P^T = exp2(S^T * scale*log2e - m) against the running max m as it stands, as B operands: k-step ks (keys
       // 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7. The row sum is taken over the fp32 P.
       bf16x8_t pb[2];
-      float lb0, lb1;
+      float lb;
       auto exps = [&](float neg_m) __attribute__((always_inline)) {
-        lb0 = 0.f;
-        lb1 = 0.f;
+        float pair[8];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -468,25 +467,21 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
             f32x2_t two = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j], sl2, neg_m)),
                            __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j + 1], sl2, neg_m))};
             const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
-            // Row sum in fp32 adds: v_dot2c_f32_bf16 (the packed alternative) does not co-execute with the
-            // matrix cores on gfx950, and the plain adds do.
-            const float pair = two[0] + two[1];
-            if (j & 2) {
-              lb1 += pair;
-            } else {
-              lb0 += pair;
-            }
+            pair[4 * ks + j / 2] = two[0] + two[1];
             pb[ks][j] = c[0];
             pb[ks][j + 1] = c[1];
           }
         }
+        // Row sum over the fp32 P as a tree of fp32 adds (v_dot2c_f32_bf16, the packed alternative, does not
+        // co-execute with the matrix cores on gfx950).
+        lb = ((pair[0] + pair[1]) + (pair[2] + pair[3])) + ((pair[4] + pair[5]) + (pair[6] + pair[7]));
       };
       exps(-m);
       // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN, as before
       // the first half, where m is -inf) some score passed m by about 20 (log2 units). Only then is the half's
       // max taken, m raised, O and l rescaled and P redone; O and l always share m, so O / l does not depend on
       // where m sits.
-      if (__builtin_amdgcn_ballot_w64(!(lb0 + lb1 <= kSumHigh)) != 0ull) {
+      if (__builtin_amdgcn_ballot_w64(!(lb <= kSumHigh)) != 0ull) {
         // Max of the raw scores (scale > 0, so it commutes with the scaling). The chain opens with a
         // compiler-visible v_med3_f32 (med3(a, b, FLT_MAX) = max(a, b) for scores below +inf), before which the
         // compiler inserts the wait states a VALU read of an MFMA result needs; the inline v_max3_f32 that follow
@@ -503,8 +498,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
         const float mn = cand > m ? cand : m;
         const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first half
         m = mn;
-        l0 *= alpha;
-        l1 *= alpha;
+        l *= alpha;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           o0[i] *= alpha;
@@ -512,8 +506,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
         }
         exps(-m);
       }
-      l0 += lb0;
-      l1 += lb1;
+      l += lb;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         // O^T += V^T . P^T for this k-step: V^T columns 32 t + 16 ks + 8 hh + 0..7 are logical chunk 2 (2 t + ks) + hh.
@@ -573,7 +566,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
     }
   }
 
-  float lsum = l0 + l1;
+  float lsum = l;
   {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(lsum), __float_as_int(lsum), false, false);
     lsum = __int_as_float(sw[0]) + __int_as_float(sw[1]);
