@@ -338,12 +338,22 @@ def main():
     ent_out = torch.empty(SLOTS, VOXELS, device=dev)
     t_entropy = time_events(lambda: entropy_batched(w.logits[0].view(SLOTS, VOXELS, CLASSES), 'voxel_major',
                                                     out=ent_out), 20)
+    # The class head's own row order (patches of 4^3 voxels, stream/fast_ops.py:305-308): the same logits selected
+    # in place, and the [n, C, Y, Z, X] copy the reference's forward makes before its selection.
+    from streamvoxel_amd.stream.patches import PatchLogits
+    patch_logits = PatchLogits(torch.empty(SLOTS, VOXELS // 64, 64 * CLASSES, device=dev), SHAPE, 4, CLASSES)
+    patch_logits.rows[:, patch_logits.row_index(torch.arange(VOXELS, device=dev))] = \
+        w.logits[0].view(SLOTS, VOXELS, CLASSES)
+    t_select_patches = time_graph(lambda: w.sel.run(patch_logits), 20)
+    t_permute = time_graph(lambda: patch_logits.class_major(), 20)
+    del patch_logits
     xattn_tflops = w.flops_per_layer / t_layer / 1e12
     select_gbs = w.select_bytes / t_select / 1e9
     entropy_bytes = SLOTS * VOXELS * (CLASSES * 4 + 4)
     peaks = measured_peaks(dev)
     log(f'xattn {t_layer * 1e6:.1f} us/layer = {xattn_tflops:.1f} TFLOP/s; select {t_select * 1e6:.1f} us = '
-        f'{select_gbs:.0f} GB/s; entropy {t_entropy * 1e6:.1f} us; peaks {peaks}')
+        f'{select_gbs:.0f} GB/s; entropy {t_entropy * 1e6:.1f} us; select from the head\'s patch order '
+        f'{t_select_patches * 1e6:.1f} us (the permute it avoids: {t_permute * 1e6:.1f} us); peaks {peaks}')
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(w, args.cpu_seconds)
@@ -366,8 +376,12 @@ def main():
                              achieved=select_gbs, peak=PEAK_HBM_GBS, unit='GB/s', frac=select_gbs / PEAK_HBM_GBS,
                              traffic=profiled_traffic('ease_select'), bytes_per_call=w.select_bytes,
                              avg_call_us=t_select * 1e6,
-                             entropy_kernel_GBps=entropy_bytes / t_entropy / 1e9, entropy_us=t_entropy * 1e6),
+                             entropy_kernel_GBps=entropy_bytes / t_entropy / 1e9, entropy_us=t_entropy * 1e6,
+                             patch_order_us=t_select_patches * 1e6,
+                             patch_order_GBps=w.select_bytes / t_select_patches / 1e9),
         components=dict(xattn_ms_per_step=LAYERS * t_layer * 1e3, select_ms_per_step=t_select * 1e3,
+                        select_from_patch_order_ms_per_step=t_select_patches * 1e3,
+                        class_major_permute_ms_avoided=t_permute * 1e3,
                         selection_bad_flag_seen=bad),
         measured_peaks=peaks,
         cpu_baseline=cpu,

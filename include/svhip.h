@@ -52,6 +52,23 @@ int svhip_air_prob(const void* logits, int dtype, int64_t batch, int64_t classes
                    void* stream);
 
 /*
+ * The same statistics over logits in the class head's patch order: patches[b, r, c] at b*stride_b + r*stride_n + c
+ * (voxel-major rows of `classes` logits), where the voxel (y, z, x) of a [Y,Z,X] window sits in row
+ *   r = ((y/p * (Z/p) + z/p) * (X/p) + x/p) * p^3 + ((y%p) * p + z%p) * p + x%p,   p = patch,
+ * the row order of `class_head(...)` before the reshape / permute to [n, C, Y, Z, X]. patch, Y, Z, X: powers of
+ * two, patch <= each; rows 16-byte aligned, classes a multiple of 16 bytes' worth of elements. out: fp32 [batch,
+ * Y*Z*X] in (y, z, x) order.
+ * Replaces: the permute in FastSlotForward.forward (streamvoxel/stream/fast_ops.py:305-308) and
+ * UnconditionalMD4.forward (streamvoxel/models/unconditional_md4.py:126-129) followed by entropy_scores / the air
+ * probability of streamvoxel/stream/slot.py:126: the permuted copy is never made.
+ */
+int svhip_entropy_patches(const void* logits, int dtype, int64_t batch, int64_t classes, int64_t Y, int64_t Z,
+                          int64_t X, int64_t patch, int64_t stride_b, int64_t stride_n, float* out, void* stream);
+int svhip_air_prob_patches(const void* logits, int dtype, int64_t batch, int64_t classes, int64_t Y, int64_t Z,
+                           int64_t X, int64_t patch, int64_t stride_b, int64_t stride_n, const int32_t* air_ids,
+                           int32_t n_air, float* out, void* stream);
+
+/*
  * Low-entropy-last update, in place on `last`:
  *   bad = (mask & air <= fp32(1 - eps)) | solid
  *   SVHIP_LEL_COLUMN: last [B,Y,Z,X] |= the top run (from y = Y-1 down) of clean voxels of every (z, x) column;
@@ -102,6 +119,18 @@ int svhip_ease_select(const void* logits, int dtype, int64_t classes, int64_t st
                       const int64_t* pos, const double* frac, const int64_t* n_total, const int64_t* committed,
                       uint8_t* chosen, uint8_t* bad, float* scores_out, void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/*
+ * svhip_ease_select over logits in the class head's patch order (row map as in svhip_entropy_patches); tokens,
+ * last, chosen and scores_out stay in (y, z, x) order. Workspace: svhip_ease_select_workspace_bytes.
+ * Replaces: the permute of fast_ops.py:305-308 followed by FastLowEntropyLastSlot.select (fast_ops.py:534-540).
+ */
+int svhip_ease_select_patches(const void* logits, int dtype, int64_t classes, int64_t patch, int64_t stride_b,
+                              int64_t stride_n, const int64_t* tokens, int64_t mask_token, const uint8_t* last,
+                              int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_t block, const int64_t* k,
+                              const int64_t* pos, const double* frac, const int64_t* n_total,
+                              const int64_t* committed, uint8_t* chosen, uint8_t* bad, float* scores_out,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Cross attention over per-window, variable-length cached keys:

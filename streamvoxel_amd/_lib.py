@@ -27,6 +27,8 @@ SIGNATURES = {
     'svhip_entropy': (ctypes.c_int, [_c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
     'svhip_air_prob': (ctypes.c_int, [_c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i32,
                                       _c_p, _c_p]),
+    'svhip_entropy_patches': (ctypes.c_int, [_c_p, ctypes.c_int] + [_c_i64] * 8 + [_c_p, _c_p]),
+    'svhip_air_prob_patches': (ctypes.c_int, [_c_p, ctypes.c_int] + [_c_i64] * 8 + [_c_p, _c_i32, _c_p, _c_p]),
     'svhip_lel_update': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_d, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
     'svhip_top_mask': (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
     'svhip_quota_select_workspace_bytes': (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
@@ -36,6 +38,9 @@ SIGNATURES = {
     'svhip_ease_select': (ctypes.c_int, [_c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
                                          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                          _c_p, _c_p, _c_p, _c_sz, _c_p]),
+    'svhip_ease_select_patches': (ctypes.c_int, [_c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
+                                                 _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
+                                                 _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     'svhip_xattn_fwd': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, ctypes.c_int, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
                                        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f, _c_p]),

@@ -14,11 +14,11 @@ struct StoreF32 {
 template <typename T, int NV, int MODE>
 __global__ __launch_bounds__(256) void stats_voxel_major(const T* __restrict__ x, int64_t total, int64_t n, int64_t C,
                                                          int64_t sb, int64_t sn, const int32_t* __restrict__ air_ids,
-                                                         int n_air, float* __restrict__ out) {
+                                                         int n_air, float* __restrict__ out, VoxelRows rows) {
   __shared__ uint32_t air_bits[MODE == kAirProb ? kMaxAirClasses / 32 : 1];
   if constexpr (MODE == kAirProb) load_air_bits(air_bits, air_ids, n_air, C);
   StoreF32 o{out};
-  voxel_major_pass<T, NV, MODE>(x, total, n, C, sb, sn, air_bits, o, blockIdx.x, gridDim.x);
+  voxel_major_pass<T, NV, MODE>(x, total, n, C, sb, sn, air_bits, o, blockIdx.x, gridDim.x, rows);
 }
 
 template <typename T, bool VEC, int MODE>
@@ -34,14 +34,19 @@ __global__ __launch_bounds__(256) void stats_class_major(const T* __restrict__ x
 
 template <typename T, int MODE>
 static int launch_stats(const T* x, int64_t batch, int64_t C, int64_t n, int64_t sb, int64_t sc, int64_t sn,
-                        const int32_t* air_ids, int n_air, float* out, hipStream_t stream) {
+                        const int32_t* air_ids, int n_air, float* out, hipStream_t stream, VoxelRows rows,
+                        const char* name) {
   const StatsPlan plan = plan_stats<T>(x, batch, C, n, sb, sc, sn);
+  SVHIP_REQUIRE(rows.p_log < 0 || plan.layout == kVoxelMajor,
+                "%s: patch-order logits must be voxel-major rows (stride_c 1, 16-byte aligned rows, classes a "
+                "multiple of %d, at most %d)",
+                name, Vec16<T>::kElems, 128 * Vec16<T>::kElems);
   const unsigned grid = static_cast<unsigned>(plan.grid);
   if (plan.layout == kVoxelMajor) {
     const int64_t total = batch * n;
 #define SVHIP_VM(NVV)                                                                                        \
   case NVV:                                                                                                  \
-    stats_voxel_major<T, NVV, MODE><<<grid, 256, 0, stream>>>(x, total, n, C, sb, sn, air_ids, n_air, out); \
+    stats_voxel_major<T, NVV, MODE><<<grid, 256, 0, stream>>>(x, total, n, C, sb, sn, air_ids, n_air, out, rows); \
     return SVHIP_OK;
     switch (plan.nv) {
       SVHIP_VM(1)
@@ -68,8 +73,7 @@ static int launch_stats(const T* x, int64_t batch, int64_t C, int64_t n, int64_t
 template <int MODE>
 static int stats_entry(const void* logits, int dtype, int64_t batch, int64_t classes, int64_t n, int64_t sb,
                        int64_t sc, int64_t sn, const int32_t* air_ids, int n_air, float* out, void* stream,
-                       const char* name) {
-  clear_error();
+                       const char* name, VoxelRows rows = kYzxRows) {
   SVHIP_REQUIRE(logits != nullptr && out != nullptr, "%s: null pointer", name);
   SVHIP_REQUIRE(batch >= 0 && n >= 0 && classes >= 1, "%s: bad sizes batch=%lld n=%lld classes=%lld", name,
                 (long long)batch, (long long)n, (long long)classes);
@@ -83,10 +87,10 @@ static int stats_entry(const void* logits, int dtype, int64_t batch, int64_t cla
   int rc;
   if (dtype == SVHIP_F32) {
     rc = launch_stats<float, MODE>(static_cast<const float*>(logits), batch, classes, n, sb, sc, sn, air_ids, n_air,
-                                   out, s);
+                                   out, s, rows, name);
   } else {
     rc = launch_stats<uint16_t, MODE>(static_cast<const uint16_t*>(logits), batch, classes, n, sb, sc, sn, air_ids,
-                                      n_air, out, s);
+                                      n_air, out, s, rows, name);
   }
   if (rc != SVHIP_OK) return rc;
   SVHIP_LAUNCHED(name);
@@ -97,6 +101,7 @@ static int stats_entry(const void* logits, int dtype, int64_t batch, int64_t cla
 
 extern "C" int svhip_entropy(const void* logits, int dtype, int64_t batch, int64_t classes, int64_t n,
                              int64_t stride_b, int64_t stride_c, int64_t stride_n, float* out, void* stream) {
+  svhip::clear_error();
   return svhip::stats_entry<svhip::kEntropy>(logits, dtype, batch, classes, n, stride_b, stride_c, stride_n, nullptr,
                                              0, out, stream, "svhip_entropy");
 }
@@ -104,6 +109,33 @@ extern "C" int svhip_entropy(const void* logits, int dtype, int64_t batch, int64
 extern "C" int svhip_air_prob(const void* logits, int dtype, int64_t batch, int64_t classes, int64_t n,
                               int64_t stride_b, int64_t stride_c, int64_t stride_n, const int32_t* air_ids,
                               int32_t n_air, float* out, void* stream) {
+  svhip::clear_error();
   return svhip::stats_entry<svhip::kAirProb>(logits, dtype, batch, classes, n, stride_b, stride_c, stride_n, air_ids,
                                              n_air, out, stream, "svhip_air_prob");
+}
+
+extern "C" int svhip_entropy_patches(const void* logits, int dtype, int64_t batch, int64_t classes, int64_t Y,
+                                     int64_t Z, int64_t X, int64_t patch, int64_t stride_b, int64_t stride_n,
+                                     float* out, void* stream) {
+  const char* name = "svhip_entropy_patches";
+  svhip::clear_error();
+  SVHIP_REQUIRE(Y >= 0 && Z >= 0 && X >= 0 && patch >= 1, "%s: bad window or patch", name);
+  svhip::VoxelRows rows;
+  const int rc = svhip::make_rows(Y, Z, X, patch, &rows, name);
+  if (rc != SVHIP_OK) return rc;
+  return svhip::stats_entry<svhip::kEntropy>(logits, dtype, batch, classes, Y * Z * X, stride_b, 1, stride_n,
+                                             nullptr, 0, out, stream, name, rows);
+}
+
+extern "C" int svhip_air_prob_patches(const void* logits, int dtype, int64_t batch, int64_t classes, int64_t Y,
+                                      int64_t Z, int64_t X, int64_t patch, int64_t stride_b, int64_t stride_n,
+                                      const int32_t* air_ids, int32_t n_air, float* out, void* stream) {
+  const char* name = "svhip_air_prob_patches";
+  svhip::clear_error();
+  SVHIP_REQUIRE(Y >= 0 && Z >= 0 && X >= 0 && patch >= 1, "%s: bad window or patch", name);
+  svhip::VoxelRows rows;
+  const int rc = svhip::make_rows(Y, Z, X, patch, &rows, name);
+  if (rc != SVHIP_OK) return rc;
+  return svhip::stats_entry<svhip::kAirProb>(logits, dtype, batch, classes, Y * Z * X, stride_b, 1, stride_n,
+                                             air_ids, n_air, out, stream, name, rows);
 }

@@ -851,7 +851,7 @@ struct KeyStore {
 template <typename T, int LAYOUT, int NV>
 __global__ __launch_bounds__(256) void ease_stats_kernel(const T* __restrict__ x, int64_t batch, int64_t n, int64_t C,
                                                          int64_t sb, int64_t sc, int64_t sn, KeyStore ks,
-                                                         ApportionArgs ap, int side) {
+                                                         ApportionArgs ap, int side, VoxelRows rows) {
   __shared__ uint64_t skey[kWaveBlocks];
   __shared__ uint32_t hist[256];
   if (static_cast<int>(blockIdx.x) < side) {
@@ -860,7 +860,7 @@ __global__ __launch_bounds__(256) void ease_stats_kernel(const T* __restrict__ x
   }
   const int64_t blk = blockIdx.x - side, nblk = gridDim.x - side;
   if constexpr (LAYOUT == kVoxelMajor) {
-    voxel_major_pass<T, NV, kEntropy>(x, batch * n, n, C, sb, sn, nullptr, ks, blk, nblk);
+    voxel_major_pass<T, NV, kEntropy>(x, batch * n, n, C, sb, sn, nullptr, ks, blk, nblk, rows);
   } else {
     class_major_pass<T, LAYOUT == kClassMajorVec, kEntropy>(x, batch, n, C, sb, sc, sn, nullptr, ks, blk, nblk);
   }
@@ -868,13 +868,18 @@ __global__ __launch_bounds__(256) void ease_stats_kernel(const T* __restrict__ x
 
 template <typename T>
 static int launch_ease_stats(const T* x, int64_t batch, int64_t C, int64_t n, int64_t sb, int64_t sc, int64_t sn,
-                             const KeyStore& ks, const ApportionArgs& ap, int side, hipStream_t s) {
+                             const KeyStore& ks, const ApportionArgs& ap, int side, hipStream_t s, VoxelRows rows,
+                             const char* name) {
   const StatsPlan plan = plan_stats<T>(x, batch, C, n, sb, sc, sn);
+  SVHIP_REQUIRE(rows.p_log < 0 || plan.layout == kVoxelMajor,
+                "%s: patch-order logits must be voxel-major rows (stride_c 1, 16-byte aligned rows, classes a "
+                "multiple of %d, at most %d)",
+                name, Vec16<T>::kElems, 128 * Vec16<T>::kElems);
   const unsigned grid = static_cast<unsigned>(plan.grid + side);
   if (plan.layout == kVoxelMajor) {
 #define SVHIP_EVM(NVV)                                                                                          \
   case NVV:                                                                                                     \
-    ease_stats_kernel<T, kVoxelMajor, NVV><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side); \
+    ease_stats_kernel<T, kVoxelMajor, NVV><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side, rows); \
     return SVHIP_OK;
     switch (plan.nv) {
       SVHIP_EVM(1)
@@ -891,11 +896,52 @@ static int launch_ease_stats(const T* x, int64_t batch, int64_t C, int64_t n, in
 #undef SVHIP_EVM
   }
   if (plan.layout == kClassMajorVec) {
-    ease_stats_kernel<T, kClassMajorVec, 0><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side);
+    ease_stats_kernel<T, kClassMajorVec, 0><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side, rows);
   } else {
-    ease_stats_kernel<T, kClassMajorScalar, 0><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side);
+    ease_stats_kernel<T, kClassMajorScalar, 0><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side, rows);
   }
   return SVHIP_OK;
+}
+
+// The EASE selection over logits whose voxel rows are found through `rows` (YZX or patch order).
+static int ease_select_impl(const void* logits, int dtype, int64_t classes, int64_t stride_b, int64_t stride_c,
+                            int64_t stride_n, const int64_t* tokens, int64_t mask_token, const uint8_t* last,
+                            int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_t block, const int64_t* k,
+                            const int64_t* pos, const double* frac, const int64_t* n_total, const int64_t* committed,
+                            uint8_t* chosen, uint8_t* bad, float* scores_out, void* workspace, size_t workspace_bytes,
+                            void* stream, VoxelRows rows, const char* name) {
+  Geometry g;
+  int rc = check_geometry(batch, Y, Z, X, block, name, &g);
+  if (rc != SVHIP_OK) return rc;
+  SVHIP_REQUIRE(logits && tokens && last && k && pos && frac && n_total && committed && chosen && bad,
+                "%s: null pointer", name);
+  SVHIP_REQUIRE(classes >= 1, "%s: bad class count %lld", name, (long long)classes);
+  SVHIP_REQUIRE(dtype == SVHIP_F32 || dtype == SVHIP_BF16, "%s: dtype %d not supported (fp32 or bf16)", name, dtype);
+  const size_t need = quota_ws_bytes(batch, g);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
+    return SVHIP_EWORKSPACE;
+  }
+  const QuotaWs w = carve(workspace, batch, g);
+  hipStream_t s = as_stream(stream);
+  // Windows of at most kWaveBlocks blocks are apportioned by side workgroups of the entropy pass.
+  const int side = g.nb <= kWaveBlocks ? static_cast<int>(batch) : 0;
+  if (side == 0) {
+    rc = launch_apportion(batch, g, k, pos, frac, n_total, committed, w, s, name);
+    if (rc != SVHIP_OK) return rc;
+  }
+  const KeyStore ks{tokens, last, mask_token, w.ckey, scores_out};
+  const ApportionArgs ap{n_total, pos, frac, k, committed, g.nb, w.target};
+  if (dtype == SVHIP_F32) {
+    rc = launch_ease_stats<float>(static_cast<const float*>(logits), batch, classes, g.n, stride_b, stride_c, stride_n,
+                                  ks, ap, side, s, rows, name);
+  } else {
+    rc = launch_ease_stats<uint16_t>(static_cast<const uint16_t*>(logits), batch, classes, g.n, stride_b, stride_c,
+                                     stride_n, ks, ap, side, s, rows, name);
+  }
+  if (rc != SVHIP_OK) return rc;
+  SVHIP_LAUNCHED(name);
+  return launch_inblock_fix(KeyStored{w.ckey}, batch, g, k, n_total, chosen, bad, w, s, name);
 }
 
 }  // namespace svhip
@@ -943,40 +989,28 @@ extern "C" int svhip_ease_select(const void* logits, int dtype, int64_t classes,
                                  const int64_t* pos, const double* frac, const int64_t* n_total,
                                  const int64_t* committed, uint8_t* chosen, uint8_t* bad, float* scores_out,
                                  void* workspace, size_t workspace_bytes, void* stream) {
-  const char* name = "svhip_ease_select";
   clear_error();
-  Geometry g;
-  int rc = check_geometry(batch, Y, Z, X, block, name, &g);
+  return ease_select_impl(logits, dtype, classes, stride_b, stride_c, stride_n, tokens, mask_token, last, batch, Y, Z,
+                          X, block, k, pos, frac, n_total, committed, chosen, bad, scores_out, workspace,
+                          workspace_bytes, stream, kYzxRows, "svhip_ease_select");
+}
+
+extern "C" int svhip_ease_select_patches(const void* logits, int dtype, int64_t classes, int64_t patch,
+                                         int64_t stride_b, int64_t stride_n, const int64_t* tokens,
+                                         int64_t mask_token, const uint8_t* last, int64_t batch, int64_t Y,
+                                         int64_t Z, int64_t X, int64_t block, const int64_t* k, const int64_t* pos,
+                                         const double* frac, const int64_t* n_total, const int64_t* committed,
+                                         uint8_t* chosen, uint8_t* bad, float* scores_out, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  const char* name = "svhip_ease_select_patches";
+  clear_error();
+  SVHIP_REQUIRE(patch >= 1, "%s: bad patch size %lld", name, (long long)patch);
+  VoxelRows rows;
+  const int rc = make_rows(Y, Z, X, patch, &rows, name);
   if (rc != SVHIP_OK) return rc;
-  SVHIP_REQUIRE(logits && tokens && last && k && pos && frac && n_total && committed && chosen && bad,
-                "%s: null pointer", name);
-  SVHIP_REQUIRE(classes >= 1, "%s: bad class count %lld", name, (long long)classes);
-  SVHIP_REQUIRE(dtype == SVHIP_F32 || dtype == SVHIP_BF16, "%s: dtype %d not supported (fp32 or bf16)", name, dtype);
-  const size_t need = quota_ws_bytes(batch, g);
-  if (workspace == nullptr || workspace_bytes < need) {
-    set_error("%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
-    return SVHIP_EWORKSPACE;
-  }
-  const QuotaWs w = carve(workspace, batch, g);
-  hipStream_t s = as_stream(stream);
-  // Windows of at most kWaveBlocks blocks are apportioned by side workgroups of the entropy pass.
-  const int side = g.nb <= kWaveBlocks ? static_cast<int>(batch) : 0;
-  if (side == 0) {
-    rc = launch_apportion(batch, g, k, pos, frac, n_total, committed, w, s, name);
-    if (rc != SVHIP_OK) return rc;
-  }
-  const KeyStore ks{tokens, last, mask_token, w.ckey, scores_out};
-  const ApportionArgs ap{n_total, pos, frac, k, committed, g.nb, w.target};
-  if (dtype == SVHIP_F32) {
-    rc = launch_ease_stats<float>(static_cast<const float*>(logits), batch, classes, g.n, stride_b, stride_c, stride_n,
-                                  ks, ap, side, s);
-  } else {
-    rc = launch_ease_stats<uint16_t>(static_cast<const uint16_t*>(logits), batch, classes, g.n, stride_b, stride_c,
-                                     stride_n, ks, ap, side, s);
-  }
-  if (rc != SVHIP_OK) return rc;
-  SVHIP_LAUNCHED(name);
-  return launch_inblock_fix(KeyStored{w.ckey}, batch, g, k, n_total, chosen, bad, w, s, name);
+  return ease_select_impl(logits, dtype, classes, stride_b, 1, stride_n, tokens, mask_token, last, batch, Y, Z, X,
+                          block, k, pos, frac, n_total, committed, chosen, bad, scores_out, workspace,
+                          workspace_bytes, stream, rows, name);
 }
 
 extern "C" int svhip_top_mask(const float* scores, const uint8_t* eligible, int64_t batch, int64_t n,

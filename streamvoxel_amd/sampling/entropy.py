@@ -4,6 +4,7 @@ from __future__ import annotations
 import torch
 
 from streamvoxel_amd import _lib
+from streamvoxel_amd.stream.patches import PatchLogits
 
 
 def _as_kernel_input(logits):
@@ -14,7 +15,10 @@ def _as_kernel_input(logits):
 
 
 def entropy_scores(logits):
-    """sum_c p_c log p_c over axis 0 (nats, fp32 arithmetic). logits [C, ...] on the GPU -> fp32 [...]."""
+    """sum_c p_c log p_c over axis 0 (nats, fp32 arithmetic). logits [C, ...] on the GPU -> fp32 [...]; a
+    PatchLogits (the class head's output in place) -> fp32 [n, Y, Z, X]."""
+    if isinstance(logits, PatchLogits):
+        return _patch_stats(logits, None)
     _lib.require_gpu(logits)
     classes = logits.shape[0]
     x = _as_kernel_input(logits).reshape(classes, -1)
@@ -60,9 +64,33 @@ def entropy_batched(logits, layout='class_major', out=None):
     return out
 
 
+def _patch_stats(logits, air_index):
+    rows = logits.rows
+    _lib.require_gpu(rows)
+    Y, Z, X = logits.shape
+    n = len(logits)
+    out = torch.empty((n, Y, Z, X), device=rows.device, dtype=torch.float32)
+    lib = _lib.load()
+    if air_index is None:
+        _lib.check(lib.svhip_entropy_patches(_lib.ptr(rows), _lib.dtype_code(rows.dtype), n, logits.classes, Y, Z, X,
+                                             logits.patch, rows.stride(0), rows.stride(1), _lib.ptr(out),
+                                             _lib.stream_of(rows)), 'svhip_entropy_patches')
+    else:
+        _lib.check(lib.svhip_air_prob_patches(_lib.ptr(rows), _lib.dtype_code(rows.dtype), n, logits.classes, Y, Z,
+                                              X, logits.patch, rows.stride(0), rows.stride(1), _lib.ptr(air_index),
+                                              int(air_index.numel()), _lib.ptr(out), _lib.stream_of(rows)),
+                   'svhip_air_prob_patches')
+    return out
+
+
 def air_prob(logits, air_ids, air_index=None):
-    """sum over the air classes of softmax(logits, 0) (stream/slot.py:126). logits [C, ...] -> fp32 [...].
-    `air_index` may carry the ids as a device int32 tensor (graph capture needs a fixed buffer)."""
+    """sum over the air classes of softmax(logits, 0) (stream/slot.py:126). logits [C, ...] -> fp32 [...]; a
+    PatchLogits -> fp32 [n, Y, Z, X]. `air_index` may carry the ids as a device int32 tensor (graph capture needs
+    a fixed buffer)."""
+    if isinstance(logits, PatchLogits):
+        if air_index is None:
+            air_index = torch.as_tensor(list(air_ids), dtype=torch.int32, device=logits.device)
+        return _patch_stats(logits, air_index)
     _lib.require_gpu(logits)
     classes = logits.shape[0]
     x = _as_kernel_input(logits).reshape(classes, -1)

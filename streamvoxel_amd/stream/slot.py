@@ -23,6 +23,7 @@ from streamvoxel_amd import _lib
 from streamvoxel_amd.sampling.block_quota import QuotaWorkspace, block_view
 from streamvoxel_amd.sampling.low_entropy_last import low_entropy_last_quotas
 from streamvoxel_amd.sampling.schedule import actual_time
+from streamvoxel_amd.stream.patches import PatchLogits
 
 ORDER_SEED_OFFSET = 9173
 
@@ -63,12 +64,13 @@ class ForwardBudget:
 
 
 def _class_major(logits, classes, total):
-    """(tensor, dtype code, stride_c, stride_n) of [C, Y, Z, X] logits as the kernels read them ([C, N] with any
-    class stride). Logits that do not flatten without a copy, or in another float type, are made so on the device."""
+    """(tensor, dtype code, stride_c, stride_n) of [C, Y, Z, X] logits as the kernels read them: [C, N] with a unit
+    stride along the voxels (class planes) or along the classes (a view of voxel rows). Logits that do not flatten
+    so without a copy, or in another float type, are made class-major on the device."""
     if logits.dtype not in (torch.float32, torch.bfloat16):
         logits = logits.float()
     x = logits.reshape(classes, total)
-    if x.stride(1) != 1:
+    if x.stride(1) != 1 and x.stride(0) != 1:
         x = x.contiguous()
     return x, _lib.dtype_code(x.dtype), x.stride(0), x.stride(1)
 
@@ -165,13 +167,21 @@ class LowEntropyLastSlot:
     def _mark(self, logits, tokens):
         """The marking forward (stream/slot.py:124-135): air probability, then the top run of clean voxels of every
         (z, x) column joins the deferred set."""
-        x, code, sc, sn = _class_major(logits, self.classes, self.total)
         lib = _lib.load()
-        stream = _lib.stream_of(x)
-        _lib.check(lib.svhip_air_prob(_lib.ptr(x), code, 1, self.classes, self.total, 0, sc, sn,
-                                      _lib.ptr(self.air_index), int(self.air_index.numel()),
-                                      _lib.ptr(self.air_p), stream), 'svhip_air_prob')
         Y, Z, X = self.shape
+        if isinstance(logits, PatchLogits):
+            rows = self._patch_rows(logits)
+            stream = _lib.stream_of(rows)
+            _lib.check(lib.svhip_air_prob_patches(
+                _lib.ptr(rows), _lib.dtype_code(rows.dtype), 1, self.classes, Y, Z, X, logits.patch, 0,
+                rows.stride(0), _lib.ptr(self.air_index), int(self.air_index.numel()), _lib.ptr(self.air_p), stream),
+                'svhip_air_prob_patches')
+        else:
+            x, code, sc, sn = _class_major(logits, self.classes, self.total)
+            stream = _lib.stream_of(x)
+            _lib.check(lib.svhip_air_prob(_lib.ptr(x), code, 1, self.classes, self.total, 0, sc, sn,
+                                          _lib.ptr(self.air_index), int(self.air_index.numel()),
+                                          _lib.ptr(self.air_p), stream), 'svhip_air_prob')
         _lib.check(lib.svhip_lel_update(_lib.ptr(self.last.view(torch.uint8)), None, _lib.ptr(self.air_p), None,
                                         self.last_eps, _lib.SVHIP_LEL_COLUMN, 1, Y, Z, X, stream),
                    'svhip_lel_update')
@@ -197,15 +207,35 @@ class LowEntropyLastSlot:
         self.frac.fill_((committed + k) / (self.total - self.last_count))
         return k
 
+    def _patch_rows(self, logits):
+        """[N, C] rows of a one-window PatchLogits of this slot's shape and classes."""
+        if len(logits) != 1 or logits.shape != self.shape or logits.classes != self.classes:
+            raise ValueError(f'patch logits of {len(logits)} x {logits.shape} windows of {logits.classes} classes, '
+                             f'the slot needs one {self.shape} window of {self.classes}')
+        _lib.require_gpu(logits.rows)
+        return logits.rows[0]
+
     def select(self, logits, tokens):
-        """Graph-capturable (fast_ops.py:534-540): reads logits [C,Y,Z,X], tokens [Y,Z,X] int64 and the static
-        buffers; writes `chosen` and `bad` (and `scores` when kept). One fused kernel sequence, no host sync."""
-        _lib.require_gpu(logits, tokens)
+        """Graph-capturable (fast_ops.py:534-540): reads logits [C,Y,Z,X] (or a PatchLogits of one window: the
+        class head's output in place), tokens [Y,Z,X] int64 and the static buffers; writes `chosen` and `bad` (and
+        `scores` when kept). One fused kernel sequence, no host sync."""
+        _lib.require_gpu(tokens)
         if tokens.dtype != torch.int64 or tokens.shape != self.shape or not tokens.is_contiguous():
             raise ValueError('tokens must be a contiguous int64 [Y, Z, X] buffer')
-        x, code, sc, sn = _class_major(logits, self.classes, self.total)
         Y, Z, X = self.shape
         lib = _lib.load()
+        if isinstance(logits, PatchLogits):
+            rows = self._patch_rows(logits)
+            _lib.check(lib.svhip_ease_select_patches(
+                _lib.ptr(rows), _lib.dtype_code(rows.dtype), self.classes, logits.patch, 0, rows.stride(0),
+                _lib.ptr(tokens), self.classes, _lib.ptr(self.last_static.view(torch.uint8)), 1, Y, Z, X,
+                self.block_size, _lib.ptr(self.k), _lib.ptr(self.pos), _lib.ptr(self.frac), _lib.ptr(self.n_total),
+                _lib.ptr(self.committed), _lib.ptr(self.chosen.view(torch.uint8)), _lib.ptr(self.bad.view(torch.uint8)),
+                _lib.ptr(self.scores), _lib.ptr(self.workspace.buffer), self.workspace.buffer.numel(),
+                _lib.stream_of(rows)), 'svhip_ease_select_patches')
+            return
+        _lib.require_gpu(logits)
+        x, code, sc, sn = _class_major(logits, self.classes, self.total)
         _lib.check(lib.svhip_ease_select(
             _lib.ptr(x), code, self.classes, self.classes * self.total, sc, sn, _lib.ptr(tokens), self.classes,
             _lib.ptr(self.last_static.view(torch.uint8)), 1, Y, Z, X, self.block_size, _lib.ptr(self.k),
@@ -222,7 +252,11 @@ class LowEntropyLastSlot:
         else:
             graph.replay()
         index = torch.nonzero_static(self.chosen.reshape(-1), size=k).squeeze(1)
-        probabilities = logits.reshape(self.classes, -1).index_select(1, index).t().contiguous().float().softmax(-1)
+        if isinstance(logits, PatchLogits):
+            rows = logits.gather(index)                                     # [k, C], voxels in index order
+        else:
+            rows = logits.reshape(self.classes, -1).index_select(1, index).t().contiguous()
+        probabilities = rows.float().softmax(-1)
         values = torch.multinomial(probabilities, 1, generator=self.generator).squeeze(-1)
         tokens.view(-1).index_copy_(0, index, values)
         host = self._host[:2 * k + 1]
@@ -251,7 +285,7 @@ class LowEntropyLastSlot:
 
     def consume(self, logits, tokens):
         """One forward for this slot (stream/slot.py:117-164). `tokens` [Y,Z,X] int64 is updated in place, `logits`
-        is [C,Y,Z,X]. Returns (finish record or None, commit or None)."""
+        is [C,Y,Z,X] or a PatchLogits of one window. Returns (finish record or None, commit or None)."""
         if self.phase == 'idle':
             return None, None
         if self.phase == 'marking':
@@ -285,7 +319,7 @@ FastLowEntropyLastSlot = LowEntropyLastSlot
 class SelectGraphs:
     """One captured `select` per (bucket, slot) over an engine's static outputs and token rows
     (fast_ops.py:584-623). `engine` provides `device`, `graphs` (non-empty once captured), `outputs`
-    ({bucket size: logits [size, C, Y, Z, X]}) and `tokens` ([slots, Y, Z, X] int64). `lookup(logits)` returns the
+    ({bucket size: logits [size, C, Y, Z, X] or PatchLogits}) and `tokens` ([slots, Y, Z, X] int64). `lookup(logits)` returns the
     bucket whose output tensor `logits` is, or None (eager logits then select eagerly)."""
 
     def __init__(self, engine, slots):

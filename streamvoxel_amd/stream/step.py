@@ -14,6 +14,7 @@ from __future__ import annotations
 import torch
 
 from streamvoxel_amd import _lib
+from streamvoxel_amd.stream.patches import PatchLogits
 from streamvoxel_amd.sampling.block_quota import QuotaWorkspace, block_view
 from streamvoxel_amd.stream.attention import attention
 
@@ -172,14 +173,31 @@ class EaseSelect:
         self.committed[index].fill_(int(committed))
         self.frac[index].fill_(float(frac))
 
+    def _patch_rows(self, logits):
+        if logits.shape != self.shape:
+            raise ValueError(f'patch logits of {logits.shape} windows, the selection is for {self.shape}')
+        return logits.rows
+
     def run(self, logits, n=None, keep_scores=False):
         """Entropy + selectable + block-quota select + bad flag for the first n windows (capturable). With
-        keep_scores the fp32 scores are also left in `self.scores`."""
+        keep_scores the fp32 scores are also left in `self.scores`. `logits` may be a PatchLogits (the class
+        head's output read in place)."""
         n = self.batch if n is None else n
-        _lib.require_gpu(logits)
-        code, C, sb, sc, sn = self._layout(logits, n, self.n)
         Y, Z, X = self.shape
         lib = _lib.load()
+        if isinstance(logits, PatchLogits):
+            rows = self._patch_rows(logits)
+            _lib.require_gpu(rows)
+            _lib.check(lib.svhip_ease_select_patches(
+                _lib.ptr(rows), _lib.dtype_code(rows.dtype), logits.classes, logits.patch, rows.stride(0),
+                rows.stride(1), _lib.ptr(self.tokens), self.classes, _lib.ptr(self.last.view(torch.uint8)), n, Y, Z,
+                X, self.block, _lib.ptr(self.k), _lib.ptr(self.pos), _lib.ptr(self.frac), _lib.ptr(self.n_total),
+                _lib.ptr(self.committed), _lib.ptr(self.chosen.view(torch.uint8)), _lib.ptr(self.bad.view(torch.uint8)),
+                _lib.ptr(self.scores) if keep_scores else None, _lib.ptr(self.ws.buffer), self.ws.buffer.numel(),
+                _lib.stream_of(rows)), 'svhip_ease_select_patches')
+            return
+        _lib.require_gpu(logits)
+        code, C, sb, sc, sn = self._layout(logits, n, self.n)
         _lib.check(lib.svhip_ease_select(
             _lib.ptr(logits), code, C, sb, sc, sn, _lib.ptr(self.tokens), self.classes,
             _lib.ptr(self.last.view(torch.uint8)), n, Y, Z, X, self.block, _lib.ptr(self.k), _lib.ptr(self.pos),
@@ -192,11 +210,20 @@ class EaseSelect:
         """Low-entropy-last marking pass (stream/slot.py:124-129): air probability of every voxel and the
         per-column top run of certain air OR-ed into `last` (capturable; the deferred count is read later)."""
         n = self.batch if n is None else n
-        code, C, sb, sc, sn = self._layout(logits, n, self.n)
         Y, Z, X = self.shape
         lib = _lib.load()
-        stream = _lib.stream_of(logits)
-        _lib.check(lib.svhip_air_prob(_lib.ptr(logits), code, n, C, self.n, sb, sc, sn, _lib.ptr(self.air_index),
-                                      int(self.air_index.numel()), _lib.ptr(self.air), stream), 'svhip_air_prob')
+        if isinstance(logits, PatchLogits):
+            rows = self._patch_rows(logits)
+            _lib.require_gpu(rows)
+            stream = _lib.stream_of(rows)
+            _lib.check(lib.svhip_air_prob_patches(
+                _lib.ptr(rows), _lib.dtype_code(rows.dtype), n, logits.classes, Y, Z, X, logits.patch, rows.stride(0),
+                rows.stride(1), _lib.ptr(self.air_index), int(self.air_index.numel()), _lib.ptr(self.air), stream),
+                'svhip_air_prob_patches')
+        else:
+            code, C, sb, sc, sn = self._layout(logits, n, self.n)
+            stream = _lib.stream_of(logits)
+            _lib.check(lib.svhip_air_prob(_lib.ptr(logits), code, n, C, self.n, sb, sc, sn, _lib.ptr(self.air_index),
+                                          int(self.air_index.numel()), _lib.ptr(self.air), stream), 'svhip_air_prob')
         _lib.check(lib.svhip_lel_update(_lib.ptr(self.last.view(torch.uint8)), None, _lib.ptr(self.air), None,
                                         float(eps), _lib.SVHIP_LEL_COLUMN, n, Y, Z, X, stream), 'svhip_lel_update')
