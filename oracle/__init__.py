@@ -10,6 +10,8 @@ Modules (each function cites the reference file:line it restates):
                 reference-form float reductions, numpy fp64 for the high-precision forms).
   slot.py       the low-entropy-last slot state machine (marking -> solid quota steps -> finish).
   attention.py  masked scaled-dot-product cross attention over per-slot key lengths (fp64 / fp32).
+  producer.py   AxialRoPE, the cached-context window layout and the e4m3 cache quantisation.
+  patches.py    the class head's patch order turned into [n, C, Y, Z, X] (explicit loops).
   selftest.py   the fixed checks that pin each function (closed forms, brute force, invariants).
 
 Parity status per function (what pins it):
@@ -25,4 +27,7 @@ Parity status per function (what pins it):
   counts / low_entropy_last_quotas      golden vectors written by the reference; sum/positivity invariants.
   LowEntropyLastSlot                    golden trajectories written by the reference (tests/golden).
   cross_attention_f64                   brute-force per-query softmax loop on tiny inputs; padding invariance.
+  producer.axial_rope / rope_frequencies golden vectors written by the reference's AxialRoPE; known answers.
+  producer.window_kv / quantize_e4m3    layout and format invariants.
+  patches.to_class_major                loops against torch's permute of the reference's form; the 4^3 block order.
 """
