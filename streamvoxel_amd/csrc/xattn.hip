@@ -31,9 +31,9 @@
 // head_dim element's 64 keys. bf16 K and V^T of the padded [B,H,Kcap,*] layout with 16-byte aligned rows take
 // buffer_load_dwordx4 ... lds, which moves a full block straight into LDS without registers, addressed by a
 // per-lane offset fixed for the window plus a scalar block offset. Every other form goes through registers,
-// prefetched one block ahead: OCP e4m3fn K/V converted exactly to bf16 (v_cvt_scalef32_pk_bf16_fp8 with
-// scale 1; the fp8 scales are folded into the softmax scale (k_scale) and the output (v_scale)), row-major V
-// transposed on the way, the packed cu_seqlens layout. The last, partial block of a window is peeled out of the
+// prefetched one block ahead in its storage format and converted when it is written to LDS: OCP e4m3fn K/V
+// converted exactly to bf16 (v_cvt_scalef32_pk_bf16_fp8 with scale 1; the fp8 scales are folded into the softmax
+// scale (k_scale) and the output (v_scale)), row-major V transposed on the way, the packed cu_seqlens layout. The last, partial block of a window is peeled out of the
 // loop and staged synchronously through registers, keys >= L as zeros.
 //
 // Workgroup order: windows are ranked by key count (longest first, ties by index) inside the kernel, so the
@@ -115,41 +115,60 @@ struct Elem {
   using T = typename std::conditional<FP8, uint8_t, uint16_t>::type;
 };
 
-// 8 consecutive elements (bf16 or e4m3) as 8 bf16 in a uint4, with one vector load (16 / 8 bytes, aligned).
+// Staged data stays in its storage format until it is written to LDS (16 bytes of bf16 or 8 bytes of e4m3 per 8
+// elements): a conversion right after a load inside a conditional would make the compiler wait for the load before
+// the branch closes, exposing its latency once per load.
 template <bool FP8>
-__device__ __forceinline__ uint4 load8_vec(const typename Elem<FP8>::T* p) {
+struct Raw {
+  using type = typename std::conditional<FP8, uint2, uint4>::type;
+};
+
+template <bool FP8>
+__device__ __forceinline__ typename Raw<FP8>::type raw_zero() {
   if constexpr (FP8) {
-    const uint2 r = *reinterpret_cast<const uint2*>(p);
-    return fp8x8_to_bf16x8(r.x, r.y);
+    return make_uint2(0u, 0u);
   } else {
-    return *reinterpret_cast<const uint4*>(p);
+    return make_uint4(0u, 0u, 0u, 0u);
   }
+}
+
+// 8 consecutive elements (bf16 or e4m3) with one vector load (16 / 8 bytes, aligned).
+template <bool FP8>
+__device__ __forceinline__ typename Raw<FP8>::type load8_vec(const typename Elem<FP8>::T* p) {
+  return *reinterpret_cast<const typename Raw<FP8>::type*>(p);
 }
 
 // The first `valid` (0..8) of 8 consecutive elements, any alignment; the rest are zero.
 template <bool FP8>
-__device__ __forceinline__ uint4 load8_scalar(const typename Elem<FP8>::T* p, int valid) {
+__device__ __forceinline__ typename Raw<FP8>::type load8_scalar(const typename Elem<FP8>::T* p, int valid) {
+  constexpr int kBits = FP8 ? 8 : 16;
+  constexpr int kPerWord = 32 / kBits;
   uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    if (e < valid) {
-      uint32_t bits;
-      if constexpr (FP8) {
-        const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<uint32_t>(p[e]), 1.0f, false);
-        bits = __builtin_bit_cast(uint32_t, c) & 0xffffu;
-      } else {
-        bits = p[e];
-      }
-      w[e >> 1] |= bits << (16 * (e & 1));
-    }
+    if (e < valid) w[e / kPerWord] |= static_cast<uint32_t>(p[e]) << (kBits * (e % kPerWord));
   }
-  return make_uint4(w[0], w[1], w[2], w[3]);
+  if constexpr (FP8) {
+    return make_uint2(w[0], w[1]);
+  } else {
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Storage -> 8 bf16 in a uint4 (e4m3 converted exactly).
+template <bool FP8>
+__device__ __forceinline__ uint4 to_bf16x8(const typename Raw<FP8>::type& r) {
+  if constexpr (FP8) {
+    return fp8x8_to_bf16x8(r.x, r.y);
+  } else {
+    return r;
+  }
 }
 
 template <bool FP8, bool VT>
 struct Stage {
-  uint4 k[2];
-  uint4 v[2];
+  typename Raw<FP8>::type k[2];
+  typename Raw<FP8>::type v[2];
 };
 
 // Global -> registers for the key block starting at kv0: each thread moves 2 chunks of 8 elements of K and of V.
@@ -165,7 +184,7 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT>& st, const XattnParams
       const int key = c >> 3, dc = c & 7;
       const int kg = kv0 + key;
       const bool ok = dc < dchunks && (!TAIL || kg < L);
-      st.k[r] = ok ? load8_vec<FP8>(K + kg * p.sk_k + dc * 8) : make_uint4(0u, 0u, 0u, 0u);
+      st.k[r] = ok ? load8_vec<FP8>(K + kg * p.sk_k + dc * 8) : raw_zero<FP8>();
     }
     if constexpr (VT) {
       const int d = c >> 3, kc = c & 7;
@@ -175,13 +194,13 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT>& st, const XattnParams
         const int valid = TAIL ? ((L - kg) < 8 ? (L - kg) : 8) : 8;
         st.v[r] = (vt_vec && valid == 8) ? load8_vec<FP8>(src) : load8_scalar<FP8>(src, valid);
       } else {
-        st.v[r] = make_uint4(0u, 0u, 0u, 0u);
+        st.v[r] = raw_zero<FP8>();
       }
     } else {
       const int key = c >> 3, dc = c & 7;
       const int kg = kv0 + key;
       const bool ok = dc < dchunks && (!TAIL || kg < L);
-      st.v[r] = ok ? load8_vec<FP8>(V + kg * p.sv_k + dc * 8) : make_uint4(0u, 0u, 0u, 0u);
+      st.v[r] = ok ? load8_vec<FP8>(V + kg * p.sv_k + dc * 8) : raw_zero<FP8>();
     }
   }
 }
@@ -194,14 +213,15 @@ __device__ __forceinline__ void stage_store(const Stage<FP8, VT>& st, uint16_t* 
     const int c = threadIdx.x + kThreads * r;
     {
       const int R = sigma_row(c >> 3), dc = c & 7;
-      *reinterpret_cast<uint4*>(sK + R * kRow + swz(R, dc) * 8) = st.k[r];
+      *reinterpret_cast<uint4*>(sK + R * kRow + swz(R, dc) * 8) = to_bf16x8<FP8>(st.k[r]);
     }
     if constexpr (VT) {
       const int d = c >> 3, kc = c & 7;
-      *reinterpret_cast<uint4*>(sV + d * kRow + swz(d, kc) * 8) = st.v[r];
+      *reinterpret_cast<uint4*>(sV + d * kRow + swz(d, kc) * 8) = to_bf16x8<FP8>(st.v[r]);
     } else {
       const int key = c >> 3, dc = c & 7;
-      const uint32_t w[4] = {st.v[r].x, st.v[r].y, st.v[r].z, st.v[r].w};
+      const uint4 vb = to_bf16x8<FP8>(st.v[r]);
+      const uint32_t w[4] = {vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int d = dc * 8 + e;
