@@ -347,11 +347,20 @@ def main():
     t_select_patches = time_graph(lambda: w.sel.run(patch_logits), 20)
     t_permute = time_graph(lambda: patch_logits.class_major(), 20)
     del patch_logits
+    # The same layer over an e4m3 cache (per-(window, head) scales, written by svhip_kv_write from layer 0's keys).
+    from streamvoxel_amd import synth
+    from streamvoxel_amd.stream.step import CachedContext
+    ctx8 = CachedContext(1, SLOTS, HEADS, HEAD_DIM, synth.MAX_KEYS, dev, kv_dtype='fp8')
+    for b, L in enumerate(w.lengths):
+        ctx8.write(0, b, w.ctx.k[0][b, :, :L], w.ctx.vt[0][b, :, :, :L].transpose(1, 2).contiguous())
+    t_layer_e4m3 = time_graph(lambda: ctx8.attend(0, w.q[1][0], out=w.o[0].transpose(1, 2)), 20)
+    del ctx8
     xattn_tflops = w.flops_per_layer / t_layer / 1e12
     select_gbs = w.select_bytes / t_select / 1e9
     entropy_bytes = SLOTS * VOXELS * (CLASSES * 4 + 4)
     peaks = measured_peaks(dev)
-    log(f'xattn {t_layer * 1e6:.1f} us/layer = {xattn_tflops:.1f} TFLOP/s; select {t_select * 1e6:.1f} us = '
+    log(f'xattn {t_layer * 1e6:.1f} us/layer = {xattn_tflops:.1f} TFLOP/s (e4m3 cache {t_layer_e4m3 * 1e6:.1f} us); '
+        f'select {t_select * 1e6:.1f} us = '
         f'{select_gbs:.0f} GB/s; entropy {t_entropy * 1e6:.1f} us; select from the head\'s patch order '
         f'{t_select_patches * 1e6:.1f} us (the permute it avoids: {t_permute * 1e6:.1f} us); peaks {peaks}')
     cpu = None
@@ -371,7 +380,8 @@ def main():
         roofline=dict(kernel='xattn_fwd_kernel', bound='mfma', achieved=xattn_tflops, peak=PEAK_BF16_TFLOPS,
                       unit='TFLOP/s', frac=xattn_tflops / PEAK_BF16_TFLOPS,
                       traffic=profiled_traffic('xattn_fwd_kernel'),
-                      flops_per_launch=w.flops_per_layer, avg_launch_us=t_layer * 1e6),
+                      flops_per_launch=w.flops_per_layer, avg_launch_us=t_layer * 1e6,
+                      e4m3_cache_us=t_layer_e4m3 * 1e6, e4m3_cache_TFLOPs=w.flops_per_layer / t_layer_e4m3 / 1e12),
         roofline_select=dict(kernel='svhip_ease_select (entropy + apportion + in-block + fix)', bound='hbm',
                              achieved=select_gbs, peak=PEAK_HBM_GBS, unit='GB/s', frac=select_gbs / PEAK_HBM_GBS,
                              traffic=profiled_traffic('ease_select'), bytes_per_call=w.select_bytes,
