@@ -574,9 +574,13 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
     uint16_t* nK = odd ? sK0 : sK1;
     uint16_t* nV = odd ? sV0 : sV1;
     if (nfull > 0) {
+      // The partial block's loads are in flight during the last full block (the other tiles are free since the
+      // last barrier).
+      Stage<FP8, VT> tl;
+      if (tail) stage_load<FP8, VT, true>(tl, p, K, V, L, nfull * kKB, dchunks, vt_vec);
       compute(Full{}, cK, cV, blk * kKB);
       if (tail) {
-        stage_tail(nK, nV);
+        stage_store<FP8, VT>(tl, nK, nV);
         wait_vmem();
         __syncthreads();
         compute(Partial{}, nK, nV, nfull * kKB);
