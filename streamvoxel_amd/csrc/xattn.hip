@@ -36,9 +36,10 @@
 // scale (k_scale) and the output (v_scale)), row-major V transposed on the way, the packed cu_seqlens layout. The last, partial block of a window is peeled out of the
 // loop and staged synchronously through registers, keys >= L as zeros.
 //
-// Workgroup order: windows are ranked by key count (longest first, ties by index) inside the kernel, so the
-// longest (window, head) pairs start first; consecutive workgroup ids go round robin to the 8 XCDs and all query
-// tiles of one (window, head) pair land on the same XCD, which reads that pair's K/V into its L2 once.
+// Workgroup order: windows are ranked by key count (longest first, ties by index; up to kMaxRankWindows windows)
+// inside the kernel, so the longest (window, head) pairs start first; consecutive workgroup ids go round robin to
+// the 8 XCDs and all query tiles of one (window, head) pair land on the same XCD, which reads that pair's K/V into
+// its L2 once.
 #include <type_traits>
 
 #include "common.hpp"
@@ -57,7 +58,9 @@ constexpr int kRow = 64;      // LDS row stride in bf16 elements (128 bytes, 16-
 constexpr int kThreads = 256;
 constexpr float kSumHigh = 1048576.0f;  // 2^20: a half's row sum above it makes the running max be raised
 constexpr float kFltMax = 3.40282347e38f;
-constexpr int kMaxRankWindows = 4096;
+// Windows are ranked by length inside every workgroup (each thread compares its candidates against all windows);
+// beyond this many windows that quadratic cost is not worth the balance and the grid keeps the window order.
+constexpr int kMaxRankWindows = 256;
 constexpr int kCusPerXcd = 32;  // MI355X: 8 XCDs x 32 CUs
 
 struct XattnParams {

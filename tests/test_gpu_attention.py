@@ -229,3 +229,19 @@ def test_score_scale_jumps_between_key_halves(dev, transposed):
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
     check(out, ref, BF16_ATOL, BF16_RTOL)
+
+
+@pytest.mark.parametrize('B,H', [(300, 1), (256, 3)])
+def test_many_windows(dev, B, H):
+    """More windows than the kernel ranks by length (300: natural order), exactly as many (256), and a window x head
+    count that is not a multiple of the 8 XCDs (300 x 1) or is (256 x 3)."""
+    from streamvoxel_amd.stream.attention import attention
+    Q, kcap, D = 40, 200, 32
+    g = torch.Generator().manual_seed(B)
+    lengths = torch.randint(0, kcap + 1, (B,), generator=g).tolist()
+    _case(f'xattn many windows B={B} H={H}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=B + H)
+    ref = A.cross_attention(q, k, v, lengths)
+    out = attention(q.to(dev), k.to(dev), v.to(dev), lengths=torch.tensor(lengths, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    check(out, ref, BF16_ATOL, BF16_RTOL)
