@@ -1,8 +1,9 @@
 """CPU restatement of StreamVoxel's per-step generation hot path — TEST INFRASTRUCTURE ONLY.
 
-This package is the checker. Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py`
-may import it, and only to compute expected values or to time the CPU baseline. The product package
-`streamvoxel_amd` never imports anything from here; on a GPU its entry points run the HIP library or raise.
+This package is the oracle the tests hold the product to. Only `tests/`, `__graft_entry__.smoke()` and the
+`cpu_baseline` leg of `bench.py` may import it, and only to compute expected values or to time the CPU baseline.
+The product package `streamvoxel_amd` never imports anything from here; on a GPU its entry points run the HIP
+library or raise.
 
 Modules (each function cites the reference file:line it restates):
   sampling.py   entropy, top_mask, block_view, block quota select (host-sync and no-sync forms), low-entropy-last
