@@ -338,6 +338,7 @@ def main():
     ent_out = torch.empty(SLOTS, VOXELS, device=dev)
     t_entropy = time_events(lambda: entropy_batched(w.logits[0].view(SLOTS, VOXELS, CLASSES), 'voxel_major',
                                                     out=ent_out), 20)
+    from streamvoxel_amd import synth
     # The class head's own row order (patches of 4^3 voxels, stream/fast_ops.py:305-308): the same logits selected
     # in place, and the [n, C, Y, Z, X] copy the reference's forward makes before its selection.
     from streamvoxel_amd.stream.patches import PatchLogits
@@ -347,8 +348,19 @@ def main():
     t_select_patches = time_graph(lambda: w.sel.run(patch_logits), 20)
     t_permute = time_graph(lambda: patch_logits.class_major(), 20)
     del patch_logits
+    # The shipped model's selection input: the class head's bf16 rows of 304 classes (autocast), in patch order.
+    from streamvoxel_amd.stream.step import EaseSelect
+    shipped_classes = 304
+    sel304 = EaseSelect(SLOTS, SHAPE, shipped_classes, BLOCK, dev)
+    for b in range(SLOTS):
+        sel304.bind_window(b, torch.randperm(VOXELS // BLOCK ** 3, generator=torch.Generator().manual_seed(b)))
+        sel304.set_step(b, w.quotas[b][0], 0, w.quotas[b][0] / VOXELS)
+    rows304 = synth.bimodal_logits(SLOTS * VOXELS, shipped_classes, 0.7, seed=304, device=dev).to(torch.bfloat16)
+    logits304 = PatchLogits(rows304.view(SLOTS, VOXELS // 64, 64 * shipped_classes), SHAPE, 4, shipped_classes)
+    t_select304 = time_graph(lambda: sel304.run(logits304), 20)
+    bytes304 = SLOTS * VOXELS * (shipped_classes * 2 + 8 + 1 + 1)
+    del sel304, logits304, rows304
     # The same layer over an e4m3 cache (per-(window, head) scales, written by svhip_kv_write from layer 0's keys).
-    from streamvoxel_amd import synth
     from streamvoxel_amd.stream.step import CachedContext
     ctx8 = CachedContext(1, SLOTS, HEADS, HEAD_DIM, synth.MAX_KEYS, dev, kv_dtype='fp8')
     for b, L in enumerate(w.lengths):
@@ -362,7 +374,8 @@ def main():
     log(f'xattn {t_layer * 1e6:.1f} us/layer = {xattn_tflops:.1f} TFLOP/s (e4m3 cache {t_layer_e4m3 * 1e6:.1f} us); '
         f'select {t_select * 1e6:.1f} us = '
         f'{select_gbs:.0f} GB/s; entropy {t_entropy * 1e6:.1f} us; select from the head\'s patch order '
-        f'{t_select_patches * 1e6:.1f} us (the permute it avoids: {t_permute * 1e6:.1f} us); peaks {peaks}')
+        f'{t_select_patches * 1e6:.1f} us (the permute it avoids: {t_permute * 1e6:.1f} us); shipped bf16 C=304 '
+        f'{t_select304 * 1e6:.1f} us; peaks {peaks}')
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(w, args.cpu_seconds)
@@ -388,7 +401,9 @@ def main():
                              avg_call_us=t_select * 1e6,
                              entropy_kernel_GBps=entropy_bytes / t_entropy / 1e9, entropy_us=t_entropy * 1e6,
                              patch_order_us=t_select_patches * 1e6,
-                             patch_order_GBps=w.select_bytes / t_select_patches / 1e9),
+                             patch_order_GBps=w.select_bytes / t_select_patches / 1e9,
+                             shipped_bf16_c304_patch_order_us=t_select304 * 1e6,
+                             shipped_bf16_c304_GBps=bytes304 / t_select304 / 1e9),
         components=dict(xattn_ms_per_step=LAYERS * t_layer * 1e3, select_ms_per_step=t_select * 1e3,
                         select_from_patch_order_ms_per_step=t_select_patches * 1e3,
                         class_major_permute_ms_avoided=t_permute * 1e3,

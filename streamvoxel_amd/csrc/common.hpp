@@ -76,6 +76,25 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// The same over groups of LPV (8 or 16) lanes: quad xor 1, quad xor 2, half-row mirror (8 lanes), row mirror (16).
+template <int LPV>
+__device__ __forceinline__ float group_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  if constexpr (LPV == 16) v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+
+template <int LPV>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  if constexpr (LPV == 16) v += dpp_f<0x140>(v);
+  return v;
+}
+
 // Order-preserving fp32 -> u32 map (ascending float -> ascending key); -0.0 is folded onto +0.0 first so that the
 // two compare equal, as IEEE comparisons (and torch's sort) treat them.
 __device__ __forceinline__ uint32_t ordered_u32(float f) {

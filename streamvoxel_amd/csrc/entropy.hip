@@ -11,14 +11,14 @@ struct StoreF32 {
   __device__ __forceinline__ void store(int64_t voxel, float value, None) const { out[voxel] = value; }
 };
 
-template <typename T, int NV, int MODE>
+template <typename T, int NV, int MODE, int LPV>
 __global__ __launch_bounds__(256) void stats_voxel_major(const T* __restrict__ x, int64_t total, int64_t n, int64_t C,
                                                          int64_t sb, int64_t sn, const int32_t* __restrict__ air_ids,
                                                          int n_air, float* __restrict__ out, VoxelRows rows) {
   __shared__ uint32_t air_bits[MODE == kAirProb ? kMaxAirClasses / 32 : 1];
   if constexpr (MODE == kAirProb) load_air_bits(air_bits, air_ids, n_air, C);
   StoreF32 o{out};
-  voxel_major_pass<T, NV, MODE>(x, total, n, C, sb, sn, air_bits, o, blockIdx.x, gridDim.x, rows);
+  voxel_major_pass<T, NV, MODE, StoreF32, LPV>(x, total, n, C, sb, sn, air_bits, o, blockIdx.x, gridDim.x, rows);
 }
 
 template <typename T, bool VEC, int MODE>
@@ -44,9 +44,15 @@ static int launch_stats(const T* x, int64_t batch, int64_t C, int64_t n, int64_t
   const unsigned grid = static_cast<unsigned>(plan.grid);
   if (plan.layout == kVoxelMajor) {
     const int64_t total = batch * n;
-#define SVHIP_VM(NVV)                                                                                        \
-  case NVV:                                                                                                  \
-    stats_voxel_major<T, NVV, MODE><<<grid, 256, 0, stream>>>(x, total, n, C, sb, sn, air_ids, n_air, out, rows); \
+#define SVHIP_VM(NVV)                                                                                            \
+  case NVV:                                                                                                      \
+    if (plan.lpv == 8) {                                                                                         \
+      stats_voxel_major<T, NVV, MODE, 8><<<grid, 256, 0, stream>>>(x, total, n, C, sb, sn, air_ids, n_air, out,  \
+                                                                   rows);                                        \
+    } else {                                                                                                     \
+      stats_voxel_major<T, NVV, MODE, 16><<<grid, 256, 0, stream>>>(x, total, n, C, sb, sn, air_ids, n_air, out, \
+                                                                    rows);                                       \
+    }                                                                                                            \
     return SVHIP_OK;
     switch (plan.nv) {
       SVHIP_VM(1)

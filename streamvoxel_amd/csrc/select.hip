@@ -848,7 +848,7 @@ struct KeyStore {
 
 // Workgroups [0, side) apportion window blockIdx.x (one wave); the rest run the entropy pass over the logits and
 // write the keys. The apportionment depends only on the selection state, so it runs alongside the HBM-bound pass.
-template <typename T, int LAYOUT, int NV>
+template <typename T, int LAYOUT, int NV, int LPV = 16>
 __global__ __launch_bounds__(256) void ease_stats_kernel(const T* __restrict__ x, int64_t batch, int64_t n, int64_t C,
                                                          int64_t sb, int64_t sc, int64_t sn, KeyStore ks,
                                                          ApportionArgs ap, int side, VoxelRows rows) {
@@ -860,7 +860,7 @@ __global__ __launch_bounds__(256) void ease_stats_kernel(const T* __restrict__ x
   }
   const int64_t blk = blockIdx.x - side, nblk = gridDim.x - side;
   if constexpr (LAYOUT == kVoxelMajor) {
-    voxel_major_pass<T, NV, kEntropy>(x, batch * n, n, C, sb, sn, nullptr, ks, blk, nblk, rows);
+    voxel_major_pass<T, NV, kEntropy, KeyStore, LPV>(x, batch * n, n, C, sb, sn, nullptr, ks, blk, nblk, rows);
   } else {
     class_major_pass<T, LAYOUT == kClassMajorVec, kEntropy>(x, batch, n, C, sb, sc, sn, nullptr, ks, blk, nblk);
   }
@@ -877,9 +877,15 @@ static int launch_ease_stats(const T* x, int64_t batch, int64_t C, int64_t n, in
                 name, Vec16<T>::kElems, 128 * Vec16<T>::kElems);
   const unsigned grid = static_cast<unsigned>(plan.grid + side);
   if (plan.layout == kVoxelMajor) {
-#define SVHIP_EVM(NVV)                                                                                          \
-  case NVV:                                                                                                     \
-    ease_stats_kernel<T, kVoxelMajor, NVV><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side, rows); \
+#define SVHIP_EVM(NVV)                                                                                        \
+  case NVV:                                                                                                   \
+    if (plan.lpv == 8) {                                                                                      \
+      ease_stats_kernel<T, kVoxelMajor, NVV, 8><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side, \
+                                                                      rows);                                  \
+    } else {                                                                                                  \
+      ease_stats_kernel<T, kVoxelMajor, NVV, 16><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap,      \
+                                                                       side, rows);                           \
+    }                                                                                                         \
     return SVHIP_OK;
     switch (plan.nv) {
       SVHIP_EVM(1)

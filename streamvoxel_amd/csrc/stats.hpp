@@ -44,8 +44,7 @@ struct Vec16 {
 };
 
 template <typename T>
-__device__ __forceinline__ void load16(const T* p, float* dst) {
-  uint4 raw = *reinterpret_cast<const uint4*>(p);
+__device__ __forceinline__ void unpack16(const uint4& raw, float* dst) {
   if constexpr (sizeof(T) == 4) {
     dst[0] = __uint_as_float(raw.x);
     dst[1] = __uint_as_float(raw.y);
@@ -59,6 +58,11 @@ __device__ __forceinline__ void load16(const T* p, float* dst) {
       dst[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
   }
+}
+
+template <typename T>
+__device__ __forceinline__ void load16(const T* p, float* dst) {
+  unpack16<T>(*reinterpret_cast<const uint4*>(p), dst);
 }
 
 template <int MODE>
@@ -93,17 +97,18 @@ struct VoxelRows {
 
 constexpr VoxelRows kYzxRows{-1, 0, 0};
 
-// Voxel-major pass: workgroup `blk` of `nblk` takes voxels blk * 16 + (tid / 16), stepping by nblk * 16.
+// Voxel-major pass: LPV (8 or 16) lanes own a voxel; workgroup `blk` of `nblk` takes voxels
+// blk * (256 / LPV) + (tid / LPV), stepping by nblk * (256 / LPV). Each lane loads NV 16-byte vectors of the row.
 // Requires 256-thread workgroups, C % (16 / sizeof(T)) == 0 and 16-byte aligned rows.
-template <typename T, int NV, int MODE, typename Out>
+template <typename T, int NV, int MODE, typename Out, int LPV = 16>
 __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_t total, int64_t n, int64_t C,
                                                  int64_t sb, int64_t sn, const uint32_t* air_bits, Out& out,
                                                  int64_t blk, int64_t nblk, VoxelRows rows = kYzxRows) {
   constexpr int E = Vec16<T>::kElems;
-  const int g = threadIdx.x & 15;
-  constexpr int64_t kRowsPerBlock = 16;
+  const int g = threadIdx.x & (LPV - 1);
+  constexpr int64_t kRowsPerBlock = 256 / LPV;
   const int64_t stride = nblk * kRowsPerBlock;
-  for (int64_t voxel = blk * kRowsPerBlock + (threadIdx.x >> 4); voxel < total; voxel += stride) {
+  for (int64_t voxel = blk * kRowsPerBlock + (threadIdx.x / LPV); voxel < total; voxel += stride) {
     const auto pre = out.prefetch(voxel);
     const int64_t b = voxel / n;
     const int64_t i = voxel - b * n;
@@ -111,12 +116,12 @@ __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_
     float v[NV * E];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      const int64_t c0 = static_cast<int64_t>(g + 16 * j) * E;
+      const int64_t c0 = static_cast<int64_t>(g + LPV * j) * E;
       load16<T>(row + (c0 < C ? c0 : 0), v + j * E);
     }
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      if (static_cast<int64_t>(g + 16 * j) * E >= C) {
+      if (static_cast<int64_t>(g + LPV * j) * E >= C) {
 #pragma unroll
         for (int e = 0; e < E; ++e) v[j * E + e] = -INFINITY;
       }
@@ -124,13 +129,13 @@ __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_
     float m = -INFINITY;
 #pragma unroll
     for (int e = 0; e < NV * E; ++e) m = fmaxf(m, v[e]);
-    m = row16_max(m);
+    m = group_max<LPV>(m);
     float s = 0.f, w = 0.f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        const int c = (g + 16 * j) * E + e;
+        const int c = (g + LPV * j) * E + e;
         if (c < C) {
           const float t = v[j * E + e] - m;
           const float p = fast_exp(t);
@@ -143,8 +148,8 @@ __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_
         }
       }
     }
-    s = row16_sum(s);
-    w = row16_sum(w);
+    s = group_sum<LPV>(s);
+    w = group_sum<LPV>(w);
     if (g == 0) out.store(voxel, finish_stat<MODE>(s, w), pre);
   }
 }
@@ -236,6 +241,7 @@ enum StatsLayout { kVoxelMajor = 0, kClassMajorVec = 1, kClassMajorScalar = 2 };
 struct StatsPlan {
   int layout;
   int nv;        // voxel-major: 16-byte vectors per lane
+  int lpv;       // voxel-major: lanes per voxel (8 when a row fits in 8 vectors per lane, else 16)
   int64_t grid;  // workgroups of 256 threads
 };
 
@@ -255,12 +261,17 @@ __host__ inline StatsPlan plan_stats(const T* x, int64_t batch, int64_t C, int64
   const int64_t bytes = sizeof(T);
   if (sc == 1 && aligned_base && (C % E) == 0 && ((sn * bytes) % 16) == 0 && ((sb * bytes) % 16) == 0 &&
       cdiv(C / E, 16) <= 8) {
-    return StatsPlan{kVoxelMajor, static_cast<int>(cdiv(C / E, 16)), stats_grid(batch * n * 16)};
+    // Eight lanes per row when that leaves fewer vector slots idle (e.g. 304 bf16 classes: 38 vectors, 5 per lane
+    // with 8 lanes, 3 with 16) and the row fits in eight vectors per lane.
+    const int64_t vecs = C / E;
+    const bool eight = cdiv(vecs, 8) <= 8 && cdiv(vecs, 8) * 8 - vecs < cdiv(vecs, 16) * 16 - vecs;
+    const int lpv = eight ? 8 : 16;
+    return StatsPlan{kVoxelMajor, static_cast<int>(cdiv(C / E, lpv)), lpv, stats_grid(batch * n * lpv)};
   }
   if (sn == 1 && aligned_base && (n % E) == 0 && ((sc * bytes) % 16) == 0 && ((sb * bytes) % 16) == 0) {
-    return StatsPlan{kClassMajorVec, 0, stats_grid(batch * (n / E))};
+    return StatsPlan{kClassMajorVec, 0, 0, stats_grid(batch * (n / E))};
   }
-  return StatsPlan{kClassMajorScalar, 0, stats_grid(batch * n)};
+  return StatsPlan{kClassMajorScalar, 0, 0, stats_grid(batch * n)};
 }
 
 // VoxelRows of a [Y, Z, X] window whose logits are in the class head's patch order with patch size `patch`

@@ -66,3 +66,33 @@ def test_product_refuses_host_tensors():
         entropy_scores(torch.zeros(4, 2, 2, 2))
     with pytest.raises(RuntimeError, match='GPU'):
         top_mask(torch.zeros(8), torch.ones(8, dtype=torch.bool), 3)
+
+
+def test_argument_errors_of_the_newer_entry_points(lib):
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails its host checks first
+    # patch order: non-power-of-two window or patch larger than the window
+    rc = lib.svhip_entropy_patches(fake, 0, 1, 256, 256, 16, 12, 4, 0, 256, fake, None)
+    assert rc == -1 and b'power-of-two' in lib.svhip_last_error()
+    rc = lib.svhip_air_prob_patches(fake, 0, 1, 256, 256, 16, 16, 32, 0, 256, fake, 1, fake, None)
+    assert rc == -1 and b'larger than the window' in lib.svhip_last_error()
+    rc = lib.svhip_ease_select_patches(fake, 0, 256, 3, 0, 256, fake, 256, fake, 1, 256, 16, 16, 4, fake, fake, fake,
+                                       fake, fake, fake, fake, None, fake, 1 << 30, None)
+    assert rc == -1 and b'power-of-two' in lib.svhip_last_error()
+    # attention: head_dim above 64 / not a multiple of 8, unknown K/V dtype, non-positive scale
+    base = [fake, fake, fake, fake]
+
+    def xattn(kv_dtype, D, scale):
+        sizes = [1, 1, 128, D, 64]                                # B, H, Q, D, kv_cap
+        strides = [128 * 64, 128 * 64, 64,                        # Q: b, h, q
+                   64 * 64, 64 * 64, 64,                          # K: b, h, key
+                   64 * 64, 64 * 64, 64, 1,                       # V: b, h, key, d
+                   128 * 64, 128 * 64, 64]                        # O: b, h, q
+        return lib.svhip_xattn_fwd(*base, kv_dtype, fake, None, None, None, *sizes, *strides, scale, None)
+
+    assert xattn(1, 96, 0.125) == -1 and b'head_dim' in lib.svhip_last_error()
+    assert xattn(1, 60, 0.125) == -1 and b'head_dim' in lib.svhip_last_error()
+    assert xattn(7, 64, 0.125) == -1 and b'dtype' in lib.svhip_last_error()
+    assert xattn(1, 64, -1.0) == -1 and b'scale' in lib.svhip_last_error()
+    assert xattn(3, 64, 0.125) == -1 and b'k_scale' in lib.svhip_last_error()
+    # the cache writer's workspace query grows with heads and capacity
+    assert lib.svhip_kv_write_workspace_bytes(16, 12672) >= lib.svhip_kv_write_workspace_bytes(8, 9792) > 0
