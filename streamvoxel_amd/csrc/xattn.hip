@@ -33,8 +33,9 @@
 // per-lane offset fixed for the window plus a scalar block offset. Every other form goes through registers,
 // prefetched one block ahead in its storage format and converted when it is written to LDS: OCP e4m3fn K/V
 // converted exactly to bf16 (v_cvt_scalef32_pk_bf16_fp8 with scale 1; the fp8 scales are folded into the softmax
-// scale (k_scale) and the output (v_scale)), row-major V transposed on the way, the packed cu_seqlens layout. The last, partial block of a window is peeled out of the
-// loop and staged synchronously through registers, keys >= L as zeros.
+// scale (k_scale) and the output (v_scale)), row-major V transposed on the way, the packed cu_seqlens layout.
+// The last, partial block of a window is peeled out of the loop and staged through registers (its loads issued
+// before the last full block is computed), keys >= L as zeros.
 //
 // Workgroup order: windows are ranked by key count (longest first, ties by index; up to kMaxRankWindows windows)
 // inside the kernel, so the longest (window, head) pairs start first; consecutive workgroup ids go round robin to
@@ -425,6 +426,8 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   uint32_t rd[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) rd[s] = static_cast<uint32_t>(col * kRow * 2 + swz(col, 2 * s + hh) * 16);
+  // 16-wide k-steps of the score product that head_dim reaches (4 at head_dim 64).
+  const int ksteps = STAGING == kDirect64 ? 4 : __builtin_amdgcn_readfirstlane(static_cast<int>((p.D + 15) / 16));
 
   f32x16_t o0 = {0}, o1 = {0};  // O^T tiles: d in [0,32) and [32,64)
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
@@ -462,12 +465,14 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
     const char* vp = reinterpret_cast<const char*>(Vt);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      // S^T of keys 32 t .. 32 t + 31 (LDS rows 32 t + col).
+      // S^T of keys 32 t .. 32 t + 31 (LDS rows 32 t + col); k-steps past head_dim (zero in Q) are skipped.
       f32x16_t s = {0};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(kp + rd[k] + t * (32 * kRow * 2));
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], s, 0, 0, 0);
+        if (k < ksteps) {
+          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(kp + rd[k] + t * (32 * kRow * 2));
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], s, 0, 0, 0);
+        }
       }
       if constexpr (MASKED) {
         // Entry i is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8).
