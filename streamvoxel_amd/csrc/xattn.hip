@@ -41,6 +41,11 @@
 // inside the kernel, so the longest (window, head) pairs start first; consecutive workgroup ids go round robin to
 // the 8 XCDs and all query tiles of one (window, head) pair land on the same XCD, which reads that pair's K/V into
 // its L2 once.
+//
+// Head widths: DT = 2, 3 or 4 output tiles of 32 head_dim elements (head_dim <= 64, 96, 128). A K block is DT / 2
+// rounded up 64 x 64 sub-tiles (head_dim 0..63 and 64..127 of every key, same layout and swizzle), V^T one tile of
+// 32 DT rows; the score product takes up to 2 DT k-steps, the second product DT accumulators. DT = 2 is the
+// 384-wide (8 x 48) and the 64-wide heads, DT = 3 the 768-wide model's 8 x 96.
 #include <type_traits>
 
 #include "common.hpp"
@@ -54,8 +59,10 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kQTile = 128;   // queries per workgroup
 constexpr int kKB = 64;       // keys per block
-constexpr int kDPad = 64;     // head_dim handled by the MFMA tiles (smaller head_dim is zero-padded)
+constexpr int kSub = 64;      // head_dim elements per K sub-tile row (smaller head_dim is zero-padded)
+constexpr int kMaxD = 128;    // widest head (DT = 4)
 constexpr int kRow = 64;      // LDS row stride in bf16 elements (128 bytes, 16-byte chunks XOR-swizzled)
+constexpr int kKTile = kKB * kRow;  // bf16 elements of one K sub-tile
 constexpr int kThreads = 256;
 constexpr float kSumHigh = 1048576.0f;  // 2^20: a half's row sum above it makes the running max be raised
 constexpr float kFltMax = 3.40282347e38f;
@@ -169,28 +176,40 @@ __device__ __forceinline__ uint4 to_bf16x8(const typename Raw<FP8>::type& r) {
   }
 }
 
-template <bool FP8, bool VT>
-struct Stage {
-  typename Raw<FP8>::type k[2];
-  typename Raw<FP8>::type v[2];
+// DT output tiles of 32 head_dim elements: K sub-tiles per block, and the per-thread chunk counts of one block
+// (a 64 x 64 K sub-tile is 512 chunks of 8 elements, two per thread; V^T takes 32 rows = 256 chunks per pass).
+template <int DT>
+struct Width {
+  static constexpr int kSubTiles = (DT + 1) / 2;
+  static constexpr int kKPasses = 2 * kSubTiles;
 };
 
-// Global -> registers for the key block starting at kv0: each thread moves 2 chunks of 8 elements of K and of V.
+template <bool FP8, bool VT, int DT>
+struct Stage {
+  typename Raw<FP8>::type k[Width<DT>::kKPasses];
+  typename Raw<FP8>::type v[VT ? DT : Width<DT>::kKPasses];
+};
+
+// Global -> registers for the key block starting at kv0. K pass r: sub-tile r / 2, chunk c = thread + 256 (r % 2)
+// (key c / 8, head_dim chunk 8 (r / 2) + c % 8); V^T pass r: rows 32 r .. 32 r + 31; row-major V as K.
 // TAIL: the block holds keys >= L (they are staged as zeros). vt_vec: V^T rows allow vector loads.
-template <bool FP8, bool VT, bool TAIL>
-__device__ __forceinline__ void stage_load(Stage<FP8, VT>& st, const XattnParams& p, const typename Elem<FP8>::T* K,
-                                           const typename Elem<FP8>::T* V, int L, int kv0, int dchunks,
-                                           bool vt_vec) {
+template <bool FP8, bool VT, int DT, bool TAIL>
+__device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnParams& p,
+                                           const typename Elem<FP8>::T* K, const typename Elem<FP8>::T* V, int L,
+                                           int kv0, int dchunks, bool vt_vec) {
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int c = threadIdx.x + kThreads * r;  // 0..511
-    {
-      const int key = c >> 3, dc = c & 7;
-      const int kg = kv0 + key;
-      const bool ok = dc < dchunks && (!TAIL || kg < L);
-      st.k[r] = ok ? load8_vec<FP8>(K + kg * p.sk_k + dc * 8) : raw_zero<FP8>();
-    }
-    if constexpr (VT) {
+  for (int r = 0; r < Width<DT>::kKPasses; ++r) {
+    const int c = threadIdx.x + kThreads * (r & 1);  // 0..511
+    const int key = c >> 3, dc = 8 * (r >> 1) + (c & 7);
+    const int kg = kv0 + key;
+    const bool ok = dc < dchunks && (!TAIL || kg < L);
+    st.k[r] = ok ? load8_vec<FP8>(K + kg * p.sk_k + dc * 8) : raw_zero<FP8>();
+    if constexpr (!VT) st.v[r] = ok ? load8_vec<FP8>(V + kg * p.sv_k + dc * 8) : raw_zero<FP8>();
+  }
+  if constexpr (VT) {
+#pragma unroll
+    for (int r = 0; r < DT; ++r) {
+      const int c = threadIdx.x + kThreads * r;
       const int d = c >> 3, kc = c & 7;
       const int kg = kv0 + kc * 8;
       const auto* src = V + d * p.sv_d + kg;
@@ -200,37 +219,37 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT>& st, const XattnParams
       } else {
         st.v[r] = raw_zero<FP8>();
       }
-    } else {
-      const int key = c >> 3, dc = c & 7;
-      const int kg = kv0 + key;
-      const bool ok = dc < dchunks && (!TAIL || kg < L);
-      st.v[r] = ok ? load8_vec<FP8>(V + kg * p.sv_k + dc * 8) : raw_zero<FP8>();
     }
   }
 }
 
-// Registers -> LDS (K rows under sigma; V as V^T [d][key]; both swizzled).
-template <bool FP8, bool VT>
-__device__ __forceinline__ void stage_store(const Stage<FP8, VT>& st, uint16_t* sK, uint16_t* sV) {
+// Registers -> LDS (K rows under sigma in their sub-tile; V as V^T [d][key]; both swizzled).
+template <bool FP8, bool VT, int DT>
+__device__ __forceinline__ void stage_store(const Stage<FP8, VT, DT>& st, uint16_t* sK, uint16_t* sV) {
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int c = threadIdx.x + kThreads * r;
-    {
-      const int R = sigma_row(c >> 3), dc = c & 7;
-      *reinterpret_cast<uint4*>(sK + R * kRow + swz(R, dc) * 8) = to_bf16x8<FP8>(st.k[r]);
-    }
-    if constexpr (VT) {
-      const int d = c >> 3, kc = c & 7;
-      *reinterpret_cast<uint4*>(sV + d * kRow + swz(d, kc) * 8) = to_bf16x8<FP8>(st.v[r]);
-    } else {
-      const int key = c >> 3, dc = c & 7;
+  for (int r = 0; r < Width<DT>::kKPasses; ++r) {
+    const int c = threadIdx.x + kThreads * (r & 1);
+    const int R = sigma_row(c >> 3), dc = c & 7;
+    *reinterpret_cast<uint4*>(sK + (r >> 1) * kKTile + R * kRow + swz(R, dc) * 8) = to_bf16x8<FP8>(st.k[r]);
+    if constexpr (!VT) {
+      const int key = c >> 3;
       const uint4 vb = to_bf16x8<FP8>(st.v[r]);
       const uint32_t w[4] = {vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int d = dc * 8 + e;
-        sV[d * kRow + swz(d, key >> 3) * 8 + (key & 7)] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+        const int d = kSub * (r >> 1) + dc * 8 + e;
+        if (d < 32 * DT) {
+          sV[d * kRow + swz(d, key >> 3) * 8 + (key & 7)] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+        }
       }
+    }
+  }
+  if constexpr (VT) {
+#pragma unroll
+    for (int r = 0; r < DT; ++r) {
+      const int c = threadIdx.x + kThreads * r;
+      const int d = c >> 3, kc = c & 7;
+      *reinterpret_cast<uint4*>(sV + d * kRow + swz(d, kc) * 8) = to_bf16x8<FP8>(st.v[r]);
     }
   }
 }
@@ -254,20 +273,25 @@ __device__ __forceinline__ int window_length(const XattnParams& p, int64_t b) {
 // descriptors bound the reads to the window's full blocks (an out-of-range read returns zeros).
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Instruction j of a K sub-tile or of V^T fills rows 8 j .. 8 j + 7; the 8 instructions of a K sub-tile go to the
+// 4 waves two each (w and w + 4), the 4 DT of V^T DT each (w + 4 t). Sub-tile 1 of K reads 64 elements further
+// along every key (added to the scalar offset: the immediate offset would move the LDS destination too).
+template <int DT>
 struct DirectLanes {
   __amdgpu_buffer_rsrc_t k_rsrc, v_rsrc;
-  uint32_t k[2];  // byte offsets of instructions w and w + 4 for the block at key 0
-  uint32_t v[2];
-  bool k_ok[2];   // the lane's K chunk lies inside head_dim
-  bool v_ok[2];   // the lane's V^T row lies inside head_dim
+  uint32_t k[2];   // byte offsets of K instructions w and w + 4 for the block at key 0
+  uint32_t v[DT];  // byte offsets of V^T instructions w + 4 t
+  bool k_ok[Width<DT>::kSubTiles][2];  // the lane's K chunk lies inside head_dim
+  bool v_ok[DT];                       // the lane's V^T row lies inside head_dim
 };
 
 // Raw buffer descriptor word 3 for 32-bit-element untyped access.
 constexpr int kRsrcFlags = 0x00020000;
 
-__device__ __forceinline__ DirectLanes direct_lanes(const XattnParams& p, const uint16_t* K, const uint16_t* V,
-                                                    int dchunks, int nfull, int w) {
-  DirectLanes dl;
+template <int DT>
+__device__ __forceinline__ DirectLanes<DT> direct_lanes(const XattnParams& p, const uint16_t* K, const uint16_t* V,
+                                                        int dchunks, int nfull, int w) {
+  DirectLanes<DT> dl;
   const int lane = threadIdx.x & 63;
   const uint32_t k_bytes = static_cast<uint32_t>(((static_cast<int64_t>(nfull) * kKB - 1) * p.sk_k + p.D) * 2);
   const uint32_t v_bytes = static_cast<uint32_t>(((p.D - 1) * p.sv_d + static_cast<int64_t>(nfull) * kKB) * 2);
@@ -278,27 +302,40 @@ __device__ __forceinline__ DirectLanes direct_lanes(const XattnParams& p, const 
     const int R = 8 * (w + 4 * t) + (lane >> 3);
     const int c = swz(R, lane & 7);  // swz is an involution in c
     dl.k[t] = static_cast<uint32_t>((sigma_row(R) * p.sk_k + 8 * c) * 2);
+#pragma unroll
+    for (int u = 0; u < Width<DT>::kSubTiles; ++u) dl.k_ok[u][t] = 8 * u + c < dchunks;
+  }
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const int R = 8 * (w + 4 * t) + (lane >> 3);
+    const int c = swz(R, lane & 7);
     dl.v[t] = static_cast<uint32_t>((R * p.sv_d + 8 * c) * 2);
-    dl.k_ok[t] = c < dchunks;
     dl.v_ok[t] = R < 8 * dchunks;
   }
   return dl;
 }
 
-// FULL_D: head_dim 64, every lane loads (no exec masking). w: the wave index (uniform).
-template <bool FULL_D>
-__device__ __forceinline__ void stage_direct(const DirectLanes& dl, uint32_t k_soff, uint32_t v_soff, int w,
+// FULL_D: head_dim = 32 DT, every lane of V^T and of K sub-tile 0 loads (no exec masking); sub-tile 1 at DT = 3
+// still masks head_dim 96..127. w: the wave index (uniform).
+template <int DT, bool FULL_D>
+__device__ __forceinline__ void stage_direct(const DirectLanes<DT>& dl, uint32_t k_soff, uint32_t v_soff, int w,
                                              uint16_t* sK, uint16_t* sV) {
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int j = w + 4 * t;
-    if (FULL_D || dl.k_ok[t]) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dl.k_rsrc, (lds_ptr_t)(sK + 512 * j), 16, dl.k[t],
-                                               k_soff, 0, 0);
+#pragma unroll
+    for (int u = 0; u < Width<DT>::kSubTiles; ++u) {
+      if ((FULL_D && 64 * (u + 1) <= 32 * DT) || dl.k_ok[u][t]) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(dl.k_rsrc, (lds_ptr_t)(sK + u * kKTile + 512 * j), 16, dl.k[t],
+                                                 k_soff + 2 * kSub * u, 0, 0);
+      }
     }
+  }
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const int j = w + 4 * t;
     if (FULL_D || dl.v_ok[t]) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dl.v_rsrc, (lds_ptr_t)(sV + 512 * j), 16, dl.v[t],
-                                               v_soff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dl.v_rsrc, (lds_ptr_t)(sV + 512 * j), 16, dl.v[t], v_soff, 0, 0);
     }
   }
 }
@@ -306,16 +343,17 @@ __device__ __forceinline__ void stage_direct(const DirectLanes& dl, uint32_t k_s
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // STAGING: kRegister (registers for every block), kDirect (direct loads for full blocks, any head_dim),
-// kDirect64 (the same at head_dim 64). The last, partial block of a window always goes through registers.
-enum Staging { kRegister = 0, kDirect = 1, kDirect64 = 2 };
+// kDirectFull (the same at head_dim 32 DT). The last, partial block of a window always goes through registers.
+enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2 };
 
-template <bool FP8, bool VT, int STAGING>
+template <bool FP8, bool VT, int STAGING, int DT>
 __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   constexpr bool DIRECT = STAGING != kRegister;
+  constexpr int kSubTiles = Width<DT>::kSubTiles;
   // Four distinct LDS objects (not one indexed array): the compiler can then tell the direct loads into one
   // buffer from the operand reads of the other and does not wait for the loads in flight before those reads.
-  __shared__ __attribute__((aligned(16))) uint16_t sK0[kKB * kRow], sK1[kKB * kRow];
-  __shared__ __attribute__((aligned(16))) uint16_t sV0[kDPad * kRow], sV1[kDPad * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t sK0[kSubTiles * kKTile], sK1[kSubTiles * kKTile];
+  __shared__ __attribute__((aligned(16))) uint16_t sV0[32 * DT * kRow], sV1[32 * DT * kRow];
   __shared__ int s_window;
 
   // Workgroup -> (rank, head, query tile): XCD x (= id % 8) takes the (rank, head) units x, x + 8, ... with all
@@ -387,9 +425,9 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   }
 
   // The wave's Q as B operands: k-step s covers d = 16 s + 8 hh + 0..7.
-  bf16x8_t qf[4];
+  bf16x8_t qf[2 * DT];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < 2 * DT; ++s) {
     const int d0 = 16 * s + 8 * hh;
     uint4 raw = make_uint4(0u, 0u, 0u, 0u);
     if (q_ok && d0 < p.D) raw = *reinterpret_cast<const uint4*>(Qp + q * p.sq_q + d0);
@@ -405,17 +443,19 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   const int nfull = L / kKB;           // full key blocks
   const bool tail = nfull * kKB < L;   // plus one partial block
 
-  DirectLanes dl;
+  DirectLanes<DT> dl;
   if constexpr (DIRECT) {
-    dl = direct_lanes(p, reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V), dchunks, nfull,
+    dl = direct_lanes<DT>(p, reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V), dchunks, nfull,
                       w);
-    if (STAGING == kDirect && dchunks < 8) {
-      // Chunks past head_dim of both K tiles are never loaded by direct loads; they must hold zeros.
-      for (int i = threadIdx.x; i < kKB * 8; i += kThreads) {
-        const int R = i >> 3, c = i & 7;
-        if (c >= dchunks) {
-          *reinterpret_cast<uint4*>(sK0 + R * kRow + swz(R, c) * 8) = make_uint4(0u, 0u, 0u, 0u);
-          *reinterpret_cast<uint4*>(sK1 + R * kRow + swz(R, c) * 8) = make_uint4(0u, 0u, 0u, 0u);
+    if (STAGING == kDirect && dchunks < 4 * DT) {
+      // Chunks past head_dim of the K tiles that the score product reads are never loaded by direct loads; they
+      // must hold zeros.
+      for (int i = threadIdx.x; i < kSubTiles * kKB * 8; i += kThreads) {
+        const int u = i / (kKB * 8), R = (i >> 3) % kKB, c = i & 7;
+        if (8 * u + c >= dchunks) {
+          const int e = u * kKTile + R * kRow + swz(R, c) * 8;
+          *reinterpret_cast<uint4*>(sK0 + e) = make_uint4(0u, 0u, 0u, 0u);
+          *reinterpret_cast<uint4*>(sK1 + e) = make_uint4(0u, 0u, 0u, 0u);
         }
       }
     }
@@ -426,33 +466,36 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   uint32_t rd[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) rd[s] = static_cast<uint32_t>(col * kRow * 2 + swz(col, 2 * s + hh) * 16);
-  // 16-wide k-steps of the score product that head_dim reaches (4 at head_dim 64).
-  const int ksteps = STAGING == kDirect64 ? 4 : __builtin_amdgcn_readfirstlane(static_cast<int>((p.D + 15) / 16));
+  // 16-wide k-steps of the score product that head_dim reaches (2 DT at head_dim 32 DT).
+  const int ksteps =
+      STAGING == kDirectFull ? 2 * DT : __builtin_amdgcn_readfirstlane(static_cast<int>((p.D + 15) / 16));
 
-  f32x16_t o0 = {0}, o1 = {0};  // O^T tiles: d in [0,32) and [32,64)
+  f32x16_t o[DT];  // O^T tiles: d in [32 j, 32 j + 32)
+#pragma unroll
+  for (int j = 0; j < DT; ++j) o[j] = f32x16_t{0};
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
   float l = 0.f;                // row-sum partial of this lane's keys
 
   // Full block `blk` into (sK, sV): issued now, complete at the next vmem wait (direct) or at `stage_commit`
   // (registers, prefetched into `st`).
-  Stage<FP8, VT> st;
+  Stage<FP8, VT, DT> st;
   auto stage_issue = [&](int blk, uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
     if constexpr (DIRECT) {
       const int kv0 = blk * kKB;
-      stage_direct<STAGING == kDirect64>(dl, static_cast<uint32_t>(kv0 * p.sk_k * 2), static_cast<uint32_t>(kv0 * 2),
+      stage_direct<DT, STAGING == kDirectFull>(dl, static_cast<uint32_t>(kv0 * p.sk_k * 2), static_cast<uint32_t>(kv0 * 2),
                                          w, sK, sV);
     } else {
-      stage_load<FP8, VT, false>(st, p, K, V, L, blk * kKB, dchunks, vt_vec);
+      stage_load<FP8, VT, DT, false>(st, p, K, V, L, blk * kKB, dchunks, vt_vec);
     }
   };
   auto stage_commit = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
-    if constexpr (!DIRECT) stage_store<FP8, VT>(st, sK, sV);
+    if constexpr (!DIRECT) stage_store<FP8, VT, DT>(st, sK, sV);
   };
   // The partial block, synchronously through registers.
   auto stage_tail = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
-    Stage<FP8, VT> tmp;
-    stage_load<FP8, VT, true>(tmp, p, K, V, L, nfull * kKB, dchunks, vt_vec);
-    stage_store<FP8, VT>(tmp, sK, sV);
+    Stage<FP8, VT, DT> tmp;
+    stage_load<FP8, VT, DT, true>(tmp, p, K, V, L, nfull * kKB, dchunks, vt_vec);
+    stage_store<FP8, VT, DT>(tmp, sK, sV);
   };
 
 
@@ -468,9 +511,10 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
       // S^T of keys 32 t .. 32 t + 31 (LDS rows 32 t + col); k-steps past head_dim (zero in Q) are skipped.
       f32x16_t s = {0};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < 2 * DT; ++k) {
         if (k < ksteps) {
-          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(kp + rd[k] + t * (32 * kRow * 2));
+          const bf16x8_t a =
+              *reinterpret_cast<const bf16x8_t*>(kp + (k >> 2) * (kKTile * 2) + rd[k & 3] + t * (32 * kRow * 2));
           s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], s, 0, 0, 0);
         }
       }
@@ -529,19 +573,21 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
         l *= alpha;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          o0[i] *= alpha;
-          o1[i] *= alpha;
+#pragma unroll
+          for (int j = 0; j < DT; ++j) o[j][i] *= alpha;
         }
         exps(-m);
       }
       l += lb;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        // O^T += V^T . P^T for this k-step: V^T columns 32 t + 16 ks + 8 hh + 0..7 are logical chunk 2 (2 t + ks) + hh.
-        const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(vp + rd[2 * t + ks]);
-        const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(vp + rd[2 * t + ks] + 32 * kRow * 2);
-        o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pb[ks], o0, 0, 0, 0);
-        o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pb[ks], o1, 0, 0, 0);
+        // O^T += V^T . P^T for this k-step: V^T columns 32 t + 16 ks + 8 hh + 0..7 are logical chunk 2 (2 t + ks) + hh
+        // of rows 32 j + col.
+        bf16x8_t a[DT];
+#pragma unroll
+        for (int j = 0; j < DT; ++j) a[j] = *reinterpret_cast<const bf16x8_t*>(vp + rd[2 * t + ks] + j * (32 * kRow * 2));
+#pragma unroll
+        for (int j = 0; j < DT; ++j) o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], pb[ks], o[j], 0, 0, 0);
       }
     }
   };
@@ -584,11 +630,11 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
     if (nfull > 0) {
       // The partial block's loads are in flight during the last full block (the other tiles are free since the
       // last barrier).
-      Stage<FP8, VT> tl;
-      if (tail) stage_load<FP8, VT, true>(tl, p, K, V, L, nfull * kKB, dchunks, vt_vec);
+      Stage<FP8, VT, DT> tl;
+      if (tail) stage_load<FP8, VT, DT, true>(tl, p, K, V, L, nfull * kKB, dchunks, vt_vec);
       compute(Full{}, cK, cV, blk * kKB);
       if (tail) {
-        stage_store<FP8, VT>(tl, nK, nV);
+        stage_store<FP8, VT, DT>(tl, nK, nV);
         wait_vmem();
         __syncthreads();
         compute(Partial{}, nK, nV, nfull * kKB);
@@ -607,14 +653,14 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   if (q_ok) {
     // O^T entry i of tile t: d = 32 t + 8 (i / 4) + 4 hh + i % 4 ; four consecutive d per group.
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < DT; ++t) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         const int d0 = 32 * t + 8 * g4 + 4 * hh;
         if (d0 < p.D) {
           float vals[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) vals[e] = (t == 0 ? o0[4 * g4 + e] : o1[4 * g4 + e]) * inv;
+          for (int e = 0; e < 4; ++e) vals[e] = o[t][4 * g4 + e] * inv;
           f32x2_t a = {vals[0], vals[1]}, c = {vals[2], vals[3]};
           const bf16x2_t ba = __builtin_convertvector(a, bf16x2_t);
           const bf16x2_t bc = __builtin_convertvector(c, bf16x2_t);
@@ -625,6 +671,27 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
         }
       }
     }
+  }
+}
+
+// The instantiation for DT = head_dim / 32 rounded up: e4m3 and row-major forms through registers, bf16 V^T
+// directly to LDS (head_dim 32 DT without exec masking).
+template <int DT>
+void launch(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool vt, bool direct) {
+  if (fp8) {
+    if (vt) {
+      xattn_fwd_kernel<true, true, kRegister, DT><<<g, kThreads, 0, s>>>(p);
+    } else {
+      xattn_fwd_kernel<true, false, kRegister, DT><<<g, kThreads, 0, s>>>(p);
+    }
+  } else if (direct && p.D == 32 * DT) {
+    xattn_fwd_kernel<false, true, kDirectFull, DT><<<g, kThreads, 0, s>>>(p);
+  } else if (direct) {
+    xattn_fwd_kernel<false, true, kDirect, DT><<<g, kThreads, 0, s>>>(p);
+  } else if (vt) {
+    xattn_fwd_kernel<false, true, kRegister, DT><<<g, kThreads, 0, s>>>(p);
+  } else {
+    xattn_fwd_kernel<false, false, kRegister, DT><<<g, kThreads, 0, s>>>(p);
   }
 }
 
@@ -643,8 +710,8 @@ extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void
   SVHIP_REQUIRE(q && k && v && o, "%s: null pointer", name);
   SVHIP_REQUIRE(kv_len || cu_seqlens, "%s: need kv_len or cu_seqlens", name);
   SVHIP_REQUIRE(B >= 0 && H >= 1 && Q >= 0, "%s: bad sizes", name);
-  SVHIP_REQUIRE(D >= 8 && D <= kDPad && D % 8 == 0, "%s: head_dim %lld unsupported (multiple of 8, <= 64)", name,
-                (long long)D);
+  SVHIP_REQUIRE(D >= 8 && D <= kMaxD && D % 8 == 0, "%s: head_dim %lld unsupported (multiple of 8, <= %d)", name,
+                (long long)D, kMaxD);
   SVHIP_REQUIRE(scale > 0.f && scale < 3.0e38f, "%s: softmax scale must be positive and finite", name);
   SVHIP_REQUIRE(kv_dtype == SVHIP_BF16 || kv_dtype == SVHIP_FP8_E4M3, "%s: kv dtype %d unsupported", name, kv_dtype);
   const bool fp8 = kv_dtype == SVHIP_FP8_E4M3;
@@ -708,20 +775,12 @@ extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void
                       (D * sv_d + kv_cap) * 2 < (1ll << 32);
   hipStream_t s = as_stream(stream);
   const unsigned g = static_cast<unsigned>(grid);
-  if (fp8) {
-    if (vt) {
-      xattn_fwd_kernel<true, true, kRegister><<<g, kThreads, 0, s>>>(p);
-    } else {
-      xattn_fwd_kernel<true, false, kRegister><<<g, kThreads, 0, s>>>(p);
-    }
-  } else if (direct && D == kDPad) {
-    xattn_fwd_kernel<false, true, kDirect64><<<g, kThreads, 0, s>>>(p);
-  } else if (direct) {
-    xattn_fwd_kernel<false, true, kDirect><<<g, kThreads, 0, s>>>(p);
-  } else if (vt) {
-    xattn_fwd_kernel<false, true, kRegister><<<g, kThreads, 0, s>>>(p);
+  if (D <= 64) {
+    launch<2>(p, g, s, fp8, vt, direct);
+  } else if (D <= 96) {
+    launch<3>(p, g, s, fp8, vt, direct);
   } else {
-    xattn_fwd_kernel<false, false, kRegister><<<g, kThreads, 0, s>>>(p);
+    launch<4>(p, g, s, fp8, vt, direct);
   }
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;

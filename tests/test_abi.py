@@ -78,7 +78,7 @@ def test_argument_errors_of_the_newer_entry_points(lib):
     rc = lib.svhip_ease_select_patches(fake, 0, 256, 3, 0, 256, fake, 256, fake, 1, 256, 16, 16, 4, fake, fake, fake,
                                        fake, fake, fake, fake, None, fake, 1 << 30, None)
     assert rc == -1 and b'power-of-two' in lib.svhip_last_error()
-    # attention: head_dim above 64 / not a multiple of 8, unknown K/V dtype, non-positive scale
+    # attention: head_dim above 128 / not a multiple of 8, unknown K/V dtype, non-positive scale
     base = [fake, fake, fake, fake]
 
     def xattn(kv_dtype, D, scale):
@@ -89,7 +89,7 @@ def test_argument_errors_of_the_newer_entry_points(lib):
                    128 * 64, 128 * 64, 64]                        # O: b, h, q
         return lib.svhip_xattn_fwd(*base, kv_dtype, fake, None, None, None, *sizes, *strides, scale, None)
 
-    assert xattn(1, 96, 0.125) == -1 and b'head_dim' in lib.svhip_last_error()
+    assert xattn(1, 136, 0.125) == -1 and b'head_dim' in lib.svhip_last_error()
     assert xattn(1, 60, 0.125) == -1 and b'head_dim' in lib.svhip_last_error()
     assert xattn(7, 64, 0.125) == -1 and b'dtype' in lib.svhip_last_error()
     assert xattn(1, 64, -1.0) == -1 and b'scale' in lib.svhip_last_error()

@@ -45,7 +45,7 @@ def check(got, ref, atol, rtol=None):
         assert err / ref.abs().max().item() <= rtol, (err, ref.abs().max().item())
 
 
-@pytest.mark.parametrize('D', [64, 48])
+@pytest.mark.parametrize('D', [64, 48, 96, 128, 72])
 def test_padded_variable_lengths(dev, D):
     from streamvoxel_amd.stream.attention import attention
     B, H, Q, kcap = 4, 3, 200, 700
@@ -76,12 +76,13 @@ def test_zero_length_window_gives_zeros_and_padding_is_ignored(dev):
     assert torch.equal(out1, out2)
 
 
-def test_packed_cu_seqlens_and_transposed_v(dev):
+@pytest.mark.parametrize('D', [64, 96])
+def test_packed_cu_seqlens_and_transposed_v(dev, D):
     from streamvoxel_amd.stream.attention import attention
-    H, Q, D = 4, 130, 64
+    H, Q = 4, 130
     lengths = [1552, 37, 1024 * 3 + 1552, 65]
     B = len(lengths)
-    _case(f'xattn packed cu_seqlens lengths={lengths}')
+    _case(f'xattn packed cu_seqlens D={D} lengths={lengths}')
     g = torch.Generator().manual_seed(4)
     total = sum(lengths)
     kp = (torch.randn(H, total, D, generator=g) / 8).to(torch.bfloat16)
@@ -134,13 +135,34 @@ def test_config_c2_shape_one_layer(dev):
     check(out.cpu()[:, sel_h, ::7], ref, BF16_ATOL, BF16_RTOL)
 
 
-def test_fp8_e4m3_cached_kv(dev):
+def test_768_wide_model_shape_direct_vt(dev):
+    """The 768-wide model's cross-attention: 8 windows, 8 heads x 96, 1024 queries, up to 12 576 keys in a
+    12 672-key cache with V stored transposed (direct staging at head_dim 96); a subset of heads and queries
+    checked against float64."""
+    from streamvoxel_amd.stream.attention import attention
+    g = torch.Generator().manual_seed(321)
+    kb = torch.randint(0, 9, (8,), generator=g)
+    lengths = (256 * 16 + 288 + 1024 * kb).tolist()
+    B, H, Q, D, kcap = 8, 8, 1024, 96, 12672
+    _case(f'xattn 768-wide D=96 lengths={lengths}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=77)
+    vt = v.transpose(2, 3).contiguous().to(dev)
+    out = attention(q.to(dev), k.to(dev), vt.transpose(2, 3),
+                    lengths=torch.tensor(lengths, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    sel_h = [0, 7]
+    ref = A.cross_attention(q[:, sel_h, ::9], k[:, sel_h], v[:, sel_h], lengths)
+    check(out.cpu()[:, sel_h, ::9], ref, BF16_ATOL, BF16_RTOL)
+
+
+@pytest.mark.parametrize('D', [64, 96, 128])
+def test_fp8_e4m3_cached_kv(dev, D):
     from streamvoxel_amd.stream.attention import attention, quantize_e4m3
     if not hasattr(torch, 'float8_e4m3fn'):
         pytest.skip('torch without float8_e4m3fn')
-    B, H, Q, kcap, D = 3, 4, 256, 1100, 64
+    B, H, Q, kcap = 3, 4, 256, 1100
     lengths = [1100, 517, 64]
-    _case('xattn fp8 e4m3 K/V')
+    _case(f'xattn fp8 e4m3 K/V D={D}')
     q, k, v = make_qkv(B, H, Q, kcap, D, seed=5)
     kc, ks = quantize_e4m3(k.float())
     vc, vs = quantize_e4m3(v.float())
@@ -184,7 +206,7 @@ def test_fp8_decode_is_exact_for_every_code(dev):
     assert torch.equal(got, expect), (got - expect).abs().max()
 
 
-@pytest.mark.parametrize('D', [64, 48])
+@pytest.mark.parametrize('D', [64, 48, 96, 128, 88, 112])
 def test_transposed_v_padded_layout_fast_path(dev, D):
     """V stored transposed in a padded [B,H,D,Kcap] buffer (the cached-context layout) takes the direct-to-LDS
     staging: full blocks, a partial last block, a window shorter than one block; NaN in the padding must not
@@ -209,15 +231,15 @@ def test_transposed_v_padded_layout_fast_path(dev, D):
     assert torch.equal(out_direct, out_rows)
 
 
-@pytest.mark.parametrize('transposed', [True, False])
-def test_score_scale_jumps_between_key_halves(dev, transposed):
+@pytest.mark.parametrize('transposed,D', [(True, 64), (False, 64), (True, 96)])
+def test_score_scale_jumps_between_key_halves(dev, transposed, D):
     """Score magnitudes that jump up and down between 32-key halves (K rows scaled by 1 .. 90 and down to 1e-3):
     the running max must be raised mid-window (after lower halves) and hold through much lower halves, on the
     direct (V^T) and the register-staged path; the windows end inside a half, on a half and inside a block."""
     from streamvoxel_amd.stream.attention import attention
-    B, H, Q, kcap, D = 3, 2, 96, 640, 64
+    B, H, Q, kcap = 3, 2, 96, 640
     lengths = [640, 333, 47]
-    _case(f'xattn score jumps transposed={transposed} lengths={lengths}')
+    _case(f'xattn score jumps transposed={transposed} D={D} lengths={lengths}')
     q, k, v = make_qkv(B, H, Q, kcap, D, seed=29)
     factors = torch.tensor([1.0, 30.0, 0.01, 90.0, 2.0, 0.3, 60.0, 0.001])
     half = torch.arange(kcap) // 32
