@@ -142,7 +142,8 @@ int svhip_ease_select_patches(const void* logits, int dtype, int64_t classes, in
  * head_dim, the reference layout) or sv_k == 1 (V stored transposed, keys contiguous: the fast staging path);
  * row = j, or cu_seqlens[b] + j in the packed layout (sk_b / sv_b are then ignored). kv_dtype SVHIP_BF16, or
  * SVHIP_FP8_E4M3 (OCP e4m3fn bytes) with per-(window, head) fp32 dequantisation scales k_scale/v_scale [B,H].
- * head_dim: a multiple of 8 up to 64 (48 and below are zero-padded to 64 inside the kernel). fp32 accumulation.
+ * head_dim: a multiple of 8 up to 128 (zero-padded inside the kernel to 64, 96 or 128: the 384-wide model's 48,
+ * the 768-wide model's 96). fp32 accumulation.
  * scale: the softmax scale, > 0 (the reference uses 1/sqrt(head_dim)).
  * Replaces: flex_attention over PackedKeys' block mask in cross_flex (streamvoxel/stream/fast_ops.py:104-108,
  * 122-159) and the masked SDPA in SlotCrossAttention.forward / cross_sdpa (streamvoxel/stream/engine.py:28-47,
@@ -187,6 +188,37 @@ int svhip_kv_write(const void* prefix_k, const void* prefix_v, int64_t P, int64_
                    const float* freq, int64_t H, int64_t D, void* cache_k, int64_t sck_h, int64_t sck_k,
                    void* cache_v, int64_t scv_h, int64_t scv_k, int64_t scv_d, int64_t kv_cap, int kv_dtype,
                    float* k_scale, float* v_scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Self-attention operands of a transformer block from its fused qkv projection: qkv bf16, element (b,n,s,h,d)
+ * (s = 0 Q, 1 K, 2 V; the Linear's [3, H, D] row) at b*sx_b + n*sx_n + (s*H + h)*D + d, rows 16-byte aligned.
+ * Q and K are rotated by AxialRoPE at positions [B,N,3] fp32 (element (b,n,t) at b*sp_b + n*sp_n + t) with freq
+ * [D/6] exactly as svhip_axial_rope does, and written to q / k (element (b,h,n,d) at b*s?_b + h*s?_h + n*s?_n + d;
+ * they may be the Q / K slices of qkv itself: in place); V is written transposed to vt (element (b,h,d,n) at
+ * b*svt_b + h*svt_h + d*svt_d + n, 16-byte aligned rows), the layout svhip_xattn_fwd stages directly into LDS.
+ * head_dim: a multiple of 24 up to 128 (48 and 96 in the shipped models).
+ * Replaces: the qkv split, the two AxialRoPE calls and the layout change before F.scaled_dot_product_attention in
+ * RotaryAttention.forward (streamvoxel/models/unconditional_md4_timefree.py:41-47, unconditional_md4.py:35-41).
+ */
+int svhip_qkv_rope(const void* qkv, const float* positions, const float* freq, int64_t B, int64_t N, int64_t H,
+                   int64_t D, int64_t sx_b, int64_t sx_n, int64_t sp_b, int64_t sp_n, void* q, int64_t sq_b,
+                   int64_t sq_h, int64_t sq_n, void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, void* vt,
+                   int64_t svt_b, int64_t svt_h, int64_t svt_d, void* stream);
+
+/*
+ * LayerNorm over the last axis of bf16 rows, with the AdaLN modulation fused in:
+ *   y = LN(x) * (1 + scale[b]) + shift[b],   LN(x) = (x - mean) / sqrt(var + eps) * weight + bias
+ * x, y bf16 [B,N,W] (element (b,n,c) at b*s?_b + n*s?_n + c, 16-byte aligned rows; y may be x). weight / bias fp32
+ * [W] or NULL (no affine; bias needs weight); shift / scale bf16 [B,W] (rows s_mod apart) or both NULL (no
+ * modulation). Mean and biased variance in fp32; 1 + scale rounded to bf16 (as the reference's bf16 tensors
+ * compute it); y rounded once. W: a multiple of 8 up to 2048.
+ * Replaces: modulate(norm1(x), s1, c1) / modulate(norm2(x), s2, c2) of UnconditionalBlock.forward
+ * (streamvoxel/models/unconditional_md4_timefree.py:12-13,60-63) and norm1 / norm2 of the affine block
+ * (streamvoxel/models/unconditional_md4.py:44-56).
+ */
+int svhip_layer_norm(const void* x, void* y, const float* weight, const float* bias, const void* shift,
+                     const void* scale, int64_t B, int64_t N, int64_t W, int64_t sx_b, int64_t sx_n, int64_t sy_b,
+                     int64_t sy_n, int64_t s_mod, float eps, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,9 @@ Modules (each function cites the reference file:line it restates):
   attention.py  masked scaled-dot-product cross attention over per-slot key lengths (fp64 / fp32).
   producer.py   AxialRoPE, the cached-context window layout and the e4m3 cache quantisation.
   patches.py    the class head's patch order turned into [n, C, Y, Z, X] (explicit loops).
-  selftest.py   the fixed checks that pin each function (closed forms, brute force, invariants).
+  backbone.py   the transformer block (LayerNorm, AdaLN modulation, GELU, rotary self-attention, MLP) in float64.
+The checks that pin each function (closed forms, brute force, invariants, golden vectors) are the tests named
+tests/test_oracle*.py.
 
 Parity status per function (what pins it):
   entropy_scores_f64 / entropy_scores   closed forms (uniform -> -ln C, one-hot -> 0, two-class analytic), shift
@@ -31,4 +33,9 @@ Parity status per function (what pins it):
   producer.axial_rope / rope_frequencies golden vectors written by the reference's AxialRoPE; known answers.
   producer.window_kv / quantize_e4m3    layout and format invariants.
   patches.to_class_major                loops against torch's permute of the reference's form; the 4^3 block order.
+  backbone.layer_norm / gelu / silu     invariants (zero mean, var / (var + eps)), known values (Phi(1), sigmoid(1)),
+                                        odd-part identities.
+  backbone.rotary_attention / block     closed forms: uniform scores -> proj(mean V), one token -> proj(v), zero
+                                        positions -> brute-force attention, zero gates -> identity, unit gates with a
+                                        zero MLP -> x + attn + bias.
 """

@@ -50,6 +50,10 @@ SIGNATURES = {
                                       _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64,
                                       _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_p, _c_p, _c_p,
                                       _c_sz, _c_p]),
+    'svhip_qkv_rope': (ctypes.c_int, [_c_p, _c_p, _c_p] + [_c_i64] * 8 + [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
+                                                                       _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
+                                                                       _c_p]),
+    'svhip_layer_norm': (ctypes.c_int, [_c_p] * 6 + [_c_i64] * 8 + [_c_f, _c_p]),
 }
 
 _lib = None

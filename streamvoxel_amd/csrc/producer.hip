@@ -10,6 +10,9 @@
 //    positions are given), zeros up to the capacity; K as rows [H, Kcap, D], V as rows or transposed
 //    [H, D, Kcap]. bf16, or OCP e4m3fn with per-head scales amax / 448 (clamped below at 1e-12) over the window's
 //    keys and codes round-to-nearest-even of x / scale.
+//  * svhip_qkv_rope: the self-attention operands of RotaryAttention.forward (models/unconditional_md4_timefree.py:
+//    41-47) from the fused qkv projection's rows [3, H, D]: Q and K rotated as svhip_axial_rope does (in place or
+//    to their own strides), V written transposed [H, D, N] so the attention kernel stages it straight to LDS.
 //
 // HBM-bound, once per window (K/V) or once per layer and step (Q); one thread per bf16 pair.
 #include "common.hpp"
@@ -247,6 +250,84 @@ __global__ __launch_bounds__(kProducerThreads) void kv_write_kernel(KvArgs a) {
   }
 }
 
+
+// Self-attention operands from the qkv projection. Workgroup = (window b, head h, 64-token tile). Q and K pairs of
+// the tile are rotated one per thread and iteration (consecutive threads on consecutive pairs of a token's head);
+// V goes through LDS: 16-byte row loads of [64 tokens, D] in, 16-byte V^T row stores of [D, 64 tokens] out.
+struct QkvArgs {
+  const uint16_t* x;   // element (b, n, s, h, d) at b*sxb + n*sxn + (s*H + h)*D + d
+  const float* pos;    // (b, n, axis) at b*spb + n*spn + axis
+  const float* freq;   // [D/6]
+  uint16_t *q, *k, *vt;
+  int64_t B, N, H, D;
+  int64_t sxb, sxn, spb, spn;
+  int64_t sqb, sqh, sqn, skb, skh, skn;
+  int64_t svb, svh, svd;  // V^T element (b, h, d, n) at b*svb + h*svh + d*svd + n
+  int64_t tiles;          // token tiles per window
+};
+
+constexpr int kQkvTokens = 64;
+constexpr int kQkvRow = kQkvTokens + 2;  // LDS V^T row stride (bf16 elements), padded against bank conflicts
+
+__global__ __launch_bounds__(kProducerThreads) void qkv_rope_kernel(QkvArgs a) {
+  __shared__ uint16_t sv[kMaxHeadDim * kQkvRow];
+  const int64_t tile = blockIdx.x % a.tiles;
+  const int64_t bh = blockIdx.x / a.tiles;
+  const int64_t h = bh % a.H, b = bh / a.H;
+  const int64_t n0 = tile * kQkvTokens;
+  const int tokens = static_cast<int>(a.N - n0 < kQkvTokens ? a.N - n0 : kQkvTokens);
+  const int pairs = static_cast<int>(a.D / 2);
+  const int per_axis = static_cast<int>(a.D / 6);
+  const int D = static_cast<int>(a.D);
+  const uint16_t* xb = a.x + b * a.sxb + n0 * a.sxn;
+
+  // V rows -> LDS, transposed: sv[d][token].
+  const int chunks = tokens * (D / 8);
+  for (int c = threadIdx.x; c < chunks; c += kProducerThreads) {
+    const int t = c / (D / 8), dc = c % (D / 8);
+    const uint4 w = *reinterpret_cast<const uint4*>(xb + t * a.sxn + (2 * a.H + h) * a.D + 8 * dc);
+    const uint32_t e[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sv[(8 * dc + j) * kQkvRow + t] = static_cast<uint16_t>(e[j >> 1] >> (16 * (j & 1)));
+  }
+
+  // Q and K: rotate every pair of the tile.
+  const int qk_pairs = 2 * tokens * pairs;
+  for (int i = threadIdx.x; i < qk_pairs; i += kProducerThreads) {
+    const int s = i / (tokens * pairs);  // 0 = Q, 1 = K
+    const int r = i - s * tokens * pairs;
+    const int t = r / pairs, pr = r - t * pairs;
+    const int axis = pr / per_axis, fi = pr - axis * per_axis;
+    const int64_t n = n0 + t;
+    const float phase = a.pos[b * a.spb + n * a.spn + axis] * a.freq[fi];
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(xb + t * a.sxn + (s * a.H + h) * a.D + 2 * pr);
+    float x0, x1, r0, r1;
+    unpack2(w, x0, x1);
+    rope_pair(x0, x1, phase, r0, r1);
+    uint16_t* dst = s == 0 ? a.q + b * a.sqb + h * a.sqh + n * a.sqn : a.k + b * a.skb + h * a.skh + n * a.skn;
+    *reinterpret_cast<uint32_t*>(dst + 2 * pr) = pack2(r0, r1);
+  }
+  __syncthreads();
+
+  // V^T rows: d-th row of the tile = tokens n0 .. n0 + tokens - 1, 8 per 16-byte store.
+  uint16_t* vt = a.vt + b * a.svb + h * a.svh + n0;
+  const int tchunks = (tokens + 7) / 8;
+  for (int c = threadIdx.x; c < D * tchunks; c += kProducerThreads) {
+    const int d = c / tchunks, tc = c % tchunks;
+    const uint16_t* src = sv + d * kQkvRow + 8 * tc;
+    if (8 * tc + 8 <= tokens) {
+      uint4 w;
+      w.x = src[0] | (static_cast<uint32_t>(src[1]) << 16);
+      w.y = src[2] | (static_cast<uint32_t>(src[3]) << 16);
+      w.z = src[4] | (static_cast<uint32_t>(src[5]) << 16);
+      w.w = src[6] | (static_cast<uint32_t>(src[7]) << 16);
+      *reinterpret_cast<uint4*>(vt + d * a.svd + 8 * tc) = w;
+    } else {
+      for (int j = 0; 8 * tc + j < tokens; ++j) vt[d * a.svd + 8 * tc + j] = src[j];
+    }
+  }
+}
+
 }  // namespace svhip
 
 using namespace svhip;
@@ -339,6 +420,37 @@ extern "C" int svhip_kv_write(const void* prefix_k, const void* prefix_v, int64_
   } else {
     kv_write_kernel<false, false><<<grid, kProducerThreads, 0, s>>>(a);
   }
+  SVHIP_LAUNCHED(name);
+  return SVHIP_OK;
+}
+
+extern "C" int svhip_qkv_rope(const void* qkv, const float* positions, const float* freq, int64_t B, int64_t N,
+                              int64_t H, int64_t D, int64_t sx_b, int64_t sx_n, int64_t sp_b, int64_t sp_n, void* q,
+                              int64_t sq_b, int64_t sq_h, int64_t sq_n, void* k, int64_t sk_b, int64_t sk_h,
+                              int64_t sk_n, void* vt, int64_t svt_b, int64_t svt_h, int64_t svt_d, void* stream) {
+  const char* name = "svhip_qkv_rope";
+  clear_error();
+  SVHIP_REQUIRE(qkv && positions && freq && q && k && vt, "%s: null pointer", name);
+  SVHIP_REQUIRE(B >= 0 && N >= 0 && H >= 1, "%s: bad sizes", name);
+  SVHIP_REQUIRE(D >= 24 && D <= kMaxHeadDim && D % 24 == 0,
+                "%s: head_dim %lld unsupported (a multiple of 24 up to %d: three even axes, 16-byte rows)", name,
+                (long long)D, kMaxHeadDim);
+  auto aligned16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  SVHIP_REQUIRE(aligned16(qkv) && sx_b % 8 == 0 && sx_n % 8 == 0, "%s: qkv rows must start on 16-byte boundaries",
+                name);
+  SVHIP_REQUIRE(reinterpret_cast<uintptr_t>(q) % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 4 == 0 &&
+                    sq_b % 2 == 0 && sq_h % 2 == 0 && sq_n % 2 == 0 && sk_b % 2 == 0 && sk_h % 2 == 0 &&
+                    sk_n % 2 == 0,
+                "%s: Q/K rows must start on 4-byte boundaries (head_dim contiguous)", name);
+  SVHIP_REQUIRE(aligned16(vt) && svt_b % 8 == 0 && svt_h % 8 == 0 && svt_d % 8 == 0,
+                "%s: V^T rows must start on 16-byte boundaries", name);
+  if (B == 0 || N == 0) return SVHIP_OK;
+  QkvArgs a{static_cast<const uint16_t*>(qkv), positions, freq, static_cast<uint16_t*>(q), static_cast<uint16_t*>(k),
+            static_cast<uint16_t*>(vt), B, N, H, D, sx_b, sx_n, sp_b, sp_n, sq_b, sq_h, sq_n, sk_b, sk_h, sk_n,
+            svt_b, svt_h, svt_d, cdiv(N, kQkvTokens)};
+  const int64_t grid = B * H * a.tiles;
+  SVHIP_REQUIRE(grid < (1ll << 31), "%s: grid too large", name);
+  qkv_rope_kernel<<<static_cast<unsigned>(grid), kProducerThreads, 0, as_stream(stream)>>>(a);
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;
 }

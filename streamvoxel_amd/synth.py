@@ -44,3 +44,64 @@ def high_entropy_share(step, steps, start=0.30, end=0.05):
     if steps <= 1:
         return start
     return start + (end - start) * step / (steps - 1)
+
+
+def patch_positions(voxel_shape=(256, 16, 16), patch=4):
+    """Self-attention positions of a window's patch tokens, fp32 [N, 3] in XYZ order: the patch centres divided by
+    the patch size (unconditional_md4.py:74-76, fast_ops.py:280): token (gy, gz, gx) in row-major YZX order sits at
+    (gx + 1/2, gy + 1/2, gz + 1/2)."""
+    gy, gz, gx = (v // patch for v in voxel_shape)
+    grid = torch.stack(torch.meshgrid(torch.arange(gy).float(), torch.arange(gz).float(), torch.arange(gx).float(),
+                                      indexing='ij'), -1).reshape(-1, 3)
+    return (grid[:, [2, 0, 1]] * patch + patch / 2) / patch
+
+
+class _Rope(torch.nn.Module):
+    def __init__(self, head_dim):
+        super().__init__()
+        axis = head_dim // 3
+        self.register_buffer('frequencies', 10000.0 ** (-torch.arange(0, axis, 2).float() / axis))
+
+
+class _Attention(torch.nn.Module):
+    def __init__(self, width, heads):
+        super().__init__()
+        self.heads = heads
+        self.qkv = torch.nn.Linear(width, 3 * width)
+        self.proj = torch.nn.Linear(width, width)
+        self.rope = _Rope(width // heads)
+
+
+class BlockWeights(torch.nn.Module):
+    """Random-initialised parameters in the layout of the reference's UnconditionalBlock (the trained weights are
+    not published): `norm1` / `norm2` (LayerNorm, eps 1e-6; affine only without AdaLN), `attn.qkv`, `attn.proj`,
+    `attn.heads`, `attn.rope.frequencies`, `mlp` = Linear, GELU, Linear and, when `timed`, `ada` = SiLU, Linear(W, 6W)
+    (unconditional_md4_timefree.py:33-63; unconditional_md4.py:27-56). Holds parameters only: the forward is
+    `streamvoxel_amd.stream.backbone.block_forward`. Linear weights xavier-uniform, biases and the AdaLN
+    projection N(0, 0.02^2) so that every gate and shift is non-zero."""
+
+    def __init__(self, width, heads, ratio=4.0, timed=True, seed=0):
+        super().__init__()
+        if width % heads or (width // heads) % 6:
+            raise ValueError('heads must split the width into head_dim multiples of 6')
+        g = torch.Generator().manual_seed(seed)
+        self.norm1 = torch.nn.LayerNorm(width, elementwise_affine=not timed, eps=1e-6)
+        self.norm2 = torch.nn.LayerNorm(width, elementwise_affine=not timed, eps=1e-6)
+        self.attn = _Attention(width, heads)
+        hidden = int(width * ratio)
+        self.mlp = torch.nn.Sequential(torch.nn.Linear(width, hidden), torch.nn.GELU(), torch.nn.Linear(hidden, width))
+        if timed:
+            self.ada = torch.nn.Sequential(torch.nn.SiLU(), torch.nn.Linear(width, 6 * width))
+        with torch.no_grad():
+            for m in self.modules():
+                if isinstance(m, torch.nn.Linear):
+                    bound = (6.0 / (m.in_features + m.out_features)) ** 0.5
+                    m.weight.copy_((torch.rand(m.weight.shape, generator=g) * 2 - 1) * bound)
+                    m.bias.copy_(torch.randn(m.bias.shape, generator=g) * 0.02)
+            if timed:
+                self.ada[1].weight.copy_(torch.randn(self.ada[1].weight.shape, generator=g) * 0.02)
+                self.ada[1].bias.copy_(torch.randn(self.ada[1].bias.shape, generator=g) * 0.02)
+            else:
+                for n in (self.norm1, self.norm2):
+                    n.weight.copy_(1 + torch.randn(width, generator=g) * 0.1)
+                    n.bias.copy_(torch.randn(width, generator=g) * 0.1)

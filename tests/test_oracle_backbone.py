@@ -1,0 +1,136 @@
+"""Pins of the transformer-block oracle (oracle/backbone.py) by closed forms and invariants, on the CPU."""
+import math
+
+import torch
+
+from oracle import attention as A
+from oracle import backbone as O
+from oracle import producer as P
+
+F64 = torch.float64
+
+
+def test_layer_norm_invariants_and_affine():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 5, 40, generator=g, dtype=F64) * 3 + 7
+    eps = 1e-6
+    y = O.layer_norm(x, eps)
+    var = x.var(-1, unbiased=False, keepdim=True)
+    assert torch.allclose(y.mean(-1), torch.zeros(3, 5, dtype=F64), atol=1e-12)
+    # biased variance: var(y) = var / (var + eps) exactly (an unbiased divisor would fail this)
+    assert torch.allclose(y.var(-1, unbiased=False, keepdim=True), var / (var + eps), rtol=1e-12)
+    w, b = torch.randn(40, generator=g, dtype=F64), torch.randn(40, generator=g, dtype=F64)
+    assert torch.allclose(O.layer_norm(x, eps, w, b), y * w + b, rtol=1e-13, atol=1e-13)
+    # a large eps pulls the output towards zero by sqrt(var / (var + eps))
+    y2 = O.layer_norm(x, 100.0)
+    assert torch.allclose(y2, y * torch.sqrt((var + eps) / (var + 100.0)), rtol=1e-12)
+
+
+def test_modulate_closed_form():
+    x = torch.tensor([[[1.0, -2.0], [0.5, 4.0]]], dtype=F64)          # [1, 2, 2]
+    shift = torch.tensor([[10.0, 20.0]], dtype=F64)
+    scale = torch.tensor([[1.0, -0.5]], dtype=F64)
+    want = torch.tensor([[[12.0, 19.0], [11.0, 22.0]]], dtype=F64)
+    assert torch.equal(O.modulate(x, shift, scale), want)
+
+
+def test_gelu_and_silu_known_values():
+    x = torch.tensor([-1.0, 0.0, 1.0], dtype=F64)
+    assert torch.allclose(O.gelu(x), torch.tensor([-0.15865525393145707, 0.0, 0.8413447460685429], dtype=F64),
+                          rtol=0, atol=1e-15)
+    assert torch.allclose(O.silu(x), torch.tensor([-0.2689414213699951, 0.0, 0.7310585786300049], dtype=F64),
+                          rtol=0, atol=1e-15)
+    t = torch.linspace(-6, 6, 97, dtype=F64)
+    # odd parts: f(x) - f(-x) = x for both (x * Phi(x) and x * sigmoid(x))
+    assert torch.allclose(O.gelu(t) - O.gelu(-t), t, atol=1e-14)
+    assert torch.allclose(O.silu(t) - O.silu(-t), t, atol=1e-14)
+
+
+def _attn_params(width, seed):
+    g = torch.Generator().manual_seed(seed)
+    return {
+        'attn.qkv.weight': torch.randn(3 * width, width, generator=g, dtype=F64) / math.sqrt(width),
+        'attn.qkv.bias': torch.randn(3 * width, generator=g, dtype=F64) * 0.1,
+        'attn.proj.weight': torch.randn(width, width, generator=g, dtype=F64) / math.sqrt(width),
+        'attn.proj.bias': torch.randn(width, generator=g, dtype=F64) * 0.1,
+    }
+
+
+def test_rotary_attention_uniform_scores_give_the_mean_of_v():
+    """Q and K projections zero: every score is 0, so every token's output is proj(mean over tokens of V)."""
+    B, N, W, H = 2, 7, 24, 2
+    p = _attn_params(W, 1)
+    p['attn.qkv.weight'][:2 * W] = 0
+    p['attn.qkv.bias'][:2 * W] = 0
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(B, N, W, generator=g, dtype=F64)
+    pos = torch.rand(B, N, 3, generator=g) * 10
+    v = x @ p['attn.qkv.weight'][2 * W:].t() + p['attn.qkv.bias'][2 * W:]
+    want = v.mean(1, keepdim=True) @ p['attn.proj.weight'].t() + p['attn.proj.bias']
+    got = O.rotary_attention(x, pos, p, H)
+    assert torch.allclose(got, want.expand(B, N, W), rtol=1e-12, atol=1e-12)
+
+
+def test_rotary_attention_single_token_and_zero_positions():
+    B, W, H = 3, 24, 2
+    p = _attn_params(W, 3)
+    g = torch.Generator().manual_seed(4)
+    # one token: softmax over one key is 1, the output is proj(v) whatever the rotation
+    x = torch.randn(B, 1, W, generator=g, dtype=F64)
+    pos = torch.rand(B, 1, 3, generator=g) * 50
+    v = x @ p['attn.qkv.weight'][2 * W:].t() + p['attn.qkv.bias'][2 * W:]
+    want = v @ p['attn.proj.weight'].t() + p['attn.proj.bias']
+    assert torch.allclose(O.rotary_attention(x, pos, p, H), want, rtol=1e-12, atol=1e-12)
+    # positions 0: the rotation is the identity, so the result is plain attention on the [3, H, D] split
+    N = 6
+    x = torch.randn(B, N, W, generator=g, dtype=F64)
+    qkv = (x @ p['attn.qkv.weight'].t() + p['attn.qkv.bias']).reshape(B, N, 3, H, W // H)
+    q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+    o = A.cross_attention_bruteforce(q, k, v, [N] * B)
+    want = o.transpose(1, 2).reshape(B, N, W) @ p['attn.proj.weight'].t() + p['attn.proj.bias']
+    got = O.rotary_attention(x, torch.zeros(B, N, 3), p, H)
+    assert torch.allclose(got, want, rtol=1e-10, atol=1e-12)
+    # and a rotation of both Q and K by the same phase everywhere leaves the scores unchanged
+    same = torch.full((B, N, 3), 3.25)
+    assert torch.allclose(O.rotary_attention(x, same, p, H), want, rtol=1e-6, atol=1e-6)
+
+
+def _block_params(W, seed, timed):
+    g = torch.Generator().manual_seed(seed)
+    p = _attn_params(W, seed)
+    p.update({
+        'mlp.0.weight': torch.randn(4 * W, W, generator=g, dtype=F64) / math.sqrt(W),
+        'mlp.0.bias': torch.randn(4 * W, generator=g, dtype=F64) * 0.1,
+        'mlp.2.weight': torch.randn(W, 4 * W, generator=g, dtype=F64) / math.sqrt(4 * W),
+        'mlp.2.bias': torch.randn(W, generator=g, dtype=F64) * 0.1,
+    })
+    if timed:
+        p['ada.1.weight'] = torch.randn(6 * W, W, generator=g, dtype=F64) * 0.1
+        p['ada.1.bias'] = torch.randn(6 * W, generator=g, dtype=F64) * 0.1
+    return p
+
+
+def test_block_gates_and_residuals():
+    B, N, W, H = 2, 5, 24, 2
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(B, N, W, generator=g, dtype=F64)
+    pos = torch.rand(B, N, 3, generator=g) * 8
+    t = torch.randn(B, W, generator=g, dtype=F64)
+    p = _block_params(W, 6, timed=True)
+    # zero AdaLN projection: both gates are 0 and the block is the identity
+    q = dict(p, **{'ada.1.weight': torch.zeros(6 * W, W, dtype=F64), 'ada.1.bias': torch.zeros(6 * W, dtype=F64)})
+    assert torch.equal(O.block(x, t, pos, q, H), x)
+    # gates 1, shifts and scales 0, MLP zero except its output bias: x1 = x + attn(LN(x)), out = x1 + bias
+    bias = torch.zeros(6 * W, dtype=F64)
+    bias[2 * W:3 * W] = 1
+    bias[5 * W:] = 1
+    q = dict(p, **{'ada.1.weight': torch.zeros(6 * W, W, dtype=F64), 'ada.1.bias': bias,
+                   'mlp.0.weight': torch.zeros(4 * W, W, dtype=F64), 'mlp.0.bias': torch.zeros(4 * W, dtype=F64),
+                   'mlp.2.weight': torch.zeros(W, 4 * W, dtype=F64)})
+    x1 = x + O.rotary_attention(O.layer_norm(x, 1e-6), pos, q, H)
+    assert torch.allclose(O.block(x, t, pos, q, H), x1 + q['mlp.2.bias'], rtol=1e-12, atol=1e-12)
+    # the affine block with unit LayerNorms and a zero attention projection is x + MLP(LN(x))
+    a = _block_params(W, 7, timed=False)
+    a.update({'attn.proj.weight': torch.zeros(W, W, dtype=F64), 'attn.proj.bias': torch.zeros(W, dtype=F64)})
+    want = x + O.mlp(O.layer_norm(x, 1e-6), a)
+    assert torch.allclose(O.block(x, None, pos, a, H), want, rtol=1e-12, atol=1e-12)
