@@ -193,9 +193,10 @@ int svhip_kv_write(const void* prefix_k, const void* prefix_v, int64_t P, int64_
  * Self-attention operands of a transformer block from its fused qkv projection: qkv bf16, element (b,n,s,h,d)
  * (s = 0 Q, 1 K, 2 V; the Linear's [3, H, D] row) at b*sx_b + n*sx_n + (s*H + h)*D + d, rows 16-byte aligned.
  * Q and K are rotated by AxialRoPE at positions [B,N,3] fp32 (element (b,n,t) at b*sp_b + n*sp_n + t) with freq
- * [D/6] exactly as svhip_axial_rope does, and written to q / k (element (b,h,n,d) at b*s?_b + h*s?_h + n*s?_n + d;
- * they may be the Q / K slices of qkv itself: in place); V is written transposed to vt (element (b,h,d,n) at
- * b*svt_b + h*svt_h + d*svt_d + n, 16-byte aligned rows), the layout svhip_xattn_fwd stages directly into LDS.
+ * [D/6] exactly as svhip_axial_rope does, and written to q / k (element (b,h,n,d) at b*s?_b + h*s?_h + n*s?_n + d,
+ * 16-byte aligned rows; they may be the Q / K slices of qkv itself: in place); V is written transposed to vt
+ * (element (b,h,d,n) at b*svt_b + h*svt_h + d*svt_d + n, 16-byte aligned rows), the layout svhip_xattn_fwd stages
+ * directly into LDS. sin / cos of a (token, pair) are evaluated once for Q and K of every head.
  * head_dim: a multiple of 24 up to 128 (48 and 96 in the shipped models).
  * Replaces: the qkv split, the two AxialRoPE calls and the layout change before F.scaled_dot_product_attention in
  * RotaryAttention.forward (streamvoxel/models/unconditional_md4_timefree.py:41-47, unconditional_md4.py:35-41).
@@ -219,6 +220,22 @@ int svhip_qkv_rope(const void* qkv, const float* positions, const float* freq, i
 int svhip_layer_norm(const void* x, void* y, const float* weight, const float* bias, const void* shift,
                      const void* scale, int64_t B, int64_t N, int64_t W, int64_t sx_b, int64_t sx_n, int64_t sy_b,
                      int64_t sy_n, int64_t s_mod, float eps, void* stream);
+
+/*
+ * The gated residual of a block, optionally followed by the next LayerNorm (+ AdaLN), in one pass:
+ *   r = x + gate[b] * branch    (the product and the sum each rounded to bf16, as `x + g[:, None] * f(...)` is
+ *                                in the reference's bf16 tensors; gate NULL: r = x + branch)
+ *   y = LN(r) * (1 + scale[b]) + shift[b]   (as svhip_layer_norm; y NULL: only r is written)
+ * x, branch, r, y bf16 [B,N,W] with 16-byte aligned rows (element (b,n,c) at b*s?_b + n*s?_n + c; r may be x);
+ * gate bf16 [B,W] rows s_gate apart; weight / bias / shift / scale / s_mod / eps as for svhip_layer_norm.
+ * Replaces: `x + g1[:, None] * self.attn(...)` followed by `modulate(self.norm2(x), s2, c2)`, and
+ * `x + g2[:, None] * self.mlp(...)`, of UnconditionalBlock.forward
+ * (streamvoxel/models/unconditional_md4_timefree.py:60-63; unconditional_md4.py:52-56 without gates).
+ */
+int svhip_residual_norm(const void* x, const void* branch, const void* gate, int64_t s_gate, void* r, void* y,
+                        const float* weight, const float* bias, const void* shift, const void* scale, int64_t s_mod,
+                        int64_t B, int64_t N, int64_t W, int64_t sx_b, int64_t sx_n, int64_t sa_b, int64_t sa_n,
+                        int64_t sr_b, int64_t sr_n, int64_t sy_b, int64_t sy_n, float eps, void* stream);
 
 #ifdef __cplusplus
 }

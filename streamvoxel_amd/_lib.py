@@ -54,6 +54,8 @@ SIGNATURES = {
                                                                        _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                                                        _c_p]),
     'svhip_layer_norm': (ctypes.c_int, [_c_p] * 6 + [_c_i64] * 8 + [_c_f, _c_p]),
+    'svhip_residual_norm': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]
+                            + [_c_i64] * 12 + [_c_f, _c_p]),
 }
 
 _lib = None

@@ -57,12 +57,15 @@ __device__ __forceinline__ uint8_t e4m3fn_rne(float x) {
   return sign | static_cast<uint8_t>(((e + 7) << 3) | static_cast<int>(m));
 }
 
-// One rotated pair: (a, b) at phase p.
-__device__ __forceinline__ void rope_pair(float a, float b, float p, float& ra, float& rb) {
-  const float s = bf16_round(sinf(p));
-  const float c = bf16_round(cosf(p));
+// One rotated pair (a, b) by sin s and cos c (already rounded to bf16).
+__device__ __forceinline__ void rope_rot(float a, float b, float s, float c, float& ra, float& rb) {
   ra = bf16_round(bf16_round(a * c) - bf16_round(b * s));
   rb = bf16_round(bf16_round(a * s) + bf16_round(b * c));
+}
+
+// One rotated pair: (a, b) at phase p.
+__device__ __forceinline__ void rope_pair(float a, float b, float p, float& ra, float& rb) {
+  rope_rot(a, b, bf16_round(sinf(p)), bf16_round(cosf(p)), ra, rb);
 }
 
 __device__ __forceinline__ void unpack2(uint32_t w, float& a, float& b) {
@@ -251,9 +254,12 @@ __global__ __launch_bounds__(kProducerThreads) void kv_write_kernel(KvArgs a) {
 }
 
 
-// Self-attention operands from the qkv projection. Workgroup = (window b, head h, 64-token tile). Q and K pairs of
-// the tile are rotated one per thread and iteration (consecutive threads on consecutive pairs of a token's head);
-// V goes through LDS: 16-byte row loads of [64 tokens, D] in, 16-byte V^T row stores of [D, 64 tokens] out.
+// Self-attention operands from the qkv projection, in one launch of two kinds of workgroup:
+//  * rotation, (window b, 8-token tile): the tile's sin / cos (rounded to bf16) of every (token, pair) go to LDS
+//    once and serve Q and K of all heads (the phase depends on the token and the pair only); the Q | K part of a
+//    token's row (2 H D contiguous elements) is then rotated 16 bytes (4 pairs) per thread, four loads in flight;
+//  * layout, (window b, head h, 64-token tile): V rows [64 tokens, D] in through LDS, V^T rows [D, 64 tokens] out,
+//    16 bytes per store.
 struct QkvArgs {
   const uint16_t* x;   // element (b, n, s, h, d) at b*sxb + n*sxn + (s*H + h)*D + d
   const float* pos;    // (b, n, axis) at b*spb + n*spn + axis
@@ -263,52 +269,91 @@ struct QkvArgs {
   int64_t sxb, sxn, spb, spn;
   int64_t sqb, sqh, sqn, skb, skh, skn;
   int64_t svb, svh, svd;  // V^T element (b, h, d, n) at b*svb + h*svh + d*svd + n
-  int64_t tiles;          // token tiles per window
+  int64_t rot_tiles;      // 8-token tiles per window
+  int64_t v_tiles;        // 64-token tiles per window
 };
 
+constexpr int kRotTokens = 8;
+constexpr int kQkvBatch = 4;  // 16-byte loads a thread issues before it uses the first
 constexpr int kQkvTokens = 64;
 constexpr int kQkvRow = kQkvTokens + 2;  // LDS V^T row stride (bf16 elements), padded against bank conflicts
 
-__global__ __launch_bounds__(kProducerThreads) void qkv_rope_kernel(QkvArgs a) {
-  __shared__ uint16_t sv[kMaxHeadDim * kQkvRow];
-  const int64_t tile = blockIdx.x % a.tiles;
-  const int64_t bh = blockIdx.x / a.tiles;
-  const int64_t h = bh % a.H, b = bh / a.H;
-  const int64_t n0 = tile * kQkvTokens;
-  const int tokens = static_cast<int>(a.N - n0 < kQkvTokens ? a.N - n0 : kQkvTokens);
+__device__ __forceinline__ void qkv_rotate(const QkvArgs& a, int64_t b, int64_t tile, float2* sc) {
+  const int64_t n0 = tile * kRotTokens;
+  const int tokens = static_cast<int>(a.N - n0 < kRotTokens ? a.N - n0 : kRotTokens);
   const int pairs = static_cast<int>(a.D / 2);
   const int per_axis = static_cast<int>(a.D / 6);
-  const int D = static_cast<int>(a.D);
-  const uint16_t* xb = a.x + b * a.sxb + n0 * a.sxn;
-
-  // V rows -> LDS, transposed: sv[d][token].
-  const int chunks = tokens * (D / 8);
-  for (int c = threadIdx.x; c < chunks; c += kProducerThreads) {
-    const int t = c / (D / 8), dc = c % (D / 8);
-    const uint4 w = *reinterpret_cast<const uint4*>(xb + t * a.sxn + (2 * a.H + h) * a.D + 8 * dc);
-    const uint32_t e[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sv[(8 * dc + j) * kQkvRow + t] = static_cast<uint16_t>(e[j >> 1] >> (16 * (j & 1)));
-  }
-
-  // Q and K: rotate every pair of the tile.
-  const int qk_pairs = 2 * tokens * pairs;
-  for (int i = threadIdx.x; i < qk_pairs; i += kProducerThreads) {
-    const int s = i / (tokens * pairs);  // 0 = Q, 1 = K
-    const int r = i - s * tokens * pairs;
-    const int t = r / pairs, pr = r - t * pairs;
+  for (int i = threadIdx.x; i < tokens * pairs; i += kProducerThreads) {
+    const int t = i / pairs, pr = i - t * pairs;
     const int axis = pr / per_axis, fi = pr - axis * per_axis;
-    const int64_t n = n0 + t;
-    const float phase = a.pos[b * a.spb + n * a.spn + axis] * a.freq[fi];
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(xb + t * a.sxn + (s * a.H + h) * a.D + 2 * pr);
-    float x0, x1, r0, r1;
-    unpack2(w, x0, x1);
-    rope_pair(x0, x1, phase, r0, r1);
-    uint16_t* dst = s == 0 ? a.q + b * a.sqb + h * a.sqh + n * a.sqn : a.k + b * a.skb + h * a.skh + n * a.skn;
-    *reinterpret_cast<uint32_t*>(dst + 2 * pr) = pack2(r0, r1);
+    const float phase = a.pos[b * a.spb + (n0 + t) * a.spn + axis] * a.freq[fi];
+    sc[i] = make_float2(bf16_round(sinf(phase)), bf16_round(cosf(phase)));
   }
   __syncthreads();
+  const int D = static_cast<int>(a.D);
+  const int W = static_cast<int>(a.H) * D;
+  const int row_chunks = 2 * W / 8;  // Q | K of one token in 16-byte chunks
+  const int total = tokens * row_chunks;
+  for (int base = 0; base < total; base += kQkvBatch * kProducerThreads) {
+    uint4 w[kQkvBatch];
+#pragma unroll
+    for (int u = 0; u < kQkvBatch; ++u) {
+      const int i = base + u * kProducerThreads + static_cast<int>(threadIdx.x);
+      if (i < total) {
+        const int t = i / row_chunks, e = 8 * (i - t * row_chunks);
+        w[u] = *reinterpret_cast<const uint4*>(a.x + b * a.sxb + (n0 + t) * a.sxn + e);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kQkvBatch; ++u) {
+      const int i = base + u * kProducerThreads + static_cast<int>(threadIdx.x);
+      if (i >= total) continue;
+      const int t = i / row_chunks, e = 8 * (i - t * row_chunks);
+      const int s = e / W, h = (e - s * W) / D, d = e - s * W - h * D;
+      const int64_t n = n0 + t;
+      const uint32_t in[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+      uint32_t out[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float2 r = sc[t * pairs + d / 2 + j];
+        float x0, x1, r0, r1;
+        unpack2(in[j], x0, x1);
+        rope_rot(x0, x1, r.x, r.y, r0, r1);
+        out[j] = pack2(r0, r1);
+      }
+      uint16_t* dst = s == 0 ? a.q + b * a.sqb + h * a.sqh + n * a.sqn : a.k + b * a.skb + h * a.skh + n * a.skn;
+      *reinterpret_cast<uint4*>(dst + d) = make_uint4(out[0], out[1], out[2], out[3]);
+    }
+  }
+}
 
+__device__ __forceinline__ void qkv_layout_v(const QkvArgs& a, int64_t b, int64_t h, int64_t tile, uint16_t* sv) {
+  const int64_t n0 = tile * kQkvTokens;
+  const int tokens = static_cast<int>(a.N - n0 < kQkvTokens ? a.N - n0 : kQkvTokens);
+  const int D = static_cast<int>(a.D);
+  const uint16_t* xb = a.x + b * a.sxb + n0 * a.sxn + (2 * a.H + h) * a.D;
+  // V rows -> LDS, transposed: sv[d][token].
+  const int total = tokens * (D / 8);
+  for (int base = 0; base < total; base += kQkvBatch * kProducerThreads) {
+    uint4 w[kQkvBatch];
+#pragma unroll
+    for (int u = 0; u < kQkvBatch; ++u) {
+      const int c = base + u * kProducerThreads + static_cast<int>(threadIdx.x);
+      if (c < total) w[u] = *reinterpret_cast<const uint4*>(xb + (c / (D / 8)) * a.sxn + 8 * (c % (D / 8)));
+    }
+#pragma unroll
+    for (int u = 0; u < kQkvBatch; ++u) {
+      const int c = base + u * kProducerThreads + static_cast<int>(threadIdx.x);
+      if (c >= total) continue;
+      const int t = c / (D / 8), dc = c % (D / 8);
+      const uint32_t e[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        sv[(8 * dc + j) * kQkvRow + t] = static_cast<uint16_t>(e[j >> 1] >> (16 * (j & 1)));
+      }
+    }
+  }
+  __syncthreads();
   // V^T rows: d-th row of the tile = tokens n0 .. n0 + tokens - 1, 8 per 16-byte store.
   uint16_t* vt = a.vt + b * a.svb + h * a.svh + n0;
   const int tchunks = (tokens + 7) / 8;
@@ -325,6 +370,19 @@ __global__ __launch_bounds__(kProducerThreads) void qkv_rope_kernel(QkvArgs a) {
     } else {
       for (int j = 0; 8 * tc + j < tokens; ++j) vt[d * a.svd + 8 * tc + j] = src[j];
     }
+  }
+}
+
+__global__ __launch_bounds__(kProducerThreads) void qkv_rope_kernel(QkvArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kMaxHeadDim * kQkvRow * 2];
+  const int64_t rot_blocks = a.B * a.rot_tiles;
+  const int64_t id = blockIdx.x;
+  if (id < rot_blocks) {
+    qkv_rotate(a, id / a.rot_tiles, id % a.rot_tiles, reinterpret_cast<float2*>(smem));
+  } else {
+    const int64_t v = id - rot_blocks;
+    const int64_t tile = v % a.v_tiles, bh = v / a.v_tiles;
+    qkv_layout_v(a, bh / a.H, bh % a.H, tile, reinterpret_cast<uint16_t*>(smem));
   }
 }
 
@@ -438,17 +496,16 @@ extern "C" int svhip_qkv_rope(const void* qkv, const float* positions, const flo
   auto aligned16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   SVHIP_REQUIRE(aligned16(qkv) && sx_b % 8 == 0 && sx_n % 8 == 0, "%s: qkv rows must start on 16-byte boundaries",
                 name);
-  SVHIP_REQUIRE(reinterpret_cast<uintptr_t>(q) % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 4 == 0 &&
-                    sq_b % 2 == 0 && sq_h % 2 == 0 && sq_n % 2 == 0 && sk_b % 2 == 0 && sk_h % 2 == 0 &&
-                    sk_n % 2 == 0,
-                "%s: Q/K rows must start on 4-byte boundaries (head_dim contiguous)", name);
+  SVHIP_REQUIRE(aligned16(q) && aligned16(k) && sq_b % 8 == 0 && sq_h % 8 == 0 && sq_n % 8 == 0 && sk_b % 8 == 0 &&
+                    sk_h % 8 == 0 && sk_n % 8 == 0,
+                "%s: Q/K rows must start on 16-byte boundaries (head_dim contiguous)", name);
   SVHIP_REQUIRE(aligned16(vt) && svt_b % 8 == 0 && svt_h % 8 == 0 && svt_d % 8 == 0,
                 "%s: V^T rows must start on 16-byte boundaries", name);
   if (B == 0 || N == 0) return SVHIP_OK;
   QkvArgs a{static_cast<const uint16_t*>(qkv), positions, freq, static_cast<uint16_t*>(q), static_cast<uint16_t*>(k),
             static_cast<uint16_t*>(vt), B, N, H, D, sx_b, sx_n, sp_b, sp_n, sq_b, sq_h, sq_n, sk_b, sk_h, sk_n,
-            svt_b, svt_h, svt_d, cdiv(N, kQkvTokens)};
-  const int64_t grid = B * H * a.tiles;
+            svt_b, svt_h, svt_d, cdiv(N, kRotTokens), cdiv(N, kQkvTokens)};
+  const int64_t grid = B * a.rot_tiles + B * H * a.v_tiles;
   SVHIP_REQUIRE(grid < (1ll << 31), "%s: grid too large", name);
   qkv_rope_kernel<<<static_cast<unsigned>(grid), kProducerThreads, 0, as_stream(stream)>>>(a);
   SVHIP_LAUNCHED(name);

@@ -5,11 +5,12 @@ Reference counterparts: `RotaryAttention.forward` and `UnconditionalBlock.forwar
 unconditional_md4.py:27-56, affine LayerNorm) and `run_block` (streamvoxel/stream/fast_ops.py:118-119), which
 `FastSlotForward.forward` calls for the 25 backbone and 13 control blocks of a step (fast_ops.py:288-298).
 
-What runs where: LayerNorm with the AdaLN modulation is `svhip_layer_norm` (one HBM pass); the qkv split, the two
-AxialRoPE rotations and V's transposed layout are `svhip_qkv_rope` (one pass); the attention is `svhip_xattn_fwd`
-over the window's own tokens (every window attends all N keys; V^T staged straight into LDS). The Linear layers
-(qkv, proj, the MLP, the AdaLN projection) and the MLP's GELU stay the block's torch modules, as in the reference:
-plain library GEMMs.
+What runs where: LayerNorm with the AdaLN modulation is `svhip_layer_norm` (one HBM pass); the gated residual
+after the attention and the second LayerNorm are one `svhip_residual_norm` pass, the gated residual after the MLP
+another; the qkv split, the two AxialRoPE rotations and V's transposed layout are `svhip_qkv_rope` (one pass); the
+attention is `svhip_xattn_fwd` over the window's own tokens (every window attends all N keys; V^T staged straight
+into LDS). The Linear layers (qkv, proj, the MLP, the AdaLN projection) and the MLP's GELU stay the block's torch
+modules, as in the reference: plain library GEMMs.
 """
 from __future__ import annotations
 
@@ -18,7 +19,7 @@ import torch
 from streamvoxel_amd import _lib
 from streamvoxel_amd.stream.attention import attention
 
-__all__ = ['layer_norm', 'qkv_rope', 'rotary_attention', 'block_forward', 'run_block']
+__all__ = ['layer_norm', 'residual_norm', 'qkv_rope', 'rotary_attention', 'block_forward', 'run_block']
 
 _full_lengths = {}
 
@@ -35,6 +36,58 @@ def _lengths(batch, tokens, device):
 
 def _f32(p):
     return None if p is None else p.detach().to(torch.float32).contiguous()
+
+
+def _rows(t, name):
+    if t.dtype != torch.bfloat16 or t.dim() != 3 or t.stride(-1) != 1:
+        raise ValueError(f'{name} must be bf16 [B, N, W] with a contiguous last axis')
+
+
+def _window_rows(t, B, W, name):
+    """A per-window [B, W] operand (gate, shift, scale) as bf16 with a contiguous last axis."""
+    t = t.to(torch.bfloat16)
+    if t.shape != (B, W) or t.stride(-1) != 1:
+        raise ValueError(f'{name} must be [B, W] with a contiguous last axis')
+    return t
+
+
+def residual_norm(x, branch, gate=None, norm=None, shift=None, scale=None):
+    """r = x + gate[:, None] * branch (x + branch without gate; bf16 roundings as the reference's tensors), and,
+    when `norm` is given, y = norm(r) modulated by shift / scale as `layer_norm` does, in one pass. Returns r, or
+    (r, y) with a norm."""
+    _lib.require_gpu(x, branch, gate, shift, scale)
+    _rows(x, 'x')
+    _rows(branch, 'branch')
+    if branch.shape != x.shape:
+        raise ValueError('branch must match x')
+    B, N, W = x.shape
+    if gate is not None:
+        gate = _window_rows(gate, B, W, 'gate')
+    if (shift is None) != (scale is None):
+        raise ValueError('shift and scale come together')
+    if shift is not None:
+        if norm is None:
+            raise ValueError('shift / scale modulate the norm')
+        shift, scale = _window_rows(shift, B, W, 'shift'), _window_rows(scale, B, W, 'scale')
+        if shift.stride(0) != scale.stride(0):
+            shift, scale = shift.contiguous(), scale.contiguous()
+    r = torch.empty_like(x)
+    y = None
+    weight = bias = None
+    eps = 0.0
+    if norm is not None:
+        if tuple(norm.normalized_shape) != (W,):
+            raise ValueError(f'LayerNorm over {tuple(norm.normalized_shape)} does not match width {W}')
+        y = torch.empty_like(x)
+        weight, bias, eps = _f32(norm.weight), _f32(norm.bias), float(norm.eps)
+    lib = _lib.load()
+    _lib.check(lib.svhip_residual_norm(
+        _lib.ptr(x), _lib.ptr(branch), _lib.ptr(gate), 0 if gate is None else gate.stride(0), _lib.ptr(r),
+        _lib.ptr(y), _lib.ptr(weight), _lib.ptr(bias), _lib.ptr(shift), _lib.ptr(scale),
+        0 if shift is None else shift.stride(0), B, N, W, x.stride(0), x.stride(1), branch.stride(0),
+        branch.stride(1), r.stride(0), r.stride(1), 0 if y is None else y.stride(0), 0 if y is None else y.stride(1),
+        eps, _lib.stream_of(x)), 'svhip_residual_norm')
+    return r if y is None else (r, y)
 
 
 def layer_norm(x, norm, shift=None, scale=None, out=None):
@@ -122,11 +175,12 @@ def block_forward(block, x, time, positions):
     """UnconditionalBlock.forward: with `time` [B,W] the AdaLN block (unconditional_md4_timefree.py:60-63), with
     time None the affine-LayerNorm block (unconditional_md4.py:52-56). x [B,N,W] bf16, positions [B,N,3]."""
     if time is None:
-        x = x + rotary_attention(block.attn, layer_norm(x, block.norm1), positions)
-        return x + block.mlp(layer_norm(x, block.norm2))
+        x, h = residual_norm(x, rotary_attention(block.attn, layer_norm(x, block.norm1), positions), None, block.norm2)
+        return residual_norm(x, block.mlp(h))
     s1, c1, g1, s2, c2, g2 = block.ada(time).chunk(6, -1)
-    x = x + g1[:, None] * rotary_attention(block.attn, layer_norm(x, block.norm1, s1, c1), positions)
-    return x + g2[:, None] * block.mlp(layer_norm(x, block.norm2, s2, c2))
+    a = rotary_attention(block.attn, layer_norm(x, block.norm1, s1, c1), positions)
+    x, h = residual_norm(x, a, g1, block.norm2, s2, c2)
+    return residual_norm(x, block.mlp(h), g2)
 
 
 def run_block(block, x, time, positions):

@@ -94,5 +94,16 @@ def test_argument_errors_of_the_newer_entry_points(lib):
     assert xattn(7, 64, 0.125) == -1 and b'dtype' in lib.svhip_last_error()
     assert xattn(1, 64, -1.0) == -1 and b'scale' in lib.svhip_last_error()
     assert xattn(3, 64, 0.125) == -1 and b'k_scale' in lib.svhip_last_error()
+    # block operands: head_dim not a multiple of 24, width not a multiple of 8, shift without scale, no residual
+    rc = lib.svhip_qkv_rope(fake, fake, fake, 1, 64, 8, 64, 3 * 512 * 64, 3 * 512, 0, 3, fake, 0, 64, 3 * 512, fake,
+                            0, 64, 3 * 512, fake, 8 * 64 * 64, 64 * 64, 64, None)
+    assert rc == -1 and b'head_dim' in lib.svhip_last_error()
+    rc = lib.svhip_layer_norm(fake, fake, None, None, None, None, 1, 4, 12, 48, 12, 48, 12, 0, 1e-6, None)
+    assert rc == -1 and b'width' in lib.svhip_last_error()
+    rc = lib.svhip_layer_norm(fake, fake, None, None, fake, None, 1, 4, 16, 64, 16, 64, 16, 16, 1e-6, None)
+    assert rc == -1 and b'together' in lib.svhip_last_error()
+    rc = lib.svhip_residual_norm(fake, None, None, 0, fake, None, None, None, None, None, 0, 1, 4, 16, 64, 16, 64, 16,
+                                 64, 16, 64, 16, 1e-6, None)
+    assert rc == -1 and b'null' in lib.svhip_last_error()
     # the cache writer's workspace query grows with heads and capacity
     assert lib.svhip_kv_write_workspace_bytes(16, 12672) >= lib.svhip_kv_write_workspace_bytes(8, 9792) > 0

@@ -83,6 +83,35 @@ def test_layer_norm_against_oracle(dev, W, affine, modulated):
     assert bool((err <= bound + 1e-5).all()), float((err - bound).max())
 
 
+@pytest.mark.parametrize('W,gated,normed', [(768, True, True), (384, True, False), (384, False, True)])
+def test_residual_norm(dev, W, gated, normed):
+    """r = x + g * a must equal torch's bf16 `x + g[:, None] * a` bit for bit (the reference's roundings); y as the
+    LayerNorm test bounds it."""
+    from streamvoxel_amd.stream.backbone import residual_norm
+    _case(f'residual_norm W={W} gated={gated} normed={normed}')
+    B, N = 3, 257
+    g = torch.Generator().manual_seed(W + 7)
+    x = torch.randn(B, N, W, generator=g).to(torch.bfloat16).to(dev)
+    a = (torch.randn(B, N, W, generator=g) * 3).to(torch.bfloat16).to(dev)
+    ada = (torch.randn(B, 6 * W, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    s2, c2, g2 = ada[:, 3 * W:4 * W], ada[:, 4 * W:5 * W], ada[:, 5 * W:]
+    norm = torch.nn.LayerNorm(W, elementwise_affine=False, eps=1e-6)
+    out = residual_norm(x, a, g2 if gated else None, norm if normed else None, s2 if normed else None,
+                        c2 if normed else None)
+    want = x + g2[:, None] * a if gated else x + a
+    torch.cuda.synchronize()
+    r, y = out if normed else (out, None)
+    assert torch.equal(r, want)
+    if normed:
+        ref = O.layer_norm(r.cpu(), 1e-6)
+        onep = (1 + c2.cpu().double()).to(torch.bfloat16).double()
+        sh = s2.cpu().double()
+        ref = ref * onep[:, None] + sh[:, None]
+        bound = 2.0 ** -8 * ref.abs() + 2.0 ** -8 * (ref - sh[:, None]).abs()
+        err = (y.cpu().double() - ref).abs()
+        assert bool((err <= bound + 1e-5).all()), float((err - bound).max())
+
+
 def _check_block(out, ref):
     out = out.float().cpu().double()
     err = (out - ref).abs()
