@@ -237,6 +237,22 @@ int svhip_residual_norm(const void* x, const void* branch, const void* gate, int
                         int64_t B, int64_t N, int64_t W, int64_t sx_b, int64_t sx_n, int64_t sa_b, int64_t sa_n,
                         int64_t sr_b, int64_t sr_n, int64_t sy_b, int64_t sy_n, float eps, void* stream);
 
+/*
+ * Gather patchify of voxel tokens (int64 [B,Y,Z,X], element (b,y,z,x) at b*st_b + (y*Z + z)*X + x, values in
+ * [0, cells)): out[b,n,:] = bias + sum_{o < p^3} table[tokens(b, voxel(n, o)) * p^3 + o, :], patch token n row-major
+ * over the (Y/p, Z/p, X/p) grid, kernel offset o = (dy*p + dz)*p + dx. table bf16 [cells * p^3, W] (16-byte aligned
+ * rows) = the patch Conv3d weight permuted to [cell, dy, dz, dx, W]; bias bf16 [W] or NULL; out bf16, element
+ * (b,n,c) at b*so_b + n*so_n + c. The p^3 rows are summed in fp32 in offset order and rounded to bf16, then the
+ * bias is added with one more bf16 rounding. A token outside [0, cells) counts as 0 and sets *bad (device int) to
+ * a non-zero value. p^3 <= 64, W a multiple of 8 up to 2048.
+ * Replaces: GatherPatch.__call__ (streamvoxel/stream/fast_ops.py:54-75: patch_offsets + F.embedding_bag(mode='sum')
+ * + bias), equal to the one-hot Conv3d patchify of UnconditionalMD4DiT.patchify
+ * (streamvoxel/models/unconditional_md4_timefree.py:141-147).
+ */
+int svhip_patch_embed(const int64_t* tokens, const void* table, const void* bias, void* out, int* bad, int64_t B,
+                      int64_t Y, int64_t Z, int64_t X, int64_t patch, int64_t cells, int64_t W, int64_t st_b,
+                      int64_t so_b, int64_t so_n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

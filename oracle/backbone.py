@@ -11,6 +11,10 @@ Everything in float64 on the CPU from a block's parameters, given as the referen
   output projection.
 * `block`: UnconditionalBlock.forward with time (AdaLN, unconditional_md4_timefree.py:60-63) or without
   (affine LayerNorm, unconditional_md4.py:52-56).
+* `patch_embed`: the patchify Conv3d of the one-hot tokens (unconditional_md4_timefree.py:141-147) as the sum of
+  the weight columns the tokens pick (stream/fast_ops.py:54-75, GatherPatch), by explicit loops over the patches.
+* `time_encoding`, `step_forward`: the time features (unconditional_md4_timefree.py:119-125) and one generation
+  step's forward of the streaming ControlNet (stream/fast_ops.py:274-308), composed from the functions above.
 """
 from __future__ import annotations
 
@@ -87,3 +91,83 @@ def block(x, time, positions, params, heads, eps=1e-6):
     s1, c1, g1, s2, c2, g2 = linear(silu(time), params['ada.1.weight'], params['ada.1.bias']).chunk(6, -1)
     x = x + g1[:, None] * rotary_attention(modulate(layer_norm(x, eps), s1, c1), positions, params, heads)
     return x + g2[:, None] * mlp(modulate(layer_norm(x, eps), s2, c2), params)
+
+
+def patch_embed(tokens, weight, bias, patch):
+    """tokens int [B,Y,Z,X] in [0, C+1); weight [W, C+1, p, p, p]; bias [W] or None -> [B, N, W] float64 with patch
+    token n row-major over (Y/p, Z/p, X/p): bias + sum over the kernel offsets (dy, dz, dx) of
+    weight[:, tokens[p*gy + dy, p*gz + dz, p*gx + dx], dy, dz, dx]."""
+    B, Y, Z, X = tokens.shape
+    W = weight.shape[0]
+    w = _d(weight)
+    gy, gz, gx = Y // patch, Z // patch, X // patch
+    out = torch.zeros(B, gy * gz * gx, W, dtype=F64)
+    for b in range(B):
+        for n in range(gy * gz * gx):
+            py, pz, px = n // (gz * gx), (n // gx) % gz, n % gx
+            acc = torch.zeros(W, dtype=F64)
+            for dy in range(patch):
+                for dz in range(patch):
+                    for dx in range(patch):
+                        cell = int(tokens[b, py * patch + dy, pz * patch + dz, px * patch + dx])
+                        acc += w[:, cell, dy, dz, dx]
+            out[b, n] = acc if bias is None else acc + _d(bias)
+    return out
+
+
+def _sub(params, prefix):
+    return {k[len(prefix):]: v for k, v in params.items() if k.startswith(prefix)}
+
+
+def time_encoding(t, params, time_dim):
+    """UnconditionalMD4DiT.time_encoding (unconditional_md4_timefree.py:119-125) in float64: sinusoidal features
+    of t, time_mlp (Linear, GELU, Linear), time_projection (SiLU, Linear)."""
+    half = time_dim // 8
+    freq = torch.exp(-math.log(10000.0) * torch.arange(half, dtype=F64) / half)
+    phase = _d(t)[:, None] * freq
+    h = torch.cat((phase.sin(), phase.cos()), -1)
+    h = linear(gelu(linear(h, params['time_mlp.0.weight'], params['time_mlp.0.bias'])), params['time_mlp.2.weight'],
+               params['time_mlp.2.bias'])
+    return linear(silu(h), params['time_projection.1.weight'], params['time_projection.1.bias'])
+
+
+def step_forward(params, tokens, timestep, origin, group_origin, keys, values, lengths, *, depth, heads,
+                 control_heads, layer_map, patch, y_range, time_dim, voxel_shape):
+    """FastSlotForward.forward (stream/fast_ops.py:274-308) in float64 from the model's state dict `params`
+    (backbone.*, control.*, cross.*, zero.*): gather patchify + height embedding, the backbone blocks with the
+    control block, cross attention over keys[j] / values[j] [n, H, Kcap, D] (first lengths[b] keys of window b)
+    and zero projection at every mapped block, final AdaLN LayerNorm, class head. Returns the head's rows
+    [n, N, p^3 C]."""
+    bb, cc = _sub(params, 'backbone.'), _sub(params, 'control.')
+    centers = _d(bb['patch_centers_xyz'])[None] + _d(origin)[:, None]
+    positions = (centers - _d(group_origin)[None, None]) / 4
+    n = len(tokens)
+    sa_positions = _d(bb['patch_centers_xyz'])[None].expand(n, -1, -1) / 4
+    y = 2 * (centers[..., 1:2] - y_range[0]) / (y_range[1] - y_range[0]) - 1
+
+    def embed(tp):
+        x = patch_embed(tokens, tp['target_patch.weight'], tp['target_patch.bias'], patch)
+        e = linear(silu(linear(y, tp['y_embed.0.weight'], tp['y_embed.0.bias'])), tp['y_embed.2.weight'],
+                   tp['y_embed.2.bias'])
+        return x + e
+
+    b, c = embed(bb), embed(cc)
+    bt, ct = time_encoding(timestep, bb, time_dim), time_encoding(timestep, cc, time_dim)
+    for i in range(depth):
+        b_next = block(b, bt, sa_positions.float(), _sub(bb, f'blocks.{i}.'), heads)
+        j = layer_map.get(i)
+        if j is not None:
+            c = block(c, ct, sa_positions.float(), _sub(cc, f'blocks.{j}.'), control_heads)
+            cp = _sub(params, f'cross.{j}.')
+            W = c.shape[-1]
+            D = W // control_heads
+            q = linear(layer_norm(c, 1e-6), cp['query.weight'], cp['query.bias'])
+            q = q.reshape(n, -1, control_heads, D).transpose(1, 2)
+            q = P.axial_rope(q, positions.float(), P.rope_frequencies(D))
+            o = A.cross_attention(q, keys[j], values[j], lengths)
+            c = c + linear(o.transpose(1, 2).reshape(n, -1, W), cp['proj.weight'], cp['proj.bias'])
+            b_next = b_next + linear(c, params[f'zero.{j}.weight'], params[f'zero.{j}.bias'])
+        b = b_next
+    shift, gain = linear(silu(bt), bb['final_ada.1.weight'], bb['final_ada.1.bias']).chunk(2, -1)
+    h = modulate(layer_norm(b, 1e-6), shift, gain)
+    return linear(h, bb['class_head.weight'], bb['class_head.bias'])

@@ -105,3 +105,87 @@ class BlockWeights(torch.nn.Module):
                 for n in (self.norm1, self.norm2):
                     n.weight.copy_(1 + torch.randn(width, generator=g) * 0.1)
                     n.bias.copy_(torch.randn(width, generator=g) * 0.1)
+
+
+class _Cross(torch.nn.Module):
+    """RotaryCrossAttention's parameters (streaming_controlnet.py:19-28): norm, query, key_value, proj, heads, width,
+    rope."""
+
+    def __init__(self, width, heads):
+        super().__init__()
+        self.heads, self.width = heads, width
+        self.query = torch.nn.Linear(width, width)
+        self.key_value = torch.nn.Linear(width, 2 * width)
+        self.proj = torch.nn.Linear(width, width)
+        self.rope = _Rope(width // heads)
+        self.norm = torch.nn.LayerNorm(width, elementwise_affine=False, eps=1e-6)
+
+
+class Trunk(torch.nn.Module):
+    """The time-conditioned patch DiT's parameters in the reference's layout (unconditional_md4_timefree.py:66-125):
+    target_patch (Conv3d), patch_centers_xyz, y_embed, time_mlp / time_projection, blocks, final_norm / final_ada /
+    class_head (`head=True`), and its sizes; `time_encoding` as the reference computes it."""
+
+    def __init__(self, classes, voxel_shape, patch, width, depth, heads, time_dim=256, y_range=(-64.0, 192.0),
+                 head=True, seed=0):
+        super().__init__()
+        self.num_classes, self.voxel_shape, self.patch_size = classes, tuple(voxel_shape), patch
+        self.hidden_dim, self.depth, self.num_heads, self.time_dim = width, depth, heads, time_dim
+        self.y_range, self.time_free = tuple(y_range), False
+        self.patch_shape = tuple(v // patch for v in self.voxel_shape)
+        self.target_patch = torch.nn.Conv3d(classes + 1, width, patch, stride=patch)
+        self.register_buffer('patch_centers_xyz', patch_positions(self.voxel_shape, patch) * patch)
+        self.y_embed = torch.nn.Sequential(torch.nn.Linear(1, width), torch.nn.SiLU(), torch.nn.Linear(width, width))
+        self.time_mlp = torch.nn.Sequential(torch.nn.Linear(time_dim // 4, time_dim), torch.nn.GELU(),
+                                            torch.nn.Linear(time_dim, time_dim))
+        self.time_projection = torch.nn.Sequential(torch.nn.SiLU(), torch.nn.Linear(time_dim, width))
+        self.blocks = torch.nn.ModuleList(BlockWeights(width, heads, seed=seed * 1000 + i) for i in range(depth))
+        if head:
+            self.final_norm = torch.nn.LayerNorm(width, elementwise_affine=False, eps=1e-6)
+            self.final_ada = torch.nn.Sequential(torch.nn.SiLU(), torch.nn.Linear(width, 2 * width))
+            self.class_head = torch.nn.Linear(width, patch ** 3 * classes)
+        g = torch.Generator().manual_seed(seed)
+        with torch.no_grad():
+            for m in [self.target_patch, *self.y_embed, *self.time_mlp, *self.time_projection,
+                      *([self.final_ada[1], self.class_head] if head else [])]:
+                if isinstance(m, (torch.nn.Linear, torch.nn.Conv3d)):
+                    fan = m.weight[0].numel() + m.weight.shape[0]
+                    m.weight.copy_((torch.rand(m.weight.shape, generator=g) * 2 - 1) * (6.0 / fan) ** 0.5)
+                    m.bias.copy_(torch.randn(m.bias.shape, generator=g) * 0.02)
+
+    def time_encoding(self, t):
+        """unconditional_md4_timefree.py:119-125 (time_free False)."""
+        import math
+        half = self.time_dim // 8
+        freq = torch.exp(-math.log(10000.0) * torch.arange(half, device=t.device).float() / half)
+        phase = t.float()[:, None] * freq
+        return self.time_projection(self.time_mlp(torch.cat((phase.sin(), phase.cos()), -1)))
+
+
+class StepModel(torch.nn.Module):
+    """Random-initialised parameters of the streaming ControlNet a generation step runs (the trained weights are
+    not published), in the reference's layout (streaming_controlnet.py:64-115, compact_controlnet.py:10-33):
+    `backbone` (Trunk with the class head), `control` (Trunk of its own width and depth, no head), `cross`
+    (one _Cross per control block, at the control width), `zero` (Linear control width -> backbone width) and
+    `layer_map` (backbone block -> control block, the uniformly spaced injections of the compact model).
+    Defaults: the shipped model (304 classes, 256 x 16 x 16 windows, patch 4, 25 x 768 backbone, 13 x 384
+    control, 8 heads)."""
+
+    def __init__(self, classes=304, voxel_shape=(256, 16, 16), patch=4, width=768, depth=25, heads=8,
+                 control_width=384, control_depth=13, seed=0):
+        super().__init__()
+        self.backbone = Trunk(classes, voxel_shape, patch, width, depth, heads, seed=seed + 1)
+        self.control = Trunk(classes, voxel_shape, patch, control_width, control_depth, heads, head=False,
+                             seed=seed + 2)
+        self.cross = torch.nn.ModuleList(_Cross(control_width, heads) for _ in range(control_depth))
+        self.zero = torch.nn.ModuleList(torch.nn.Linear(control_width, width) for _ in range(control_depth))
+        indices = [0] if control_depth == 1 else [round(i * (depth - 1) / (control_depth - 1))
+                                                  for i in range(control_depth)]
+        self.layer_map = {idx: j for j, idx in enumerate(indices)}
+        g = torch.Generator().manual_seed(seed + 3)
+        with torch.no_grad():
+            for m in [*self.cross.modules(), *self.zero]:
+                if isinstance(m, torch.nn.Linear):
+                    bound = (6.0 / (m.in_features + m.out_features)) ** 0.5
+                    m.weight.copy_((torch.rand(m.weight.shape, generator=g) * 2 - 1) * bound)
+                    m.bias.copy_(torch.randn(m.bias.shape, generator=g) * 0.02)

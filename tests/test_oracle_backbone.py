@@ -134,3 +134,46 @@ def test_block_gates_and_residuals():
     a.update({'attn.proj.weight': torch.zeros(W, W, dtype=F64), 'attn.proj.bias': torch.zeros(W, dtype=F64)})
     want = x + O.mlp(O.layer_norm(x, 1e-6), a)
     assert torch.allclose(O.block(x, None, pos, a, H), want, rtol=1e-12, atol=1e-12)
+
+
+def test_patch_embed_equals_the_one_hot_conv():
+    """The gather form against torch's Conv3d of the one-hot tokens (a library routine), in float64."""
+    g = torch.Generator().manual_seed(8)
+    B, Y, Z, X, p, C, W = 2, 8, 4, 8, 4, 6, 5
+    tokens = torch.randint(0, C + 1, (B, Y, Z, X), generator=g)
+    weight = torch.randn(W, C + 1, p, p, p, generator=g, dtype=F64)
+    bias = torch.randn(W, generator=g, dtype=F64)
+    onehot = torch.zeros(B, C + 1, Y, Z, X, dtype=F64).scatter_(1, tokens[:, None], 1.0)
+    want = torch.nn.functional.conv3d(onehot, weight, bias, stride=p).flatten(2).transpose(1, 2)
+    assert torch.allclose(O.patch_embed(tokens, weight, bias, p), want, rtol=1e-12, atol=1e-12)
+
+
+def test_step_forward_with_identity_blocks_is_the_head_of_the_embedding():
+    """Every block's AdaLN projection zero (gates 0: blocks are identities) and the zero projections zero: the
+    step's output is class_head(modulate(LN(patchify + height embedding), final shift, gain))."""
+    from streamvoxel_amd import synth
+    model = synth.StepModel(classes=5, voxel_shape=(8, 4, 4), patch=4, width=48, depth=2, heads=1,
+                            control_width=24, control_depth=1, seed=2)
+    params = {k: v.double() for k, v in model.state_dict().items()}
+    for k in list(params):
+        if '.ada.1.' in k or k.startswith('zero.'):
+            params[k] = torch.zeros_like(params[k])
+    g = torch.Generator().manual_seed(3)
+    tokens = torch.randint(0, 6, (2, 8, 4, 4), generator=g)
+    t = torch.tensor([0.1, 0.9])
+    origin = torch.tensor([[0.0, -64.0, 0.0], [4.0, 0.0, 8.0]])
+    group = torch.zeros(3)
+    keys = [torch.randn(2, 1, 8, 24, generator=g, dtype=F64)]
+    out = O.step_forward(params, tokens, t, origin, group, keys, keys, [8, 3], depth=2, heads=1, control_heads=1,
+                         layer_map=model.layer_map, patch=4, y_range=(-64.0, 192.0), time_dim=256,
+                         voxel_shape=(8, 4, 4))
+    bb = {k[len('backbone.'):]: v for k, v in params.items() if k.startswith('backbone.')}
+    centers = bb['patch_centers_xyz'][None] + origin.double()[:, None]
+    y = 2 * (centers[..., 1:2] + 64) / 256 - 1
+    e = O.linear(O.silu(O.linear(y, bb['y_embed.0.weight'], bb['y_embed.0.bias'])), bb['y_embed.2.weight'],
+                 bb['y_embed.2.bias'])
+    x = O.patch_embed(tokens, bb['target_patch.weight'], bb['target_patch.bias'], 4) + e
+    bt = O.time_encoding(t, bb, 256)
+    shift, gain = O.linear(O.silu(bt), bb['final_ada.1.weight'], bb['final_ada.1.bias']).chunk(2, -1)
+    want = O.linear(O.modulate(O.layer_norm(x, 1e-6), shift, gain), bb['class_head.weight'], bb['class_head.bias'])
+    assert torch.allclose(out, want, rtol=1e-12, atol=1e-12)
