@@ -49,6 +49,9 @@ def parse():
     p.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     p.add_argument('--cpu-seconds', type=float, default=12.0, help='bounded CPU sample budget')
     p.add_argument('--kv-dtype', default='bf16', choices=['bf16', 'fp8'])
+    p.add_argument('--no-forward', action='store_true', help='skip the whole-step forward component')
+    p.add_argument('--forward-only', action='store_true',
+                   help='time only the whole-step forward (shipped shape) and print its line')
     return p.parse_args()
 
 
@@ -297,6 +300,38 @@ def cpu_baseline(w, budget_s):
                 cpu_count=os.cpu_count(), wall_s=time.perf_counter() - began)
 
 
+def step_forward_component(dev, lengths_seed=7):
+    """Seconds per call of one whole generation step's forward at the shipped model's shape (random weights, the
+    trained ones are not published): gather patchify, 25 x 768 backbone blocks, 13 x 384 control blocks each with
+    cross attention over its cached context (L_b = 4384 + 1024 k_b keys of 12 672) and zero projection, final
+    AdaLN norm, class head to 304 classes in patch order; 8 windows, one graph."""
+    import torch
+    from streamvoxel_amd import synth
+    from streamvoxel_amd.stream.forward import StepForward
+    from streamvoxel_amd.stream.step import CachedContext
+    model = synth.StepModel(seed=1)
+    for p in model.parameters():
+        p.data = p.data.to(torch.bfloat16)
+    model = model.to(dev)
+    g = torch.Generator().manual_seed(lengths_seed)
+    lengths = (256 * 16 + 288 + 1024 * torch.randint(0, 9, (SLOTS,), generator=g)).tolist()
+    ctx = CachedContext(len(model.cross), SLOTS, 8, 48, 12672, dev)
+    for j in range(ctx.layers):
+        ctx.k[j].normal_().mul_(0.3)
+        ctx.vt[j].normal_()
+    for b, L in enumerate(lengths):
+        ctx.set_length(b, L)
+    step = StepForward(model, ctx)
+    tokens = torch.randint(0, 305, (SLOTS, *SHAPE), device=dev, generator=torch.Generator(dev).manual_seed(3))
+    timestep = torch.full((SLOTS,), 0.5, device=dev)
+    origin = torch.tensor([[16.0 * i, -64.0, 0.0] for i in range(SLOTS)], device=dev)
+    group = torch.tensor([0.0, -64.0, 0.0], device=dev)
+    t = time_graph(lambda: step(tokens, timestep, origin, group), 1, replays=5)
+    del step, ctx, model
+    torch.cuda.empty_cache()
+    return t, lengths
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -306,6 +341,11 @@ def main():
     import streamvoxel_amd
     streamvoxel_amd.load()
     dev = torch.device('cuda:0')
+    if args.forward_only:
+        t_forward, lengths = step_forward_component(dev)
+        print(json.dumps(dict(component='shipped_step_forward', ms=t_forward * 1e3, slots=SLOTS, kv_lengths=lengths,
+                              reference_fast_forward_rtx4090d_ms=44.0)), flush=True)
+        return
     t0 = time.perf_counter()
     w = Workload(dev, args.seed, args.kv_dtype)
     log(f'inputs ready in {time.perf_counter() - t0:.1f}s')
@@ -367,6 +407,10 @@ def main():
         ctx8.write(0, b, w.ctx.k[0][b, :, :L], w.ctx.vt[0][b, :, :, :L].transpose(1, 2).contiguous())
     t_layer_e4m3 = time_graph(lambda: ctx8.attend(0, w.q[1][0], out=w.o[0].transpose(1, 2)), 20)
     del ctx8
+    t_forward = forward_lengths = None
+    if not args.no_forward:
+        t_forward, forward_lengths = step_forward_component(dev)
+        log(f'whole step forward (shipped shape, 8 windows) {t_forward * 1e3:.2f} ms')
     xattn_tflops = w.flops_per_layer / t_layer / 1e12
     select_gbs = w.select_bytes / t_select / 1e9
     entropy_bytes = SLOTS * VOXELS * (CLASSES * 4 + 4)
@@ -407,7 +451,14 @@ def main():
         components=dict(xattn_ms_per_step=LAYERS * t_layer * 1e3, select_ms_per_step=t_select * 1e3,
                         select_from_patch_order_ms_per_step=t_select_patches * 1e3,
                         class_major_permute_ms_avoided=t_permute * 1e3,
-                        selection_bad_flag_seen=bad),
+                        selection_bad_flag_seen=bad,
+                        shipped_step_forward_ms=None if t_forward is None else t_forward * 1e3,
+                        shipped_step_forward_kv_lengths=forward_lengths,
+                        shipped_step_forward_plus_select_ms=(None if t_forward is None else
+                                                             (t_forward + t_select304) * 1e3),
+                        shipped_model_voxels_per_s=(None if t_forward is None else
+                                                    SLOTS * VOXELS / (STEPS_PER_WINDOW * (t_forward + t_select304))),
+                        reference_fast_forward_rtx4090d_ms=44.0),
         measured_peaks=peaks,
         cpu_baseline=cpu,
     )
