@@ -7,7 +7,7 @@
 // Per wave and key block (v_mfma_f32_32x32x16_bf16 throughout), in two 32-key halves that each run the whole
 // online-softmax step (a half's scores take 16 registers, which leaves room for three waves per SIMD):
 //   S^T[key, q] = K . Q^T         A = K rows from LDS, B = the wave's Q (registers, loaded once)
-//   P^T = exp2(S^T * scale*log2e - m)   online softmax; every lane owns one query column (q = lane % 32) and
+//   P^T = exp2(S^T - m)           online softmax; every lane owns one query column (q = lane % 32) and
 //                                       8 of every 16 keys, its partner lane (lane ^ 32) the other 8
 //   O^T[d, q] += V^T . P^T        A = V^T rows from LDS, B = P^T straight from the S^T accumulators
 // The C layout of a 32x32 MFMA gives lane l the rows 8*(i/4) + 4*(l/32) + i%4 of column l%32. K rows are
@@ -17,13 +17,19 @@
 // Because O^T's columns are queries too, the per-query rescale and the final 1/l are lane-local.
 //
 // The softmax is VALU-bound at head_dim 64 (one exp per score against 2 x 64 MACs), so per score it costs one
-// fma (scale and max subtraction fused), one exp, half a bf16 pack and one fp32 add (the row sum; v_dot2c_f32_bf16
-// over the packed P would need half the instructions but does not co-execute with the matrix cores), and no max:
+// exp, half a bf16 pack and one fp32 add (the row sum; v_dot2c_f32_bf16 over the packed P would need half the
+// instructions but does not co-execute with the matrix cores), and no scaling, subtraction or max:
+//   * Q is loaded once, multiplied by scale * log2(e) (and the e4m3 K scale) and rounded to bf16, so the scores
+//     come out in log2 units; the first MFMA of every score chain takes -m (16 registers holding the running
+//     max, negated) as its C operand, so the accumulators hold S - m and P = exp2(S^T) directly.
 //   * P is formed against the running max m as it stands. The half's row sum tells whether m still bounds the
-//     half's scores: only a sum above 2^20 (or inf / NaN, as on the first half, where m is -inf) makes the wave
-//     take the half's max (16 three-input maxes and the partner's over v_permlane32_swap), raise m, rescale O
-//     and l and redo P. P may thus reach 2^20, harmless in fp32 sums and bf16 P; O and l always share m, so
+//     half's scores: only a sum above 2^20 (and always the window's first half) makes the wave take the half's
+//     max (16 three-input maxes and the partner's over v_permlane32_swap), raise m, rescale O and l and redo P
+//     shifted by the rise. P may thus reach 2^20, harmless in fp32 sums and bf16 P; O and l always share m, so
 //     O / l does not depend on where m sits.
+//   * With direct staging and head_dim below 32 DT (the shipped 48) V^T row D, a padding row, holds ones: the
+//     second product then accumulates the row sum of the bf16 P in O^T row D, and the VALU drops the adds. The
+//     trigger becomes the half's own max (8 three-input maxes): a score more than 20 above m.
 //   * key masking runs only in the last, partial block; padding keys are staged as zeros.
 //
 // Staging. An LDS tile holds 64 rows of 128 bytes, the eight 16-byte chunks of row r XOR-swizzled by (r / 2) % 8
@@ -65,6 +71,7 @@ constexpr int kRow = 64;      // LDS row stride in bf16 elements (128 bytes, 16-
 constexpr int kKTile = kKB * kRow;  // bf16 elements of one K sub-tile
 constexpr int kThreads = 256;
 constexpr float kSumHigh = 1048576.0f;  // 2^20: a half's row sum above it makes the running max be raised
+constexpr float kMaxHigh = 20.0f;       // the same bound on a single score above the running max (log2 units)
 constexpr float kFltMax = 3.40282347e38f;
 // Windows are ranked by length inside every workgroup (each thread compares its candidates against all windows);
 // beyond this many windows that quadratic cost is not worth the balance and the grid keeps the window order.
@@ -193,7 +200,27 @@ struct Stage {
 // Global -> registers for the key block starting at kv0. K pass r: sub-tile r / 2, chunk c = thread + 256 (r % 2)
 // (key c / 8, head_dim chunk 8 (r / 2) + c % 8); V^T pass r: rows 32 r .. 32 r + 31; row-major V as K.
 // TAIL: the block holds keys >= L (they are staged as zeros). vt_vec: V^T rows allow vector loads.
-template <bool FP8, bool VT, int DT, bool TAIL>
+template <bool FP8>
+__device__ __forceinline__ typename Raw<FP8>::type raw_one() {
+  if constexpr (FP8) {
+    return make_uint2(0x38383838u, 0x38383838u);  // e4m3 1.0
+  } else {
+    return make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);  // bf16 1.0
+  }
+}
+
+// The same with only the first of the 8 elements 1.0 (head_dim D of a row-major V row, when D % 8 == 0).
+template <bool FP8>
+__device__ __forceinline__ typename Raw<FP8>::type raw_one_first() {
+  if constexpr (FP8) {
+    return make_uint2(0x38u, 0u);
+  } else {
+    return make_uint4(0x3F80u, 0u, 0u, 0u);
+  }
+}
+
+// ONES: V^T row D (the first padding row) is staged as ones, so that the second product forms the row sum.
+template <bool FP8, bool VT, int DT, bool TAIL, bool ONES = false>
 __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnParams& p,
                                            const typename Elem<FP8>::T* K, const typename Elem<FP8>::T* V, int L,
                                            int kv0, int dchunks, bool vt_vec) {
@@ -204,7 +231,10 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnPa
     const int kg = kv0 + key;
     const bool ok = dc < dchunks && (!TAIL || kg < L);
     st.k[r] = ok ? load8_vec<FP8>(K + kg * p.sk_k + dc * 8) : raw_zero<FP8>();
-    if constexpr (!VT) st.v[r] = ok ? load8_vec<FP8>(V + kg * p.sv_k + dc * 8) : raw_zero<FP8>();
+    if constexpr (!VT) {
+      st.v[r] = ok ? load8_vec<FP8>(V + kg * p.sv_k + dc * 8)
+                   : ((ONES && dc == dchunks) ? raw_one_first<FP8>() : raw_zero<FP8>());
+    }
   }
   if constexpr (VT) {
 #pragma unroll
@@ -217,7 +247,7 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnPa
         const int valid = TAIL ? ((L - kg) < 8 ? (L - kg) : 8) : 8;
         st.v[r] = (vt_vec && valid == 8) ? load8_vec<FP8>(src) : load8_scalar<FP8>(src, valid);
       } else {
-        st.v[r] = raw_zero<FP8>();
+        st.v[r] = (ONES && d == p.D) ? raw_one<FP8>() : raw_zero<FP8>();
       }
     }
   }
@@ -346,9 +376,11 @@ __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" 
 // kDirectFull (the same at head_dim 32 DT). The last, partial block of a window always goes through registers.
 enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2 };
 
-template <bool FP8, bool VT, int STAGING, int DT>
+// ONES: head_dim below 32 DT, the row sum comes from the matrix cores (V^T row D of ones).
+template <bool FP8, bool VT, int STAGING, int DT, bool ONES>
 __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   constexpr bool DIRECT = STAGING != kRegister;
+  static_assert(!ONES || STAGING != kDirectFull, "a full-width head has no padding row");
   constexpr int kSubTiles = Width<DT>::kSubTiles;
   // Four distinct LDS objects (not one indexed array): the compiler can then tell the direct loads into one
   // buffer from the operand reads of the other and does not wait for the loads in flight before those reads.
@@ -431,7 +463,11 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
     const int d0 = 16 * s + 8 * hh;
     uint4 raw = make_uint4(0u, 0u, 0u, 0u);
     if (q_ok && d0 < p.D) raw = *reinterpret_cast<const uint4*>(Qp + q * p.sq_q + d0);
-    qf[s] = __builtin_bit_cast(bf16x8_t, raw);
+    // Q pre-scaled by scale * log2(e) (and the e4m3 K scale), rounded to bf16: the scores come out in log2 units.
+    const bf16x8_t qb = __builtin_bit_cast(bf16x8_t, raw);
+    typedef float f32x8_t __attribute__((ext_vector_type(8)));
+    const f32x8_t qs = __builtin_convertvector(qb, f32x8_t) * sl2;
+    qf[s] = __builtin_convertvector(qs, bf16x8_t);
   }
 
   using T = typename Elem<FP8>::T;
@@ -459,6 +495,12 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
         }
       }
     }
+    if (ONES && threadIdx.x < 16) {
+      // Direct loads never write V^T rows >= D: row D of both buffers holds ones for the whole kernel.
+      const int R = static_cast<int>(p.D), c = threadIdx.x & 7;
+      uint16_t* buf = threadIdx.x < 8 ? sV0 : sV1;
+      *reinterpret_cast<uint4*>(buf + R * kRow + swz(R, c) * 8) = raw_one<false>();
+    }
   }
 
   // Operand reads: lane (col, hh) takes logical chunk 2 s + hh of rows col and 32 + col of a tile; the two rows
@@ -475,6 +517,10 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   for (int j = 0; j < DT; ++j) o[j] = f32x16_t{0};
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
   float l = 0.f;                // row-sum partial of this lane's keys
+  // The score accumulators start at -mc (the MFMA's C operand), so they hold S - mc; mc = m after the first half.
+  float mc = 0.f;
+  f32x16_t negm = {0};
+  bool first = true;            // uniform: the window's first half always takes the max
 
   // Full block `blk` into (sK, sV): issued now, complete at the next vmem wait (direct) or at `stage_commit`
   // (registers, prefetched into `st`).
@@ -485,7 +531,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
       stage_direct<DT, STAGING == kDirectFull>(dl, static_cast<uint32_t>(kv0 * p.sk_k * 2), static_cast<uint32_t>(kv0 * 2),
                                          w, sK, sV);
     } else {
-      stage_load<FP8, VT, DT, false>(st, p, K, V, L, blk * kKB, dchunks, vt_vec);
+      stage_load<FP8, VT, DT, false, ONES>(st, p, K, V, L, blk * kKB, dchunks, vt_vec);
     }
   };
   auto stage_commit = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
@@ -494,7 +540,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   // The partial block, synchronously through registers.
   auto stage_tail = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
     Stage<FP8, VT, DT> tmp;
-    stage_load<FP8, VT, DT, true>(tmp, p, K, V, L, nfull * kKB, dchunks, vt_vec);
+    stage_load<FP8, VT, DT, true, ONES>(tmp, p, K, V, L, nfull * kKB, dchunks, vt_vec);
     stage_store<FP8, VT, DT>(tmp, sK, sV);
   };
 
@@ -509,13 +555,13 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       // S^T of keys 32 t .. 32 t + 31 (LDS rows 32 t + col); k-steps past head_dim (zero in Q) are skipped.
-      f32x16_t s = {0};
+      f32x16_t s;
 #pragma unroll
       for (int k = 0; k < 2 * DT; ++k) {
-        if (k < ksteps) {
+        if (k == 0 || k < ksteps) {
           const bf16x8_t a =
               *reinterpret_cast<const bf16x8_t*>(kp + (k >> 2) * (kKTile * 2) + rd[k & 3] + t * (32 * kRow * 2));
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], k == 0 ? negm : s, 0, 0, 0);
         }
       }
       if constexpr (MASKED) {
@@ -526,18 +572,20 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
           if (kv0 + 32 * t + kin >= L) s[i] = -INFINITY;
         }
       }
-      // P^T = exp2(S^T * scale*log2e - m) against the running max m as it stands, as B operands: k-step ks (keys
-      // 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7. The row sum is taken over the fp32 P.
+      // P^T = exp2(S^T - m) against the running max m as it stands (the accumulators already hold S - mc, mc = m
+      // after the first half), as B operands: k-step ks (keys 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7.
+      // The row sum is taken over the fp32 P (unless the matrix cores form it).
       bf16x8_t pb[2];
       float lb;
-      auto exps = [&](float neg_m) __attribute__((always_inline)) {
+      auto exps = [&](auto shifted, float d) __attribute__((always_inline)) {
+        constexpr bool SHIFT = decltype(shifted)::value;
         float pair[8];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
           for (int j = 0; j < 8; j += 2) {
-            f32x2_t two = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j], sl2, neg_m)),
-                           __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j + 1], sl2, neg_m))};
+            f32x2_t two = {__builtin_amdgcn_exp2f(SHIFT ? s[8 * ks + j] - d : s[8 * ks + j]),
+                           __builtin_amdgcn_exp2f(SHIFT ? s[8 * ks + j + 1] - d : s[8 * ks + j + 1])};
             const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
             pair[4 * ks + j / 2] = two[0] + two[1];
             pb[ks][j] = c[0];
@@ -548,25 +596,18 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
         // co-execute with the matrix cores on gfx950).
         lb = ((pair[0] + pair[1]) + (pair[2] + pair[3])) + ((pair[4] + pair[5]) + (pair[6] + pair[7]));
       };
-      exps(-m);
-      // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN, as before
-      // the first half, where m is -inf) some score passed m by about 20 (log2 units). Only then is the half's
-      // max taken, m raised, O and l rescaled and P redone; O and l always share m, so O / l does not depend on
-      // where m sits.
-      if (__builtin_amdgcn_ballot_w64(!(lb <= kSumHigh)) != 0ull) {
-        // Max of the raw scores (scale > 0, so it commutes with the scaling). The chain opens with a
-        // compiler-visible v_med3_f32 (med3(a, b, FLT_MAX) = max(a, b) for scores below +inf), before which the
-        // compiler inserts the wait states a VALU read of an MFMA result needs; the inline v_max3_f32 that follow
-        // (the compiler does not check inline asm for that hazard) read the same, by then complete,
-        // accumulator. The partner lane's max comes over v_permlane32_swap, which gives (x[l % 32],
-        // x[l % 32 + 32]) in every lane. Every query has a key below L in the first half, so m is finite after
-        // it.
-        float mr = __builtin_amdgcn_fmed3f(s[0], s[1], kFltMax);
-#pragma unroll
-        for (int i = 2; i < 16; i += 2) mr = max3(mr, s[i], s[i + 1]);
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mr), __float_as_int(mr), false, false);
-        mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
-        const float cand = mr * sl2;
+      // The slow path: the half's max (S - mc; the chain opens with a compiler-visible v_med3_f32, med3(a, b,
+      // FLT_MAX) = max(a, b) for scores below +inf, before which the compiler inserts the wait states a VALU read
+      // of an MFMA result needs; the inline v_max3_f32 that follow, which the compiler does not check for that
+      // hazard, read the same, by then complete, accumulator) joined with the partner lane's over
+      // v_permlane32_swap, which gives (x[l % 32], x[l % 32 + 32]) in every lane; m raised to it, O and l
+      // rescaled, P redone shifted by the rise, the C operand moved to -m. Every query has a key below L in the
+      // first half, so m is finite after it.
+      auto raise = [&](float mx) __attribute__((always_inline)) {
+        first = false;
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
+        const float mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
+        const float cand = mr + mc;
         const float mn = cand > m ? cand : m;
         const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first half
         m = mn;
@@ -576,9 +617,31 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
 #pragma unroll
           for (int j = 0; j < DT; ++j) o[j][i] *= alpha;
         }
-        exps(-m);
+        exps(std::true_type{}, mn - mc);
+        mc = mn;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) negm[i] = -mn;
+      };
+      auto half_max = [&]() __attribute__((always_inline)) {
+        float mx = __builtin_amdgcn_fmed3f(s[0], s[1], kFltMax);
+#pragma unroll
+        for (int i = 2; i < 16; i += 2) mx = max3(mx, s[i], s[i + 1]);
+        return mx;
+      };
+      if constexpr (ONES) {
+        // The half's own max decides: a score more than kMaxHigh above m raises it (P of the fast path stays
+        // below 2^kMaxHigh); the row sum accumulates in O^T row D.
+        const float mx = half_max();
+        exps(std::false_type{}, 0.f);
+        if (first || __builtin_amdgcn_ballot_w64(mx > kMaxHigh) != 0ull) raise(mx);
+      } else {
+        // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN) some
+        // score passed m by about 20 (log2 units). Only then (and on the window's first half, where m is -inf)
+        // is the slow path taken.
+        exps(std::false_type{}, 0.f);
+        if (first || __builtin_amdgcn_ballot_w64(!(lb <= kSumHigh)) != 0ull) raise(half_max());
+        l += lb;
       }
-      l += lb;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         // O^T += V^T . P^T for this k-step: V^T columns 32 t + 16 ks + 8 hh + 0..7 are logical chunk 2 (2 t + ks) + hh
@@ -631,7 +694,7 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
       // The partial block's loads are in flight during the last full block (the other tiles are free since the
       // last barrier).
       Stage<FP8, VT, DT> tl;
-      if (tail) stage_load<FP8, VT, DT, true>(tl, p, K, V, L, nfull * kKB, dchunks, vt_vec);
+      if (tail) stage_load<FP8, VT, DT, true, ONES>(tl, p, K, V, L, nfull * kKB, dchunks, vt_vec);
       compute(Full{}, cK, cV, blk * kKB);
       if (tail) {
         stage_store<FP8, VT, DT>(tl, nK, nV);
@@ -645,7 +708,20 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
   }
 
   float lsum = l;
-  {
+  if constexpr (ONES) {
+    // O^T row D = the row sum, entry 4 (r / 8) of tile D / 32 in the lanes of half 0 (r = D % 32, a multiple of 8).
+    const int jd = static_cast<int>(p.D) / 32, gd = (static_cast<int>(p.D) % 32) / 8;
+    float v = 0.f;
+#pragma unroll
+    for (int j = 0; j < DT; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        if (j == jd && g == gd) v = o[j][4 * g];
+      }
+    }
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    lsum = __int_as_float(sw[0]);
+  } else {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(lsum), __float_as_int(lsum), false, false);
     lsum = __int_as_float(sw[0]) + __int_as_float(sw[1]);
   }
@@ -676,22 +752,33 @@ __global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
 
 // The instantiation for DT = head_dim / 32 rounded up: e4m3 and row-major forms through registers, bf16 V^T
 // directly to LDS (head_dim 32 DT without exec masking).
-template <int DT>
-void launch(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool vt, bool direct) {
+template <int DT, bool ONES>
+void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool vt, bool direct) {
   if (fp8) {
     if (vt) {
-      xattn_fwd_kernel<true, true, kRegister, DT><<<g, kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<true, true, kRegister, DT, ONES><<<g, kThreads, 0, s>>>(p);
     } else {
-      xattn_fwd_kernel<true, false, kRegister, DT><<<g, kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<true, false, kRegister, DT, ONES><<<g, kThreads, 0, s>>>(p);
     }
-  } else if (direct && p.D == 32 * DT) {
-    xattn_fwd_kernel<false, true, kDirectFull, DT><<<g, kThreads, 0, s>>>(p);
+  } else if (direct && !ONES) {
+    xattn_fwd_kernel<false, true, kDirectFull, DT, false><<<g, kThreads, 0, s>>>(p);
   } else if (direct) {
-    xattn_fwd_kernel<false, true, kDirect, DT><<<g, kThreads, 0, s>>>(p);
+    xattn_fwd_kernel<false, true, kDirect, DT, true><<<g, kThreads, 0, s>>>(p);
   } else if (vt) {
-    xattn_fwd_kernel<false, true, kRegister, DT><<<g, kThreads, 0, s>>>(p);
+    xattn_fwd_kernel<false, true, kRegister, DT, ONES><<<g, kThreads, 0, s>>>(p);
   } else {
-    xattn_fwd_kernel<false, false, kRegister, DT><<<g, kThreads, 0, s>>>(p);
+    xattn_fwd_kernel<false, false, kRegister, DT, ONES><<<g, kThreads, 0, s>>>(p);
+  }
+}
+
+// The instantiation for DT = head_dim / 32 rounded up: e4m3 and row-major forms through registers, bf16 V^T
+// directly to LDS; head_dim below 32 DT takes the row sum from the matrix cores.
+template <int DT>
+void launch(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool vt, bool direct) {
+  if (p.D < 32 * DT) {
+    launch_dt<DT, true>(p, g, s, fp8, vt, direct);
+  } else {
+    launch_dt<DT, false>(p, g, s, fp8, vt, direct);
   }
 }
 
