@@ -376,9 +376,11 @@ __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" 
 // kDirectFull (the same at head_dim 32 DT). The last, partial block of a window always goes through registers.
 enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2 };
 
-// ONES: head_dim below 32 DT, the row sum comes from the matrix cores (V^T row D of ones).
+// ONES: head_dim below 32 DT, the row sum comes from the matrix cores (V^T row D of ones). The e4m3 V^T kernel up
+// to head_dim 64 is held to 168 VGPRs (three waves per SIMD; it needs 170 unbounded, without spilling at 168); the
+// bf16 direct-staged ones fit by themselves.
 template <bool FP8, bool VT, int STAGING, int DT, bool ONES>
-__global__ __launch_bounds__(kThreads, 2) void xattn_fwd_kernel(XattnParams p) {
+__global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
   constexpr bool DIRECT = STAGING != kRegister;
   static_assert(!ONES || STAGING != kDirectFull, "a full-width head has no padding row");
   constexpr int kSubTiles = Width<DT>::kSubTiles;
