@@ -171,13 +171,15 @@ def rotary_attention(attn, x, positions):
     return attn.proj(out.view(b, n, d))
 
 
-def block_forward(block, x, time, positions):
+def block_forward(block, x, time, positions, modulation=None):
     """UnconditionalBlock.forward: with `time` [B,W] the AdaLN block (unconditional_md4_timefree.py:60-63), with
-    time None the affine-LayerNorm block (unconditional_md4.py:52-56). x [B,N,W] bf16, positions [B,N,3]."""
-    if time is None:
+    time None the affine-LayerNorm block (unconditional_md4.py:52-56). x [B,N,W] bf16, positions [B,N,3].
+    `modulation` [B, 6W] (optional) is `block.ada(time)` computed beforehand (a step batches the projections of all
+    blocks into one GEMM: they share the time vector)."""
+    if time is None and modulation is None:
         x, h = residual_norm(x, rotary_attention(block.attn, layer_norm(x, block.norm1), positions), None, block.norm2)
         return residual_norm(x, block.mlp(h))
-    s1, c1, g1, s2, c2, g2 = block.ada(time).chunk(6, -1)
+    s1, c1, g1, s2, c2, g2 = (block.ada(time) if modulation is None else modulation).chunk(6, -1)
     a = rotary_attention(block.attn, layer_norm(x, block.norm1, s1, c1), positions)
     x, h = residual_norm(x, a, g1, block.norm2, s2, c2)
     return residual_norm(x, block.mlp(h), g2)

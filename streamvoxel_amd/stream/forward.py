@@ -10,14 +10,15 @@ Kernels: `svhip_patch_embed` (patchify), the block path of `backbone` (`svhip_la
 `svhip_xattn_fwd`, `svhip_residual_norm`), `svhip_axial_rope` + `svhip_xattn_fwd` over `CachedContext` (cross
 attention), `svhip_residual_norm` for every residual sum and `svhip_layer_norm` for the final norm. The Linear
 layers and the small time / height embeddings stay the model's torch modules, run under bf16 autocast as in the
-reference (fast_ops.py:312).
+reference (fast_ops.py:312); the blocks' AdaLN projections of a trunk run as one GEMM per step (they share the
+time vector).
 """
 from __future__ import annotations
 
 import torch
 
 from streamvoxel_amd import _lib
-from streamvoxel_amd.stream.backbone import layer_norm, residual_norm, run_block
+from streamvoxel_amd.stream.backbone import block_forward, layer_norm, residual_norm
 from streamvoxel_amd.stream.patches import PatchLogits
 from streamvoxel_amd.stream.producer import axial_rope
 
@@ -69,10 +70,33 @@ def cross_step(cross, value, positions, context, layer):
     return residual_norm(value, cross.proj(out.view(n, N, W)))
 
 
+class _AdaStack:
+    """The AdaLN projections (`ada` = SiLU, Linear(W, 6W)) of every block of a trunk, stacked into one weight: they
+    all act on the same time vector, so one GEMM per step gives every block's gates, shifts and scales."""
+
+    def __init__(self, blocks):
+        self.width = blocks[0].ada[1].in_features
+        self.weight = torch.cat([b.ada[1].weight.detach() for b in blocks], 0)
+        self.bias = torch.cat([b.ada[1].bias.detach() for b in blocks], 0)
+
+    def __call__(self, time):
+        out = torch.nn.functional.linear(torch.nn.functional.silu(time), self.weight, self.bias)
+        return out.view(len(time), -1, 6 * self.width).unbind(1)
+
+
+def _ada_stack(trunk):
+    blocks = list(trunk.blocks)
+    if not blocks or not all(hasattr(b, 'ada') and isinstance(b.ada[0], torch.nn.SiLU) for b in blocks):
+        return None
+    return _AdaStack(blocks)
+
+
 class StepForward:
     """FastSlotForward.forward for the model `model` (the reference's StreamingControlNet / compact form, or a
     module with the same attributes: backbone, control, cross, zero, layer_map) over the cached context `context`
-    (one layer per control block). Weights are used in their own dtype under bf16 autocast."""
+    (one layer per control block). Weights are used in their own dtype under bf16 autocast. The patch tables and
+    the stacked AdaLN projections are taken from the weights when the object is built (as the reference's
+    GatherPatch tables are); build a new one after loading other weights."""
 
     def __init__(self, model, context):
         self.model, self.context = model, context
@@ -80,6 +104,8 @@ class StepForward:
         self.patch_b, self.patch_c = GatherPatch(bb.target_patch), GatherPatch(cc.target_patch)
         self.layer_map = getattr(model, 'layer_map', None) or {i: i for i in range(bb.depth)}
         self.timed = hasattr(bb, 'time_encoding')
+        self.ada_b = _ada_stack(bb) if self.timed else None
+        self.ada_c = _ada_stack(cc) if self.timed else None
         if len(model.cross) != context.layers:
             raise ValueError('the context needs one layer per cross-attention')
 
@@ -102,14 +128,17 @@ class StepForward:
         c = residual_norm(self.patch_c(tokens), cc.y_embed(y).to(torch.bfloat16))
         bt = bb.time_encoding(timestep) if self.timed else None
         ct = cc.time_encoding(timestep) if self.timed else None
+        mod_b = self.ada_b(bt) if self.ada_b is not None else [None] * bb.depth
+        mod_c = self.ada_c(ct) if self.ada_c is not None else [None] * len(cc.blocks)
         for i in range(bb.depth):
             j = self.layer_map.get(i)
             if j is None:
-                b = run_block(bb.blocks[i], b, bt, sa_positions)
+                b = block_forward(bb.blocks[i], b, bt, sa_positions, mod_b[i])
                 continue
-            c = run_block(cc.blocks[j], c, ct, sa_positions)
+            c = block_forward(cc.blocks[j], c, ct, sa_positions, mod_c[j])
             c = cross_step(model.cross[j], c, positions, self.context, j)
-            b = residual_norm(run_block(bb.blocks[i], b, bt, sa_positions), model.zero[j](c).to(torch.bfloat16))
+            b = residual_norm(block_forward(bb.blocks[i], b, bt, sa_positions, mod_b[i]),
+                              model.zero[j](c).to(torch.bfloat16))
         if self.timed:
             shift, gain = bb.final_ada(bt).chunk(2, -1)
             h = layer_norm(b, bb.final_norm, shift, gain)
