@@ -115,3 +115,44 @@ def test_step_forward_against_oracle(dev):
     err = (got - ref).abs()
     assert float(err.max()) <= 4e-2 * float(ref.abs().max()), (float(err.max()), float(ref.abs().max()))
     assert float(err.mean()) <= 1e-2 * float(ref.abs().mean()), (float(err.mean()), float(ref.abs().mean()))
+
+
+def test_step_forward_graph_replays_equal_eager(dev):
+    """The step forward captured in one graph and replayed three times with new tokens, timesteps and origins written
+    into its static inputs (eager work and synchronisations between the replays): every replay's class-head rows
+    equal the eager forward's on the same inputs bit for bit."""
+    from streamvoxel_amd.stream.forward import StepForward
+    from streamvoxel_amd.stream.step import CachedContext
+    _case('step forward graph replays')
+    model = _small_model(dev)
+    n, H, D, kcap = 2, 4, 24, 192
+    ctx = CachedContext(2, n, H, D, kcap, dev)
+    g = torch.Generator().manual_seed(21)
+    for j in range(2):
+        for b, L in enumerate([120, 64]):
+            ctx.write(j, b, (torch.randn(H, L, D, generator=g) / 2).to(torch.bfloat16).to(dev),
+                      torch.randn(H, L, D, generator=g).to(torch.bfloat16).to(dev))
+    step = StepForward(model, ctx)
+    tokens = torch.zeros(n, 32, 8, 8, dtype=torch.int64, device=dev)
+    timestep = torch.zeros(n, device=dev)
+    origin = torch.zeros(n, 3, device=dev)
+    group = torch.tensor([0.0, -64.0, 0.0], device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(tokens, timestep, origin, group)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = step(tokens, timestep, origin, group)
+    for r in range(3):
+        tokens.copy_(torch.randint(0, 17, (n, 32, 8, 8), generator=g).to(dev))
+        timestep.copy_(torch.rand(n, generator=g).to(dev))
+        origin.copy_(torch.tensor([[16.0 * r, -64.0, 0.0], [0.0, -64.0, 16.0 * r]], device=dev))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = captured.patches.clone()
+        eager = step(tokens, timestep, origin, group).patches
+        torch.randn(1000, device=dev).sum()                       # unrelated eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), r
