@@ -46,6 +46,27 @@ __device__ __forceinline__ float bf16_bits_to_float(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
+// Round to nearest even bf16 in hardware (v_cvt_pk_bf16_f32, two values per instruction). Equal to the integer
+// rounding (u + 0x7fff + lsb) >> 16 for every non-NaN value; a NaN comes out as the quiet NaN.
+typedef __bf16 svhip_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float svhip_f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t bf16_pack2(float a, float b) {
+  const svhip_f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, svhip_bf16x2_t));
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+
+// Both values rounded to bf16 and back to fp32.
+__device__ __forceinline__ void bf16_round2(float& a, float& b) {
+  const uint32_t p = bf16_pack2(a, b);
+  a = __uint_as_float(p << 16);
+  b = __uint_as_float(p & 0xffff0000u);
+}
+
+__device__ __forceinline__ float bf16_round1(float f) { return __uint_as_float(static_cast<uint32_t>(bf16_bits(f)) << 16); }
+
 template <typename T>
 __device__ __forceinline__ float to_float(T v);
 template <>

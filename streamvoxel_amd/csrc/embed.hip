@@ -22,12 +22,6 @@ constexpr int kEmbedTokens = kEmbedThreads / kEmbedLanes;  // patch tokens per w
 constexpr int kEmbedMaxOffsets = 64;                        // p^3 up to 4^3
 constexpr int kEmbedMaxWidth = 2048;
 
-__device__ __forceinline__ uint16_t embed_bf16_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-}
-
 struct EmbedArgs {
   const int64_t* tokens;  // (b, y, z, x) at b*stb + ((y*Z) + z)*X + x
   const uint16_t* table;  // [(C+1) * p^3, W]
@@ -111,13 +105,13 @@ __global__ __launch_bounds__(kEmbedThreads) void patch_embed_kernel(EmbedArgs a)
     uint32_t out[4];
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
-      float v[2];
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        v[e] = bf16_bits_to_float(embed_bf16_rne(acc[c][j + e]));
-        if (a.bias) v[e] += bf16_bits_to_float(a.bias[8 * ch + j + e]);
+      float v0 = acc[c][j], v1 = acc[c][j + 1];
+      bf16_round2(v0, v1);
+      if (a.bias) {
+        v0 += bf16_bits_to_float(a.bias[8 * ch + j]);
+        v1 += bf16_bits_to_float(a.bias[8 * ch + j + 1]);
       }
-      out[j / 2] = static_cast<uint32_t>(embed_bf16_rne(v[0])) | (static_cast<uint32_t>(embed_bf16_rne(v[1])) << 16);
+      out[j / 2] = bf16_pack2(v0, v1);
     }
     *reinterpret_cast<uint4*>(dst + 8 * ch) = make_uint4(out[0], out[1], out[2], out[3]);
   }

@@ -17,13 +17,7 @@ namespace svhip {
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxWidth = 2048;  // 64 lanes x 4 chunks x 8 elements
 
-__device__ __forceinline__ uint16_t norm_bf16_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-}
 
-__device__ __forceinline__ float norm_round(float f) { return bf16_bits_to_float(norm_bf16_rne(f)); }
 
 // Sum over the LPR lanes of a row (16: one DPP row; 64: the whole wave, the four DPP rows read back by readlane).
 template <int LPR>
@@ -105,15 +99,18 @@ __global__ __launch_bounds__(kNormThreads) void layer_norm_kernel(NormArgs a) {
         float g[8];
         load_row8<VEC>(gr + 8 * ch, g);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) br[j] = norm_round(g[j] * br[j]);
+        for (int j = 0; j < 8; j += 2) {
+          br[j] *= g[j];
+          br[j + 1] *= g[j + 1];
+          bf16_round2(br[j], br[j + 1]);
+        }
       }
       uint32_t out[4];
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
-        v[c][j] = norm_round(v[c][j] + br[j]);
-        v[c][j + 1] = norm_round(v[c][j + 1] + br[j + 1]);
-        out[j / 2] = static_cast<uint32_t>(norm_bf16_rne(v[c][j])) |
-                     (static_cast<uint32_t>(norm_bf16_rne(v[c][j + 1])) << 16);
+        out[j / 2] = bf16_pack2(v[c][j] + br[j], v[c][j + 1] + br[j + 1]);
+        v[c][j] = __uint_as_float(out[j / 2] << 16);
+        v[c][j + 1] = __uint_as_float(out[j / 2] & 0xffff0000u);
       }
       if (live) *reinterpret_cast<uint4*>(rr + 8 * ch) = make_uint4(out[0], out[1], out[2], out[3]);
     }
@@ -159,12 +156,17 @@ __global__ __launch_bounds__(kNormThreads) void layer_norm_kernel(NormArgs a) {
       load_row8<VEC>(sc + 8 * ch, s8);
       load_row8<VEC>(sh + 8 * ch, h8);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) t[j] = t[j] * norm_round(1.0f + s8[j]) + h8[j];
+      for (int j = 0; j < 8; j += 2) {
+        float o0 = 1.0f + s8[j], o1 = 1.0f + s8[j + 1];
+        bf16_round2(o0, o1);
+        t[j] = t[j] * o0 + h8[j];
+        t[j + 1] = t[j + 1] * o1 + h8[j + 1];
+      }
     }
     uint32_t out[4];
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
-      out[j / 2] = static_cast<uint32_t>(norm_bf16_rne(t[j])) | (static_cast<uint32_t>(norm_bf16_rne(t[j + 1])) << 16);
+      out[j / 2] = bf16_pack2(t[j], t[j + 1]);
     }
     *reinterpret_cast<uint4*>(yr + 8 * ch) = make_uint4(out[0], out[1], out[2], out[3]);
   }

@@ -23,13 +23,9 @@ constexpr int kTileKeys = 64;
 constexpr int kProducerThreads = 256;
 constexpr int kMaxHeadDim = 128;
 
-__device__ __forceinline__ uint16_t bf16_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-}
+__device__ __forceinline__ uint16_t bf16_rne(float f) { return bf16_bits(f); }
 
-__device__ __forceinline__ float bf16_round(float f) { return bf16_bits_to_float(bf16_rne(f)); }
+__device__ __forceinline__ float bf16_round(float f) { return bf16_round1(f); }
 
 // OCP e4m3fn (bias 7, 3 mantissa bits, no infinities, S.1111.111 = NaN, largest finite 448, quantum 2^-9 below
 // 2^-6), round to nearest even. Magnitudes above 464 (half way between 448 and the NaN code's 480) and NaN give
@@ -57,10 +53,15 @@ __device__ __forceinline__ uint8_t e4m3fn_rne(float x) {
   return sign | static_cast<uint8_t>(((e + 7) << 3) | static_cast<int>(m));
 }
 
-// One rotated pair (a, b) by sin s and cos c (already rounded to bf16).
+// One rotated pair (a, b) by sin s and cos c (already rounded to bf16): every product and both sums rounded to
+// bf16, two roundings per instruction.
 __device__ __forceinline__ void rope_rot(float a, float b, float s, float c, float& ra, float& rb) {
-  ra = bf16_round(bf16_round(a * c) - bf16_round(b * s));
-  rb = bf16_round(bf16_round(a * s) + bf16_round(b * c));
+  float ac = a * c, bs = b * s, as = a * s, bc = b * c;
+  bf16_round2(ac, bs);
+  bf16_round2(as, bc);
+  ra = ac - bs;
+  rb = as + bc;
+  bf16_round2(ra, rb);
 }
 
 // One rotated pair: (a, b) at phase p.
@@ -73,9 +74,7 @@ __device__ __forceinline__ void unpack2(uint32_t w, float& a, float& b) {
   b = __uint_as_float(w & 0xffff0000u);
 }
 
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return static_cast<uint32_t>(bf16_rne(a)) | (static_cast<uint32_t>(bf16_rne(b)) << 16);
-}
+__device__ __forceinline__ uint32_t pack2(float a, float b) { return bf16_pack2(a, b); }
 
 struct RopeArgs {
   const uint16_t* x;

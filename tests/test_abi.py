@@ -68,6 +68,21 @@ def test_product_refuses_host_tensors():
         top_mask(torch.zeros(8), torch.ones(8, dtype=torch.bool), 3)
 
 
+def test_block_path_refuses_host_tensors():
+    import torch
+    from streamvoxel_amd.stream.backbone import layer_norm, qkv_rope, residual_norm
+    from streamvoxel_amd.stream.forward import GatherPatch
+    x = torch.zeros(1, 4, 48, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match='GPU'):
+        layer_norm(x, torch.nn.LayerNorm(48))
+    with pytest.raises(RuntimeError, match='GPU'):
+        residual_norm(x, x)
+    with pytest.raises(RuntimeError, match='GPU'):
+        qkv_rope(torch.zeros(1, 4, 144, dtype=torch.bfloat16), torch.zeros(1, 4, 3), torch.ones(8), 1)
+    with pytest.raises(RuntimeError, match='GPU'):
+        GatherPatch(torch.nn.Conv3d(3, 16, 4, stride=4))(torch.zeros(1, 4, 4, 4, dtype=torch.int64))
+
+
 def test_argument_errors_of_the_newer_entry_points(lib):
     fake = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails its host checks first
     # patch order: non-power-of-two window or patch larger than the window

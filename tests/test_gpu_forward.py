@@ -156,3 +156,43 @@ def test_step_forward_graph_replays_equal_eager(dev):
         torch.randn(1000, device=dev).sum()                       # unrelated eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(replayed, eager), r
+
+
+def test_step_forward_over_an_e4m3_context(dev):
+    """The same small step over a cached context stored as e4m3 codes with per-(window, head) scales (written by
+    svhip_kv_write from the bf16 keys and values): against the float64 step on the dequantised keys and values,
+    within the e4m3 bar of the attention (5e-2 of max |reference|, max-abs) and 1e-2 of mean |reference|."""
+    from oracle import attention as A
+    from streamvoxel_amd.stream.forward import StepForward
+    from streamvoxel_amd.stream.step import CachedContext
+    if not hasattr(torch, 'float8_e4m3fn'):
+        pytest.skip('torch without float8_e4m3fn')
+    _case('step forward e4m3 context')
+    model = _small_model(dev)
+    n, H, D, kcap = 2, 4, 24, 192
+    lengths = [150, 37]
+    ctx = CachedContext(2, n, H, D, kcap, dev, kv_dtype='fp8')
+    g = torch.Generator().manual_seed(31)
+    keys, values = [], []
+    for j in range(2):
+        for b in range(n):
+            k = (torch.randn(H, lengths[b], D, generator=g) / 2).to(torch.bfloat16)
+            v = torch.randn(H, lengths[b], D, generator=g).to(torch.bfloat16)
+            ctx.write(j, b, k.to(dev), v.to(dev))
+        ks = ctx.k_scale[j].cpu()[:, :, None, None]
+        vs = ctx.v_scale[j].cpu()[:, :, None, None]
+        keys.append(A.dequant_e4m3(ctx.k[j].view(torch.uint8).cpu(), ks))
+        values.append(A.dequant_e4m3(ctx.vt[j].view(torch.uint8).cpu().transpose(2, 3), vs))
+    tokens = torch.randint(0, 17, (n, 32, 8, 8), generator=g)
+    timestep = torch.tensor([0.4, 0.6])
+    origin = torch.tensor([[16.0, -64.0, 32.0], [0.0, -64.0, 48.0]])
+    group = torch.tensor([0.0, -64.0, 16.0])
+    out = StepForward(model, ctx)(tokens.to(dev), timestep.to(dev), origin.to(dev), group.to(dev))
+    torch.cuda.synchronize()
+    params = {k: v.cpu() for k, v in model.state_dict().items()}
+    ref = O.step_forward(params, tokens, timestep, origin, group, keys, values, lengths, depth=3, heads=4,
+                         control_heads=H, layer_map=model.layer_map, patch=4, y_range=(-64.0, 192.0), time_dim=256,
+                         voxel_shape=(32, 8, 8))
+    err = (out.patches.float().cpu().double() - ref).abs()
+    assert float(err.max()) <= 5e-2 * float(ref.abs().max()), (float(err.max()), float(ref.abs().max()))
+    assert float(err.mean()) <= 1e-2 * float(ref.abs().mean()), (float(err.mean()), float(ref.abs().mean()))
