@@ -7,8 +7,8 @@
 // variance in fp32 over the row held in registers (one HBM read of each input); 1 + scale is rounded to bf16 as
 // the reference's bf16 tensors compute it, the rest is fp32 and y is rounded once.
 //
-// HBM-bound: rows up to 1024 wide take 16 lanes each (4 rows per wave, sums over DPP within the 16-lane row),
-// wider rows a whole wave; 16-byte loads and stores of the rows and of the per-window gate / shift / scale rows
+// HBM-bound: rows of 256 to 1024 in multiples of 256 take 32 lanes each (2 rows per wave), other rows up to 1024
+// wide 16 lanes (4 rows per wave, sums over DPP within the 16-lane row), wider rows a whole wave; 16-byte loads and stores of the rows and of the per-window gate / shift / scale rows
 // when those are 16-byte aligned.
 #include "common.hpp"
 
@@ -19,11 +19,14 @@ constexpr int kNormMaxWidth = 2048;  // 64 lanes x 4 chunks x 8 elements
 
 
 
-// Sum over the LPR lanes of a row (16: one DPP row; 64: the whole wave, the four DPP rows read back by readlane).
+// Sum over the LPR lanes of a row (16: one DPP row; 32: two DPP rows joined by a lane swap across 16; 64: the
+// whole wave, the four DPP rows read back by readlane).
 template <int LPR>
 __device__ __forceinline__ float row_sum(float v) {
   v = row16_sum(v);
-  if constexpr (LPR == 64) {
+  if constexpr (LPR == 32) {
+    v += __shfl_xor(v, 16, 64);  // the other 16-lane row of the pair
+  } else if constexpr (LPR == 64) {
     v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)) +
         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
@@ -176,7 +179,16 @@ template <bool RES, bool VEC>
 void launch_norm(const NormArgs& a, hipStream_t s) {
   const int64_t rows = a.B * a.N;
   const int64_t chunks = a.W / 8;
-  if (chunks <= 16 * 8) {
+  if (chunks % 32 == 0 && chunks <= 32 * 4) {
+    // Rows of 256, 512, 768 or 1024: 32 lanes per row, two rows per wave (twice the waves of 16 lanes per row).
+    const unsigned g = static_cast<unsigned>(cdiv(rows, kNormThreads / 32));
+    switch (chunks / 32) {
+      case 1: layer_norm_kernel<32, 1, RES, VEC><<<g, kNormThreads, 0, s>>>(a); break;
+      case 2: layer_norm_kernel<32, 2, RES, VEC><<<g, kNormThreads, 0, s>>>(a); break;
+      case 3: layer_norm_kernel<32, 3, RES, VEC><<<g, kNormThreads, 0, s>>>(a); break;
+      default: layer_norm_kernel<32, 4, RES, VEC><<<g, kNormThreads, 0, s>>>(a); break;
+    }
+  } else if (chunks <= 16 * 8) {
     const unsigned g = static_cast<unsigned>(cdiv(rows, kNormThreads / 16));
     if (chunks <= 16 * 2) {
       layer_norm_kernel<16, 2, RES, VEC><<<g, kNormThreads, 0, s>>>(a);
