@@ -87,25 +87,59 @@ struct RopeArgs {
   int64_t spb, spn;
 };
 
+constexpr int kRopeTokens = 8;  // tokens per workgroup of the rotation kernel
+
+// Workgroup = (b, 8 tokens), all heads: the tile's sin / cos (rounded to bf16) of every (token, pair) go to LDS once
+// (the phase depends on the token and the pair, not on the head), then every (token, head) row is rotated, 4 pairs
+// (16 bytes) per item when VEC (rows 16-byte aligned), else one pair.
+template <bool VEC>
 __global__ __launch_bounds__(kProducerThreads) void axial_rope_kernel(RopeArgs a) {
-  const int64_t pairs = a.D / 2;
-  const int64_t per_axis = a.D / 6;  // pairs per axis = number of frequencies
-  const int64_t total = a.B * a.H * a.N * pairs;
-  for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
-       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t pr = t % pairs;
-    int64_t r = t / pairs;
-    const int64_t n = r % a.N;
-    r /= a.N;
-    const int64_t h = r % a.H;
-    const int64_t b = r / a.H;
-    const int64_t axis = pr / per_axis, i = pr - axis * per_axis;
-    const float phase = a.pos[b * a.spb + n * a.spn + axis] * a.freq[i];
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(a.x + b * a.sxb + h * a.sxh + n * a.sxn + 2 * pr);
-    float x0, x1, r0, r1;
-    unpack2(w, x0, x1);
-    rope_pair(x0, x1, phase, r0, r1);
-    *reinterpret_cast<uint32_t*>(a.out + b * a.sob + h * a.soh + n * a.son + 2 * pr) = pack2(r0, r1);
+  __shared__ float2 sc[kRopeTokens * kMaxHeadDim / 2];
+  const int64_t tiles = cdiv(a.N, kRopeTokens);
+  const int64_t b = blockIdx.x / tiles, n0 = (blockIdx.x % tiles) * kRopeTokens;
+  const int tokens = static_cast<int>(a.N - n0 < kRopeTokens ? a.N - n0 : kRopeTokens);
+  const int pairs = static_cast<int>(a.D / 2);
+  const int per_axis = static_cast<int>(a.D / 6);  // pairs per axis = number of frequencies
+  for (int i = threadIdx.x; i < tokens * pairs; i += kProducerThreads) {
+    const int t = i / pairs, pr = i - t * pairs;
+    const int axis = pr / per_axis, fi = pr - axis * per_axis;
+    const float phase = a.pos[b * a.spb + (n0 + t) * a.spn + axis] * a.freq[fi];
+    sc[i] = make_float2(bf16_round(sinf(phase)), bf16_round(cosf(phase)));
+  }
+  __syncthreads();
+  constexpr int kPer = VEC ? 4 : 1;  // pairs per item
+  const int groups = pairs / kPer;
+  const int items = tokens * static_cast<int>(a.H) * groups;
+  for (int i = threadIdx.x; i < items; i += kProducerThreads) {
+    const int g = i % groups;
+    const int th = i / groups;
+    const int h = th % static_cast<int>(a.H), t = th / static_cast<int>(a.H);
+    const int64_t n = n0 + t;
+    const uint16_t* src = a.x + b * a.sxb + h * a.sxh + n * a.sxn + 2 * kPer * g;
+    uint16_t* dst = a.out + b * a.sob + h * a.soh + n * a.son + 2 * kPer * g;
+    uint32_t in[kPer], out[kPer];
+    if constexpr (VEC) {
+      const uint4 w = *reinterpret_cast<const uint4*>(src);
+      in[0] = w.x;
+      in[1] = w.y;
+      in[2] = w.z;
+      in[3] = w.w;
+    } else {
+      in[0] = *reinterpret_cast<const uint32_t*>(src);
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const float2 r = sc[t * pairs + kPer * g + j];
+      float x0, x1, r0, r1;
+      unpack2(in[j], x0, x1);
+      rope_rot(x0, x1, r.x, r.y, r0, r1);
+      out[j] = pack2(r0, r1);
+    }
+    if constexpr (VEC) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(out[0], out[1], out[2], out[3]);
+    } else {
+      *reinterpret_cast<uint32_t*>(dst) = out[0];
+    }
   }
 }
 
@@ -402,13 +436,22 @@ extern "C" int svhip_axial_rope(const void* x, void* out, const float* positions
                     sx_b % 2 == 0 && sx_h % 2 == 0 && sx_n % 2 == 0 && so_b % 2 == 0 && so_h % 2 == 0 &&
                     so_n % 2 == 0,
                 "%s: rows must start on 4-byte boundaries (head_dim contiguous)", name);
+  SVHIP_REQUIRE(D <= kMaxHeadDim, "%s: head_dim %lld above %d", name, (long long)D, kMaxHeadDim);
   const int64_t total = B * H * N * (D / 2);
   if (total == 0) return SVHIP_OK;
   RopeArgs a{static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), positions, freq, B, H, N, D,
              sx_b, sx_h, sx_n, so_b, so_h, so_n, sp_b, sp_n};
-  int64_t grid = cdiv(total, kProducerThreads);
-  if (grid > 65536) grid = 65536;
-  axial_rope_kernel<<<static_cast<unsigned>(grid), kProducerThreads, 0, as_stream(stream)>>>(a);
+  const int64_t grid = B * cdiv(N, kRopeTokens);
+  SVHIP_REQUIRE(grid < (1ll << 31), "%s: grid too large", name);
+  // Four pairs per item when every row of x and out starts on a 16-byte boundary (head_dim a multiple of 8).
+  const bool vec = D % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0 && sx_b % 8 == 0 && sx_h % 8 == 0 && sx_n % 8 == 0 &&
+                   so_b % 8 == 0 && so_h % 8 == 0 && so_n % 8 == 0;
+  if (vec) {
+    axial_rope_kernel<true><<<static_cast<unsigned>(grid), kProducerThreads, 0, as_stream(stream)>>>(a);
+  } else {
+    axial_rope_kernel<false><<<static_cast<unsigned>(grid), kProducerThreads, 0, as_stream(stream)>>>(a);
+  }
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;
 }
