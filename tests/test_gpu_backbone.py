@@ -139,3 +139,30 @@ def test_block_against_oracle(dev, W, H, timed):
     params = {k: v.cpu() for k, v in block.state_dict().items()}
     ref = O.block(x, t, pos, params, H)
     _check_block(out, ref)
+
+
+def test_in_place_forms(dev):
+    """The forms the C ABI documents as allowed: the residual written over x (svhip_residual_norm with r = x) and
+    LayerNorm written over its input; both equal the out-of-place results bit for bit."""
+    from streamvoxel_amd import _lib
+    from streamvoxel_amd.stream.backbone import layer_norm, residual_norm
+    _case('in-place residual / layer_norm')
+    B, N, W = 2, 130, 768
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(B, N, W, generator=g).to(torch.bfloat16).to(dev)
+    a = torch.randn(B, N, W, generator=g).to(torch.bfloat16).to(dev)
+    ada = (torch.randn(B, 3 * W, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    gate, shift, scale = ada[:, :W], ada[:, W:2 * W], ada[:, 2 * W:]
+    norm = torch.nn.LayerNorm(W, elementwise_affine=False, eps=1e-6)
+    r_ref, y_ref = residual_norm(x, a, gate, norm, shift, scale)
+    xi = x.clone()
+    lib = _lib.load()
+    rc = lib.svhip_residual_norm(_lib.ptr(xi), _lib.ptr(a), _lib.ptr(gate), gate.stride(0), _lib.ptr(xi), None, None,
+                                 None, None, None, 0, B, N, W, xi.stride(0), xi.stride(1), a.stride(0), a.stride(1),
+                                 xi.stride(0), xi.stride(1), 0, 0, 1e-6, _lib.stream_of(xi))
+    assert rc == 0, lib.svhip_last_error()
+    yi = r_ref.clone()
+    layer_norm(yi, norm, shift, scale, out=yi)
+    torch.cuda.synchronize()
+    assert torch.equal(xi, r_ref)
+    assert torch.equal(yi, y_ref)

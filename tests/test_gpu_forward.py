@@ -28,12 +28,13 @@ def dev():
     return torch.device('cuda:0')
 
 
-@pytest.mark.parametrize('W,shape,C', [(768, (64, 16, 16), 304), (384, (32, 8, 8), 20), (200, (8, 4, 4), 3)])
-def test_gather_patch(dev, W, shape, C):
+@pytest.mark.parametrize('W,shape,C,p', [(768, (64, 16, 16), 304, 4), (384, (32, 8, 8), 20, 4), (200, (8, 4, 4), 3, 4),
+                                        (256, (16, 8, 8), 12, 2)])
+def test_gather_patch(dev, W, shape, C, p):
     from streamvoxel_amd.stream.forward import GatherPatch
-    _case(f'gather patch W={W} shape={shape} C={C}')
+    _case(f'gather patch W={W} shape={shape} C={C} p={p}')
     g = torch.Generator().manual_seed(W)
-    conv = torch.nn.Conv3d(C + 1, W, 4, stride=4)
+    conv = torch.nn.Conv3d(C + 1, W, p, stride=p)
     with torch.no_grad():
         conv.weight.copy_(torch.randn(conv.weight.shape, generator=g) * 0.3)
         conv.bias.copy_(torch.randn(W, generator=g))
@@ -44,7 +45,6 @@ def test_gather_patch(dev, W, shape, C):
     gp = GatherPatch(conv.to(dev))
     out = gp(tokens.to(dev))
     # the reference's form: patch_offsets + embedding_bag(mode='sum') + bias, in bf16
-    p = 4
     Y, Z, X = shape
     cells = tokens.reshape(B, Y // p, p, Z // p, p, X // p, p).permute(0, 1, 3, 5, 2, 4, 6).reshape(-1, p ** 3)
     index = (cells * p ** 3 + torch.arange(p ** 3)).to(dev)
