@@ -11,7 +11,9 @@ Kernels: `svhip_patch_embed` (patchify), the block path of `backbone` (`svhip_la
 attention), `svhip_residual_norm` for every residual sum and `svhip_layer_norm` for the final norm. The Linear
 layers and the small time / height embeddings stay the model's torch modules, run under bf16 autocast as in the
 reference (fast_ops.py:312); the blocks' AdaLN projections of a trunk run as one GEMM per step (they share the
-time vector).
+time vector). At every injection the control branch (control block, cross attention, zero projection) runs on a
+second stream beside the backbone block, which does not read it until the sum (same kernels, same bits; a step
+captured in a graph keeps the two branches).
 """
 from __future__ import annotations
 
@@ -98,8 +100,9 @@ class StepForward:
     the stacked AdaLN projections are taken from the weights when the object is built (as the reference's
     GatherPatch tables are); build a new one after loading other weights."""
 
-    def __init__(self, model, context):
+    def __init__(self, model, context, concurrent=True):
         self.model, self.context = model, context
+        self.side = torch.cuda.Stream(device=context.lengths.device) if concurrent else None
         bb, cc = model.backbone, model.control
         self.patch_b, self.patch_c = GatherPatch(bb.target_patch), GatherPatch(cc.target_patch)
         self.layer_map = getattr(model, 'layer_map', None) or {i: i for i in range(bb.depth)}
@@ -115,6 +118,30 @@ class StepForward:
         class head (n windows)."""
         with torch.autocast('cuda', dtype=torch.bfloat16):
             return self._forward(tokens, timestep, origin, group_origin)
+
+    def _injection(self, i, j, b, c, bt, ct, sa_positions, positions, mod_b, mod_c):
+        """Backbone block i with control block j injected (fast_ops.py:293-298): the control branch on the side
+        stream (when there is one) while the backbone block runs on the current stream."""
+        model = self.model
+        bb, cc = model.backbone, model.control
+
+        def control(c):
+            c = block_forward(cc.blocks[j], c, ct, sa_positions, mod_c)
+            c = cross_step(model.cross[j], c, positions, self.context, j)
+            return c, model.zero[j](c).to(torch.bfloat16)
+
+        if self.side is None:
+            c, z = control(c)
+            return residual_norm(block_forward(bb.blocks[i], b, bt, sa_positions, mod_b), z), c
+        main = torch.cuda.current_stream()
+        self.side.wait_stream(main)
+        with torch.cuda.stream(self.side):
+            c, z = control(c)
+        b = block_forward(bb.blocks[i], b, bt, sa_positions, mod_b)
+        main.wait_stream(self.side)
+        c.record_stream(main)
+        z.record_stream(main)
+        return residual_norm(b, z), c
 
     def _forward(self, tokens, timestep, origin, group_origin):
         model = self.model
@@ -135,10 +162,7 @@ class StepForward:
             if j is None:
                 b = block_forward(bb.blocks[i], b, bt, sa_positions, mod_b[i])
                 continue
-            c = block_forward(cc.blocks[j], c, ct, sa_positions, mod_c[j])
-            c = cross_step(model.cross[j], c, positions, self.context, j)
-            b = residual_norm(block_forward(bb.blocks[i], b, bt, sa_positions, mod_b[i]),
-                              model.zero[j](c).to(torch.bfloat16))
+            b, c = self._injection(i, j, b, c, bt, ct, sa_positions, positions, mod_b[i], mod_c[j])
         if self.timed:
             shift, gain = bb.final_ada(bt).chunk(2, -1)
             h = layer_norm(b, bb.final_norm, shift, gain)
