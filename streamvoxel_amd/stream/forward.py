@@ -11,9 +11,10 @@ Kernels: `svhip_patch_embed` (patchify), the block path of `backbone` (`svhip_la
 attention), `svhip_residual_norm` for every residual sum and `svhip_layer_norm` for the final norm. The Linear
 layers and the small time / height embeddings stay the model's torch modules, run under bf16 autocast as in the
 reference (fast_ops.py:312); the blocks' AdaLN projections of a trunk run as one GEMM per step (they share the
-time vector). At every injection the control branch (control block, cross attention, zero projection) runs on a
-second stream beside the backbone block, which does not read it until the sum (same kernels, same bits; a step
-captured in a graph keeps the two branches).
+time vector). The control branch (13 control blocks, each with its cross attention and zero projection) never
+reads the backbone, so it runs on a second stream from the start of the step while the backbone's 25 blocks run on
+the current one; the backbone waits only for each zero projection it adds (an event per injection). Same kernels,
+same bits; a step captured in a graph keeps the two branches.
 """
 from __future__ import annotations
 
@@ -143,6 +144,33 @@ class StepForward:
         z.record_stream(main)
         return residual_norm(b, z), c
 
+    def _two_streams(self, b, c, bt, ct, sa_positions, positions, mod_b, mod_c):
+        """The control chain on the side stream, an event after each zero projection; the backbone on the current
+        stream, waiting for event j before adding projection j after backbone block layer_map^-1(j)."""
+        model = self.model
+        bb, cc = model.backbone, model.control
+        main = torch.cuda.current_stream()
+        self.side.wait_stream(main)
+        zs = []
+        with torch.cuda.stream(self.side):
+            for j in range(len(cc.blocks)):
+                c = block_forward(cc.blocks[j], c, ct, sa_positions, mod_c[j])
+                c = cross_step(model.cross[j], c, positions, self.context, j)
+                z = model.zero[j](c).to(torch.bfloat16)
+                done = torch.cuda.Event()
+                done.record(self.side)
+                zs.append((z, done))
+        for i in range(bb.depth):
+            b = block_forward(bb.blocks[i], b, bt, sa_positions, mod_b[i])
+            j = self.layer_map.get(i)
+            if j is not None:
+                z, done = zs[j]
+                main.wait_event(done)
+                z.record_stream(main)
+                b = residual_norm(b, z)
+        main.wait_stream(self.side)
+        return b
+
     def _forward(self, tokens, timestep, origin, group_origin):
         model = self.model
         bb, cc = model.backbone, model.control
@@ -157,12 +185,15 @@ class StepForward:
         ct = cc.time_encoding(timestep) if self.timed else None
         mod_b = self.ada_b(bt) if self.ada_b is not None else [None] * bb.depth
         mod_c = self.ada_c(ct) if self.ada_c is not None else [None] * len(cc.blocks)
-        for i in range(bb.depth):
-            j = self.layer_map.get(i)
-            if j is None:
-                b = block_forward(bb.blocks[i], b, bt, sa_positions, mod_b[i])
-                continue
-            b, c = self._injection(i, j, b, c, bt, ct, sa_positions, positions, mod_b[i], mod_c[j])
+        if self.side is None:
+            for i in range(bb.depth):
+                j = self.layer_map.get(i)
+                if j is None:
+                    b = block_forward(bb.blocks[i], b, bt, sa_positions, mod_b[i])
+                    continue
+                b, c = self._injection(i, j, b, c, bt, ct, sa_positions, positions, mod_b[i], mod_c[j])
+        else:
+            b = self._two_streams(b, c, bt, ct, sa_positions, positions, mod_b, mod_c)
         if self.timed:
             shift, gain = bb.final_ada(bt).chunk(2, -1)
             h = layer_norm(b, bb.final_norm, shift, gain)
