@@ -253,6 +253,24 @@ int svhip_patch_embed(const int64_t* tokens, const void* table, const void* bias
                       int64_t Y, int64_t Z, int64_t X, int64_t patch, int64_t cells, int64_t W, int64_t st_b,
                       int64_t so_b, int64_t so_n, void* stream);
 
+/*
+ * Counter-based categorical sampling of the chosen voxels of `batch` windows [Y,Z,X], at a fixed launch size.
+ * Logit (b, class c, voxel v) at b*stride_b + c*stride_c + row(v)*stride_n, row(v) = v (patch == 0, YZX order) or
+ * the class head's patch order (patch > 0, row map as in svhip_entropy_patches). chosen u8 [batch, N]; values
+ * int16 [batch, N] gets the class of every chosen voxel and -1 elsewhere; tokens int64 [batch, N] (or NULL) gets the
+ * class of every chosen voxel, other entries untouched. seed, step: device int64 [batch]. Voxel v of window b draws
+ * u = (floor(w0 / 2^41) + 1/2) / 2^23 from Philox4x64-10 at counter (v, step[b], 0, 0) under key
+ * (seed[b], 0x53414D504C455631) and takes the first class whose softmax CDF passes u (fp32 sums). A chosen row with
+ * no finite maximum or a NaN sets *err (device int). classes <= 1024.
+ * Replaces (as a counter-based alternative with its own random stream): the tail of
+ * FastLowEntropyLastSlot.stage (streamvoxel/stream/fast_ops.py:548-553: nonzero_static -> gather -> softmax ->
+ * torch.multinomial -> index_copy_), whose sizes depend on the step's k.
+ */
+int svhip_sample_chosen(const void* logits, int dtype, int64_t classes, int64_t patch, int64_t stride_b,
+                        int64_t stride_c, int64_t stride_n, const uint8_t* chosen, int64_t* tokens, int16_t* values,
+                        const int64_t* seed, const int64_t* step, int* err, int64_t batch, int64_t Y, int64_t Z,
+                        int64_t X, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,6 +14,8 @@ Modules (each function cites the reference file:line it restates):
   producer.py   AxialRoPE, the cached-context window layout and the e4m3 cache quantisation.
   patches.py    the class head's patch order turned into [n, C, Y, Z, X] (explicit loops).
   backbone.py   the transformer block (LayerNorm, AdaLN modulation, GELU, rotary self-attention, MLP) in float64.
+  sampler.py    the counter-based sampling tail: Philox4x64-10 uniforms per (seed, step, voxel) and the inverse
+                softmax-CDF draw (float64).
 The checks that pin each function (closed forms, brute force, invariants, golden vectors) are the tests named
 tests/test_oracle*.py.
 
@@ -35,6 +37,10 @@ Parity status per function (what pins it):
   patches.to_class_major                loops against torch's permute of the reference's form; the 4^3 block order.
   backbone.layer_norm / gelu / silu     invariants (zero mean, var / (var + eps)), known values (Phi(1), sigmoid(1)),
                                         odd-part identities.
+  sampler.philox4x64 / uniforms         numpy.random.Philox (the same generator, one counter step apart); the
+                                        uniforms' fp32 format, moments and deciles.
+  sampler.invert / sample_chosen        closed forms (equal logits -> floor(u C), two-class and dominant-class
+                                        rows, -inf classes), frequencies against softmax over 20 000 draws.
   backbone.rotary_attention / block     closed forms: uniform scores -> proj(mean V), one token -> proj(v), zero
                                         positions -> brute-force attention, zero gates -> identity, unit gates with a
                                         zero MLP -> x + attn + bias.

@@ -57,6 +57,7 @@ SIGNATURES = {
     'svhip_residual_norm': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]
                             + [_c_i64] * 12 + [_c_f, _c_p]),
     'svhip_patch_embed': (ctypes.c_int, [_c_p] * 5 + [_c_i64] * 10 + [_c_p]),
+    'svhip_sample_chosen': (ctypes.c_int, [_c_p, ctypes.c_int] + [_c_i64] * 5 + [_c_p] * 6 + [_c_i64] * 4 + [_c_p]),
 }
 
 _lib = None

@@ -12,7 +12,10 @@ The device work of a window:
     of its count (the reference's `int(last.sum())`, stream/slot.py:130);
   * solid forward: `svhip_ease_select` (entropy, selectable = unfilled & not deferred, block-quota selection, the
     `bad` flag) into static buffers, capturable in a graph; then the eager tail the reference keeps in torch
-    (`nonzero_static` -> softmax -> multinomial -> `index_copy_`, fast_ops.py:548-553) and one pinned D2H copy;
+    (`nonzero_static` -> softmax -> multinomial -> `index_copy_`, fast_ops.py:548-553) and one pinned D2H copy.
+    With `sampler='philox'` the tail is `svhip_sample_chosen` instead, a counter-based draw per chosen voxel inside
+    the captured selection (a different random stream from the reference's), and the D2H copy is one int16 per
+    voxel;
   * finish: the deferred voxels are written as `air_token`.
 """
 from __future__ import annotations
@@ -24,6 +27,7 @@ from streamvoxel_amd.sampling.block_quota import QuotaWorkspace, block_view
 from streamvoxel_amd.sampling.low_entropy_last import low_entropy_last_quotas
 from streamvoxel_amd.sampling.schedule import actual_time
 from streamvoxel_amd.stream.patches import PatchLogits
+from streamvoxel_amd.stream.sampler import sample_chosen
 
 ORDER_SEED_OFFSET = 9173
 
@@ -78,12 +82,19 @@ def _class_major(logits, classes, total):
 class LowEntropyLastSlot:
     """One window of `shape` ([Y,Z,X]) inside a batched forward (stream/slot.py:50-176, with the solid steps of
     `FastLowEntropyLastSlot`, fast_ops.py:481-581). `entropy` names the score kernel; only 'hip' exists here.
-    `keep_scores=True` also leaves each solid step's fp32 scores in `self.scores` (for checking)."""
+    `keep_scores=True` also leaves each solid step's fp32 scores in `self.scores` (for checking).
+    `sampler` draws the chosen voxels' classes: 'multinomial' (the reference's tail: `torch.multinomial` on the
+    slot's generator, eager, k-sized) or 'philox' (`svhip_sample_chosen`: a counter-based draw per voxel keyed by
+    the window's seed and the solid step, inside `select` and thus inside a captured step; the host reads back one
+    int16 per voxel)."""
 
     def __init__(self, shape, classes, air_ids, air_token, last_eps, block_size, device, entropy='hip',
-                 keep_scores=False):
+                 keep_scores=False, sampler='multinomial'):
         if entropy != 'hip':
             raise ValueError("entropy must be 'hip' (the HIP entropy kernel)")
+        if sampler not in ('multinomial', 'philox'):
+            raise ValueError("sampler must be 'multinomial' or 'philox'")
+        self.sampler = sampler
         self.shape = tuple(int(s) for s in shape)
         if len(self.shape) != 3:
             raise ValueError('shape is [Y, Z, X]')
@@ -125,6 +136,13 @@ class LowEntropyLastSlot:
         self.workspace = QuotaWorkspace(1, self.shape, b, dev, fused=True)
         self._bound = False
         self._host = torch.empty(2 * self.total + 1, dtype=torch.int64, pin_memory=True)
+        if sampler == 'philox':
+            self.seed_dev = torch.zeros(1, dtype=torch.int64, device=dev)
+            self.step_dev = torch.zeros(1, dtype=torch.int64, device=dev)
+            self.sample_err = torch.zeros(1, dtype=torch.int32, device=dev)
+            self.drawn = torch.full(self.shape, -1, dtype=torch.int16, device=dev)
+            self._host16 = torch.empty(self.total, dtype=torch.int16, pin_memory=True)
+            self._host_flags = torch.empty(2, dtype=torch.int32, pin_memory=True)
 
     @property
     def idle(self):
@@ -143,6 +161,9 @@ class LowEntropyLastSlot:
         order_rng = torch.Generator(device=self.device).manual_seed(self.seed + ORDER_SEED_OFFSET)
         self.order = torch.randperm(blocks, device=self.device, generator=order_rng)
         self.generator = torch.Generator(device=self.device).manual_seed(self.seed)
+        if self.sampler == 'philox':
+            self.seed_dev.fill_(self.seed)
+            self.sample_err.zero_()
         self.step_map = torch.zeros(self.shape, dtype=torch.int16)
         self.values = torch.full(self.shape, -1, dtype=torch.int16)
         self._bound = False
@@ -205,6 +226,8 @@ class LowEntropyLastSlot:
         self.k.fill_(k)
         self.committed.fill_(committed)
         self.frac.fill_((committed + k) / (self.total - self.last_count))
+        if self.sampler == 'philox':
+            self.step_dev.fill_(self.solid_calls)
         return k
 
     def _patch_rows(self, logits):
@@ -218,7 +241,14 @@ class LowEntropyLastSlot:
     def select(self, logits, tokens):
         """Graph-capturable (fast_ops.py:534-540): reads logits [C,Y,Z,X] (or a PatchLogits of one window: the
         class head's output in place), tokens [Y,Z,X] int64 and the static buffers; writes `chosen` and `bad` (and
-        `scores` when kept). One fused kernel sequence, no host sync."""
+        `scores` when kept). One fused kernel sequence, no host sync. With the 'philox' sampler it also draws the
+        chosen voxels into `tokens` and `drawn` (the whole solid step on the device)."""
+        self._select(logits, tokens)
+        if self.sampler == 'philox':
+            sample_chosen(logits if isinstance(logits, PatchLogits) else logits.unsqueeze(0), self.chosen,
+                          self.seed_dev, self.step_dev, self.drawn, self.sample_err, tokens)
+
+    def _select(self, logits, tokens):
         _lib.require_gpu(tokens)
         if tokens.dtype != torch.int64 or tokens.shape != self.shape or not tokens.is_contiguous():
             raise ValueError('tokens must be a contiguous int64 [Y, Z, X] buffer')
@@ -251,6 +281,13 @@ class LowEntropyLastSlot:
             self.select(logits, tokens)
         else:
             graph.replay()
+        if self.sampler == 'philox':
+            self._host16.copy_(self.drawn.view(-1), non_blocking=True)
+            self._host_flags[:1].copy_(self.bad.int(), non_blocking=True)
+            self._host_flags[1:].copy_(self.sample_err, non_blocking=True)
+            event = torch.cuda.Event()
+            event.record()
+            return k, None, event, tokens
         index = torch.nonzero_static(self.chosen.reshape(-1), size=k).squeeze(1)
         if isinstance(logits, PatchLogits):
             rows = logits.gather(index)                                     # [k, C], voxels in index order
@@ -269,10 +306,21 @@ class LowEntropyLastSlot:
         """Wait for the step's copy and do the host bookkeeping (fast_ops.py:560-575)."""
         k, host, event, tokens = staged
         event.synchronize()
-        if int(host[2 * k]):
-            raise AssertionError('low-entropy-last solid step did not meet its quota')
-        positions = host[:k].clone()
-        values_cpu = host[k:2 * k].to(torch.int16)
+        if host is None:
+            # 'philox': the drawn classes of the whole window, -1 where not chosen.
+            if int(self._host_flags[0]):
+                raise AssertionError('low-entropy-last solid step did not meet its quota')
+            if int(self._host_flags[1]):
+                raise RuntimeError('probability tensor contains either `inf`, `nan` or element < 0')
+            positions = torch.nonzero(self._host16 >= 0).squeeze(1)
+            if len(positions) != k:
+                raise AssertionError(f'{len(positions)} voxels drawn for a quota of {k}')
+            values_cpu = self._host16[positions].clone()
+        else:
+            if int(host[2 * k]):
+                raise AssertionError('low-entropy-last solid step did not meet its quota')
+            positions = host[:k].clone()
+            values_cpu = host[k:2 * k].to(torch.int16)
         self.solid_calls += 1
         self.actual += 1
         self.nfe += 1
@@ -328,6 +376,11 @@ class SelectGraphs:
         if not getattr(engine, 'graphs', None):
             return
         device = engine.device
+        # Warm-up and capture select nothing (k = 0): a slot with the 'philox' sampler would otherwise draw into the
+        # engine's token rows. prepare() sets k before every step.
+        saved_k = [slot.k.clone() for slot in slots]
+        for slot in slots:
+            slot.k.zero_()
         current = torch.cuda.current_stream(device)
         warm = torch.cuda.Stream(device=device)
         warm.wait_stream(current)
@@ -346,9 +399,10 @@ class SelectGraphs:
                     with torch.cuda.graph(graph, pool=pool, stream=stream, capture_error_mode='thread_local'):
                         slots[i].select(out[i], engine.tokens[i])
                     self.graphs[size, i] = graph
-        for slot in slots:
+        for slot, k in zip(slots, saved_k):
             slot.chosen.zero_()
             slot.bad.zero_()
+            slot.k.copy_(k)
 
     def lookup(self, logits):
         for size, out in self.engine.outputs.items():

@@ -231,6 +231,31 @@ def test_transposed_v_padded_layout_fast_path(dev, D):
     assert torch.equal(out_direct, out_rows)
 
 
+@pytest.mark.parametrize('D', [64, 48, 32, 8])
+def test_direct_staging_every_block_count(dev, D):
+    """Direct staging alternates two LDS tile pairs and peels the last full block and the partial one: windows of
+    0..10 full blocks, with and without a partial last block, cover every entry into and exit from its unrolled
+    loop and both tile parities at the end. The result must match the float64 oracle and equal the row-major-V
+    path (staged through registers) bit for bit; every key block carries its own score scale and value offset, so
+    a block read from the wrong tile changes the result."""
+    from streamvoxel_amd.stream.attention import attention
+    lengths = [64 * n + t for n in range(11) for t in (0, 29) if 64 * n + t > 0]
+    B, H, Q, kcap = len(lengths), 2, 96, 704
+    _case(f'xattn direct block counts D={D} lengths={lengths}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=101 + D)
+    block = torch.arange(kcap) // 64
+    k = (k.float() * (1 + 0.37 * (block % 5)).view(1, 1, -1, 1)).to(torch.bfloat16)
+    v = (v.float() + 0.05 * block.view(1, 1, -1, 1)).to(torch.bfloat16)
+    ref = A.cross_attention(q, k, v, lengths)
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    vt = v.transpose(2, 3).contiguous().to(dev)
+    out_direct = attention(q.to(dev), k.to(dev), vt.transpose(2, 3), lengths=lt)
+    out_rows = attention(q.to(dev), k.to(dev), v.to(dev), lengths=lt)
+    torch.cuda.synchronize()
+    check(out_direct, ref, BF16_ATOL, BF16_RTOL)
+    assert torch.equal(out_direct, out_rows)
+
+
 @pytest.mark.parametrize('transposed,D', [(True, 64), (False, 64), (True, 96)])
 def test_score_scale_jumps_between_key_halves(dev, transposed, D):
     """Score magnitudes that jump up and down between 32-key halves (K rows scaled by 1 .. 90 and down to 1e-3):
