@@ -332,6 +332,62 @@ def step_forward_component(dev, lengths_seed=7):
     return t, lengths
 
 
+def sampling_tail_component(w, dev, s=12):
+    """The solid step's tail after the selection, for the 8 windows at solid step `s` of the schedule: the
+    reference's eager form per window (nonzero_static(k) -> gather -> softmax -> torch.multinomial -> index_copy_ ->
+    one D2H copy of positions and values, fast_ops.py:548-558) against the counter-based `svhip_sample_chosen`
+    (one launch over the 8 windows, capturable with the selection) and its D2H copy of one int16 per voxel. Times
+    with HIP events around the whole tail (the eager form includes its launch gaps)."""
+    import torch
+    from streamvoxel_amd.stream.sampler import sample_chosen
+    w.sel.k.copy_(w.k_tab[s])
+    w.sel.committed.copy_(w.com_tab[s])
+    w.sel.frac.copy_(w.frac_tab[s])
+    w.sel.tokens.fill_(CLASSES)
+    w.sel.run(w.logits[s])
+    torch.cuda.synchronize()
+    ks = [int(v) for v in w.k_tab[s].tolist()]
+    rows = w.logits[s].view(SLOTS, VOXELS, CLASSES)
+    chosen = w.sel.chosen.view(SLOTS, VOXELS)
+    tokens = w.sel.tokens.clone()
+    gens = [torch.Generator(device=dev).manual_seed(b) for b in range(SLOTS)]
+    hosts = [torch.empty(2 * k + 1, dtype=torch.int64, pin_memory=True) for k in ks]
+
+    def multinomial_tail():
+        for b in range(SLOTS):
+            index = torch.nonzero_static(chosen[b], size=ks[b]).squeeze(1)
+            probabilities = rows[b].index_select(0, index).float().softmax(-1)
+            values = torch.multinomial(probabilities, 1, generator=gens[b]).squeeze(-1)
+            tokens[b].index_copy_(0, index, values)
+            hosts[b].copy_(torch.cat((index, values, w.sel.bad[b:b + 1].long())), non_blocking=True)
+
+    logits5 = rows.view(SLOTS, *SHAPE, CLASSES).permute(0, 4, 1, 2, 3)
+    seeds = torch.arange(SLOTS, dtype=torch.int64, device=dev)
+    steps = torch.full((SLOTS,), s, dtype=torch.int64, device=dev)
+    drawn = torch.empty(SLOTS, *SHAPE, dtype=torch.int16, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    host16 = torch.empty(SLOTS * VOXELS, dtype=torch.int16, pin_memory=True)
+    chosen5 = chosen.view(SLOTS, *SHAPE)
+    tokens5 = tokens.view(SLOTS, *SHAPE)
+
+    def philox_kernel():
+        sample_chosen(logits5, chosen5, seeds, steps, drawn, err, tokens5)
+
+    def philox_tail():
+        philox_kernel()
+        host16.copy_(drawn.view(-1), non_blocking=True)
+
+    t_multi = time_events(multinomial_tail, 10)
+    t_kernel = time_graph(philox_kernel, 20)
+    t_philox = time_events(philox_tail, 10)
+    torch.cuda.synchronize()
+    assert int(err) == 0
+    drawn_per_window = (drawn >= 0).view(SLOTS, -1).sum(1).tolist()
+    assert drawn_per_window == ks, (drawn_per_window, ks)
+    return dict(solid_step=s, k_per_window=ks, multinomial_eager_us=t_multi * 1e6,
+                philox_kernel_us=t_kernel * 1e6, philox_with_d2h_us=t_philox * 1e6)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -407,6 +463,10 @@ def main():
         ctx8.write(0, b, w.ctx.k[0][b, :, :L], w.ctx.vt[0][b, :, :, :L].transpose(1, 2).contiguous())
     t_layer_e4m3 = time_graph(lambda: ctx8.attend(0, w.q[1][0], out=w.o[0].transpose(1, 2)), 20)
     del ctx8
+    tail = sampling_tail_component(w, dev)
+    log(f'sampling tail (8 windows, solid step {tail["solid_step"]}): multinomial eager '
+        f'{tail["multinomial_eager_us"]:.1f} us, counter-based kernel {tail["philox_kernel_us"]:.1f} us '
+        f'({tail["philox_with_d2h_us"]:.1f} us with its D2H copy)')
     t_forward = forward_lengths = None
     if not args.no_forward:
         t_forward, forward_lengths = step_forward_component(dev)
@@ -458,7 +518,8 @@ def main():
                                                              (t_forward + t_select304) * 1e3),
                         shipped_model_voxels_per_s=(None if t_forward is None else
                                                     SLOTS * VOXELS / (STEPS_PER_WINDOW * (t_forward + t_select304))),
-                        reference_fast_forward_rtx4090d_ms=44.0),
+                        reference_fast_forward_rtx4090d_ms=44.0,
+                        sampling_tail=tail),
         measured_peaks=peaks,
         cpu_baseline=cpu,
     )
