@@ -75,6 +75,9 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// PL: classes per lane held in registers (4, 8 or 16: up to 256, 512 or 1024 classes), so that short rows keep
+// more waves resident.
+template <int PL>
 __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t b = blockIdx.y;
@@ -95,10 +98,10 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
     todo &= todo - 1;
     const int64_t vox = base + i;
     const int64_t row = a.rows(vox) * a.sn;
-    float e[kSampleMaxPerLane];
+    float e[PL];
     float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kSampleMaxPerLane; ++j) {
+    for (int j = 0; j < PL; ++j) {
       const int c = c0 + j;
       e[j] = (j < cpl && c < a.C) ? load_logit(xb, a.dtype, row + c * a.sc) : -INFINITY;
       m = fmaxf(m, e[j]);
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
     const float mx = wave_max(m);
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < kSampleMaxPerLane; ++j) {
+    for (int j = 0; j < PL; ++j) {
       e[j] = fast_exp(e[j] - mx);
       s += e[j];
     }
@@ -136,7 +139,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
       int found = -1, last = -1;
       float run = excl;
 #pragma unroll
-      for (int j = 0; j < kSampleMaxPerLane; ++j) {
+      for (int j = 0; j < PL; ++j) {
         if (e[j] > 0.f) last = c0 + j;
         run += e[j];
         if (found < 0 && run > target && e[j] > 0.f) found = c0 + j;
@@ -192,7 +195,14 @@ extern "C" int svhip_sample_chosen(const void* logits, int dtype, int64_t classe
   a.N = N;
   const int64_t waves = cdiv(N, 64);
   const dim3 grid(static_cast<unsigned>(cdiv(waves, kSampleThreads / 64)), static_cast<unsigned>(batch));
-  sample_chosen_kernel<<<grid, kSampleThreads, 0, as_stream(stream)>>>(a);
+  const int64_t per_lane = cdiv(classes, 64);
+  if (per_lane <= 4) {
+    sample_chosen_kernel<4><<<grid, kSampleThreads, 0, as_stream(stream)>>>(a);
+  } else if (per_lane <= 8) {
+    sample_chosen_kernel<8><<<grid, kSampleThreads, 0, as_stream(stream)>>>(a);
+  } else {
+    sample_chosen_kernel<kSampleMaxPerLane><<<grid, kSampleThreads, 0, as_stream(stream)>>>(a);
+  }
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;
 }
