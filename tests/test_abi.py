@@ -122,3 +122,32 @@ def test_argument_errors_of_the_newer_entry_points(lib):
     assert rc == -1 and b'null' in lib.svhip_last_error()
     # the cache writer's workspace query grows with heads and capacity
     assert lib.svhip_kv_write_workspace_bytes(16, 12672) >= lib.svhip_kv_write_workspace_bytes(8, 9792) > 0
+
+
+def test_argument_errors_of_the_sampling_tail(lib):
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails its host checks first
+
+    def sample(dtype=0, classes=256, patch=0, shape=(16, 16, 16), err=fake, logits=fake, batch=1):
+        return lib.svhip_sample_chosen(logits, dtype, classes, patch, 16 ** 3 * classes, 1, classes, fake, fake, fake,
+                                       fake, fake, err, batch, *shape, None)
+
+    assert sample(classes=1025) == -1 and b'classes' in lib.svhip_last_error()
+    assert sample(classes=0) == -1 and b'classes' in lib.svhip_last_error()
+    assert sample(dtype=3) == -1 and b'dtype' in lib.svhip_last_error()
+    assert sample(err=None) == -1 and b'null' in lib.svhip_last_error()
+    assert sample(logits=None) == -1 and b'null' in lib.svhip_last_error()
+    assert sample(patch=4, shape=(16, 12, 16)) == -1 and b'power-of-two' in lib.svhip_last_error()
+    assert sample(patch=32) == -1 and b'larger than the window' in lib.svhip_last_error()
+    assert sample(batch=-1) == -1 and b'sizes' in lib.svhip_last_error()
+    # nothing to draw: returns without launching
+    assert sample(batch=0) == 0 and sample(shape=(0, 16, 16)) == 0
+
+
+def test_sampling_tail_refuses_host_tensors():
+    import torch
+    from streamvoxel_amd.stream.sampler import sample_chosen
+    shape = (4, 4, 4)
+    with pytest.raises(RuntimeError, match='GPU'):
+        sample_chosen(torch.zeros(8, *shape), torch.zeros(shape, dtype=torch.bool), torch.zeros(1, dtype=torch.int64),
+                      torch.zeros(1, dtype=torch.int64), torch.zeros(shape, dtype=torch.int16),
+                      torch.zeros(1, dtype=torch.int32))
