@@ -327,9 +327,38 @@ def step_forward_component(dev, lengths_seed=7):
     origin = torch.tensor([[16.0 * i, -64.0, 0.0] for i in range(SLOTS)], device=dev)
     group = torch.tensor([0.0, -64.0, 0.0], device=dev)
     t = time_graph(lambda: step(tokens, timestep, origin, group), 1, replays=5)
-    del step, ctx, model
+    # The whole solid step in one graph: the forward from the windows' token state, the EASE selection over the
+    # class head's bf16 rows in place (304 classes, 2 621 voxels per window of a fresh window) and the
+    # counter-based sampling tail drawing the chosen voxels into the same token state. The token state is reset to
+    # the mask token at the start of the step so that every replay does the same work.
+    from streamvoxel_amd.stream.sampler import sample_chosen
+    from streamvoxel_amd.stream.step import EaseSelect
+    classes = 304
+    sel = EaseSelect(SLOTS, SHAPE, classes, BLOCK, dev)
+    k = VOXELS // (STEPS_PER_WINDOW - 1)
+    for b in range(SLOTS):
+        sel.bind_window(b, torch.randperm(VOXELS // BLOCK ** 3, generator=torch.Generator().manual_seed(b)))
+        sel.set_step(b, k, 0, k / VOXELS)
+    state = sel.tokens.view(SLOTS, *SHAPE)
+    seeds = torch.arange(SLOTS, dtype=torch.int64, device=dev)
+    steps = torch.zeros(SLOTS, dtype=torch.int64, device=dev)
+    drawn = torch.empty(SLOTS, *SHAPE, dtype=torch.int16, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def whole_step():
+        state.fill_(classes)
+        logits = step(state, timestep, origin, group)
+        sel.run(logits)
+        sample_chosen(logits, sel.chosen.view(SLOTS, *SHAPE), seeds, steps, drawn, err, state)
+
+    t_whole = time_graph(whole_step, 1, replays=5)
+    torch.cuda.synchronize()
+    filled = (state != classes).view(SLOTS, -1).sum(1).tolist()
+    if int(err) != 0 or bool(sel.bad.any()) or filled != [k] * SLOTS:
+        raise RuntimeError(f'whole-step check failed: err={int(err)} bad={sel.bad.tolist()} filled={filled}')
+    del step, ctx, model, sel
     torch.cuda.empty_cache()
-    return t, lengths
+    return t, lengths, t_whole
 
 
 def sampling_tail_component(w, dev, s=12):
@@ -398,9 +427,9 @@ def main():
     streamvoxel_amd.load()
     dev = torch.device('cuda:0')
     if args.forward_only:
-        t_forward, lengths = step_forward_component(dev)
+        t_forward, lengths, t_whole = step_forward_component(dev)
         print(json.dumps(dict(component='shipped_step_forward', ms=t_forward * 1e3, slots=SLOTS, kv_lengths=lengths,
-                              reference_fast_forward_rtx4090d_ms=44.0)), flush=True)
+                              whole_step_ms=t_whole * 1e3, reference_fast_forward_rtx4090d_ms=44.0)), flush=True)
         return
     t0 = time.perf_counter()
     w = Workload(dev, args.seed, args.kv_dtype)
@@ -467,10 +496,11 @@ def main():
     log(f'sampling tail (8 windows, solid step {tail["solid_step"]}): multinomial eager '
         f'{tail["multinomial_eager_us"]:.1f} us, counter-based kernel {tail["philox_kernel_us"]:.1f} us '
         f'({tail["philox_with_d2h_us"]:.1f} us with its D2H copy)')
-    t_forward = forward_lengths = None
+    t_forward = forward_lengths = t_whole = None
     if not args.no_forward:
-        t_forward, forward_lengths = step_forward_component(dev)
-        log(f'whole step forward (shipped shape, 8 windows) {t_forward * 1e3:.2f} ms')
+        t_forward, forward_lengths, t_whole = step_forward_component(dev)
+        log(f'whole step forward (shipped shape, 8 windows) {t_forward * 1e3:.2f} ms; forward + select + sampling '
+            f'in one graph {t_whole * 1e3:.2f} ms')
     xattn_tflops = w.flops_per_layer / t_layer / 1e12
     select_gbs = w.select_bytes / t_select / 1e9
     entropy_bytes = SLOTS * VOXELS * (CLASSES * 4 + 4)
@@ -518,6 +548,9 @@ def main():
                                                              (t_forward + t_select304) * 1e3),
                         shipped_model_voxels_per_s=(None if t_forward is None else
                                                     SLOTS * VOXELS / (STEPS_PER_WINDOW * (t_forward + t_select304))),
+                        shipped_whole_step_one_graph_ms=None if t_whole is None else t_whole * 1e3,
+                        shipped_whole_step_voxels_per_s=(None if t_whole is None else
+                                                         SLOTS * VOXELS / (STEPS_PER_WINDOW * t_whole)),
                         reference_fast_forward_rtx4090d_ms=44.0,
                         sampling_tail=tail),
         measured_peaks=peaks,
