@@ -243,10 +243,14 @@ class LowEntropyLastSlot:
         class head's output in place), tokens [Y,Z,X] int64 and the static buffers; writes `chosen` and `bad` (and
         `scores` when kept). One fused kernel sequence, no host sync. With the 'philox' sampler it also draws the
         chosen voxels into `tokens` and `drawn` (the whole solid step on the device)."""
-        self._select(logits, tokens)
+        x = self._select(logits, tokens)
         if self.sampler == 'philox':
-            sample_chosen(logits if isinstance(logits, PatchLogits) else logits.unsqueeze(0), self.chosen,
-                          self.seed_dev, self.step_dev, self.drawn, self.sample_err, tokens)
+            if not isinstance(logits, PatchLogits):
+                # the class-major tensor the selection read, as [1, C, Y, Z, X] (its voxels are one strided axis)
+                Y, Z, X = self.shape
+                sc, sn = x.stride(0), x.stride(1)
+                logits = x.as_strided((1, self.classes, Y, Z, X), (0, sc, Z * X * sn, X * sn, sn))
+            sample_chosen(logits, self.chosen, self.seed_dev, self.step_dev, self.drawn, self.sample_err, tokens)
 
     def _select(self, logits, tokens):
         _lib.require_gpu(tokens)
@@ -272,6 +276,7 @@ class LowEntropyLastSlot:
             _lib.ptr(self.pos), _lib.ptr(self.frac), _lib.ptr(self.n_total), _lib.ptr(self.committed),
             _lib.ptr(self.chosen.view(torch.uint8)), _lib.ptr(self.bad.view(torch.uint8)), _lib.ptr(self.scores),
             _lib.ptr(self.workspace.buffer), self.workspace.buffer.numel(), _lib.stream_of(x)), 'svhip_ease_select')
+        return x
 
     def stage(self, logits, tokens, graph=None):
         """Selection (eager, or a replay of `graph`, a captured `select`), then the eager tail; no host wait.

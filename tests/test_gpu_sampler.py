@@ -213,3 +213,31 @@ def test_philox_slot_window_eager_equals_graph_and_oracle_draws(dev):
     assert torch.equal(tok_e, engine.tokens[0])
     assert commits == len(eager.quotas) and rec_e is not None
     assert int((tok_e == CLASSES).sum()) == 0
+
+
+def test_philox_slot_reads_voxel_row_views(dev):
+    """Logits handed to a 'philox' slot as a view of voxel rows (class stride 1) are sampled where the selection
+    read them: the slot's draws equal `sample_chosen` over the same values in class planes on the slot's own
+    chosen mask, seed and step."""
+    from streamvoxel_amd.stream.sampler import sample_chosen
+    from streamvoxel_amd.stream.slot import LowEntropyLastSlot
+    from tests.test_gpu_slot import AIR, AIR_TOKEN, CAP, CLASSES, EPS as LEL_EPS, SHAPE, marking_logits, solid_logits
+    _case('philox slot, voxel-row view of the logits')
+    slot = LowEntropyLastSlot(SHAPE, CLASSES, AIR, AIR_TOKEN, LEL_EPS, 4, dev, sampler='philox')
+    slot.arm(seed=77, cap=CAP, target=(0, 0, 0))
+    tokens = torch.full(SHAPE, CLASSES, dtype=torch.int64, device=dev)
+    slot.consume(marking_logits(9, dev), tokens)                      # the marking forward
+    planes = solid_logits(901, 1, CAP + 1, dev).contiguous()           # [C, Y, Z, X]
+    rows_view = planes.permute(1, 2, 3, 0).contiguous().permute(3, 0, 1, 2)
+    assert rows_view.stride(0) == 1
+    k = slot.prepare()
+    before = tokens.clone()
+    slot.select(rows_view, tokens)
+    torch.cuda.synchronize()
+    assert int(slot.chosen.sum()) == k and int(slot.sample_err) == 0
+    values, _, _, err = _buffers(1, SHAPE, dev)
+    want_tokens = before.clone()
+    sample_chosen(planes, slot.chosen, slot.seed_dev, slot.step_dev, values, err, want_tokens.view(1, *SHAPE))
+    torch.cuda.synchronize()
+    assert torch.equal(slot.drawn, values.view(SHAPE))
+    assert torch.equal(tokens, want_tokens)
