@@ -52,6 +52,9 @@ def parse():
     p.add_argument('--no-forward', action='store_true', help='skip the whole-step forward component')
     p.add_argument('--forward-only', action='store_true',
                    help='time only the whole-step forward (shipped shape) and print its line')
+    p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'select'],
+                   help='build only that kernel\'s inputs (the step\'s layer-0 attention or its first solid '
+                        'selection), time 20 back-to-back launches and print one line: the run to profile')
     return p.parse_args()
 
 
@@ -417,6 +420,40 @@ def sampling_tail_component(w, dev, s=12):
                 philox_kernel_us=t_kernel * 1e6, philox_with_d2h_us=t_philox * 1e6)
 
 
+def kernel_only(dev, args):
+    """One kernel of the step alone, on the step's own inputs: the cross-attention layer (8 windows, 12 x 64 heads,
+    1024 queries, the step's key lengths; bf16 or e4m3 cache) or the first solid selection (8 windows, fp32 logits
+    [8 x 65536, 256], fresh token state). 20 launches in one graph, replayed 5 times."""
+    import torch
+    from streamvoxel_amd import synth
+    from streamvoxel_amd.stream.step import CachedContext, EaseSelect
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    lengths = synth.kv_lengths(SLOTS, args.seed)
+    if args.kernel.startswith('xattn'):
+        kv_dtype = 'fp8' if args.kernel == 'xattn_e4m3' else 'bf16'
+        ctx = CachedContext(1, SLOTS, HEADS, HEAD_DIM, synth.MAX_KEYS, dev, kv_dtype)
+        w = torch.randn(WIDTH, 2 * WIDTH, device=dev, generator=g) / math.sqrt(WIDTH)
+        for b, L in enumerate(lengths):
+            kv = (torch.randn(L, WIDTH, device=dev, generator=g) @ w).reshape(L, 2, HEADS, HEAD_DIM).permute(1, 2, 0, 3)
+            ctx.write(0, b, kv[0].to(torch.bfloat16), kv[1].to(torch.bfloat16))
+        q = (torch.randn(SLOTS, QUERIES, HEADS, HEAD_DIM, device=dev, generator=g) / 8).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        t = time_graph(lambda: ctx.attend(0, q.transpose(1, 2), out=o.transpose(1, 2)), 20)
+        flops = 4 * HEADS * HEAD_DIM * QUERIES * sum(lengths)
+        return dict(kernel=args.kernel, us_per_launch=t * 1e6, TFLOPs=flops / t / 1e12, flops_per_launch=flops,
+                    kv_lengths=lengths)
+    sel = EaseSelect(SLOTS, SHAPE, CLASSES, BLOCK, dev, air_ids=(0,))
+    logits = torch.empty(SLOTS * VOXELS, CLASSES, device=dev)
+    synth.bimodal_logits_(logits, 0.7, generator=g)
+    k = VOXELS // (STEPS_PER_WINDOW - 1)
+    for b in range(SLOTS):
+        sel.bind_window(b, torch.randperm(VOXELS // BLOCK ** 3, generator=torch.Generator().manual_seed(b)))
+        sel.set_step(b, k, 0, k / VOXELS)
+    t = time_graph(lambda: sel.run(logits), 20)
+    nbytes = SLOTS * VOXELS * (CLASSES * 4 + 8 + 1 + 1)
+    return dict(kernel=args.kernel, us_per_call=t * 1e6, GBps=nbytes / t / 1e9, bytes_per_call=nbytes)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -430,6 +467,9 @@ def main():
         t_forward, lengths, t_whole = step_forward_component(dev)
         print(json.dumps(dict(component='shipped_step_forward', ms=t_forward * 1e3, slots=SLOTS, kv_lengths=lengths,
                               whole_step_ms=t_whole * 1e3, reference_fast_forward_rtx4090d_ms=44.0)), flush=True)
+        return
+    if args.kernel:
+        print(json.dumps(kernel_only(dev, args)), flush=True)
         return
     t0 = time.perf_counter()
     w = Workload(dev, args.seed, args.kv_dtype)

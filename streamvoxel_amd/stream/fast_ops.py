@@ -11,11 +11,16 @@ import torch
 from streamvoxel_amd.sampling.block_quota import quota_select, top_mask
 from streamvoxel_amd.sampling.entropy import entropy_scores
 from streamvoxel_amd.stream.attention import attention
+from streamvoxel_amd.stream.engine import RECOMMENDED, SlotEngine
 from streamvoxel_amd.stream.producer import cross_query, local_kv
 from streamvoxel_amd.stream.slot import FastLowEntropyLastSlot, SelectGraphs, consume_batch
 
-__all__ = ['local_kv', 'cross_query', 'cross_flex', 'cross_sdpa', 'entropy_torch', 'entropy_triton',
-           'top_mask_nosync', 'quota_select_nosync', 'FastLowEntropyLastSlot', 'SelectGraphs', 'consume_batch']
+__all__ = ['RECOMMENDED', 'FastSlotForward', 'local_kv', 'cross_query', 'cross_flex', 'cross_sdpa', 'entropy_torch',
+           'entropy_triton', 'top_mask_nosync', 'quota_select_nosync', 'FastLowEntropyLastSlot', 'SelectGraphs',
+           'consume_batch']
+
+# fast_ops.py:164-375: the slot engine the worker drives (tokens, load_slot, wait_loads, replay, numerical_gate).
+FastSlotForward = SlotEngine
 
 
 def _project(cross, out, batch, queries, width):

@@ -182,6 +182,8 @@ class StepModel(torch.nn.Module):
         indices = [0] if control_depth == 1 else [round(i * (depth - 1) / (control_depth - 1))
                                                   for i in range(control_depth)]
         self.layer_map = {idx: j for j, idx in enumerate(indices)}
+        # The condition layout of the shipped model (biome window of halo 4 pooled by 2: 288 local biome keys).
+        self.biome_halo, self.biome_patch = 4, 2
         g = torch.Generator().manual_seed(seed + 3)
         with torch.no_grad():
             for m in [*self.cross.modules(), *self.zero]:
@@ -189,3 +191,32 @@ class StepModel(torch.nn.Module):
                     bound = (6.0 / (m.in_features + m.out_features)) ** 0.5
                     m.weight.copy_((torch.rand(m.weight.shape, generator=g) * 2 - 1) * bound)
                     m.bias.copy_(torch.randn(m.bias.shape, generator=g) * 0.02)
+
+
+class WindowSpec:
+    """The window geometry the slot engine reads from the reference's ModelSpec (streamvoxel/stream/condition.py):
+    height, tile (windows of height x tile x tile voxels), num_classes and y_origin. Defaults: the shipped model."""
+
+    def __init__(self, height=256, tile=16, num_classes=304, y_origin=-64.0):
+        self.height, self.tile, self.num_classes, self.y_origin = int(height), int(tile), int(num_classes), y_origin
+
+
+def condition(model, prefix_keys, local_keys, seed, device, scale=1.0):
+    """A seeded synthetic window condition in the layout the reference's encoders produce (the encoders and their
+    inputs are not part of this library): per cross-attention layer a prefix (K, V) [H, P, D] bf16 (K of unit
+    variance times `scale`), local context features [1, L, W] ~ N(0, 1) (the encoders end in a LayerNorm) and their
+    XYZ positions [1, L, 3] in patch units (x, z in [-8, 8), y in [0, 64))."""
+    from streamvoxel_amd.stream.engine import Encoded
+    g = torch.Generator().manual_seed(seed)
+    cross = model.cross[0]
+    H, W = int(cross.heads), int(cross.width)
+    D = W // H
+    prefix = []
+    for _ in model.cross:
+        k = (torch.randn(H, prefix_keys, D, generator=g) * scale).to(torch.bfloat16)
+        v = torch.randn(H, prefix_keys, D, generator=g).to(torch.bfloat16)
+        prefix.append((k.to(device), v.to(device)))
+    local = torch.randn(1, local_keys, W, generator=g)
+    positions = torch.rand(1, local_keys, 3, generator=g) * torch.tensor([16.0, 64.0, 16.0]) - torch.tensor(
+        [8.0, 0.0, 8.0])
+    return Encoded(prefix, local.to(device), positions.to(device))
