@@ -8,9 +8,10 @@ from streamvoxel_amd.stream import fast_ops
 
 def test_reference_names_exported():
     want = {'local_kv', 'cross_query', 'cross_flex', 'cross_sdpa', 'entropy_torch', 'entropy_triton',
-            'top_mask_nosync', 'quota_select_nosync', 'FastLowEntropyLastSlot', 'SelectGraphs', 'consume_batch'}
+            'top_mask_nosync', 'quota_select_nosync', 'FastLowEntropyLastSlot', 'SelectGraphs', 'consume_batch',
+            'FastSlotForward', 'RECOMMENDED'}
     assert want == set(fast_ops.__all__)
-    assert all(callable(getattr(fast_ops, name)) for name in want)
+    assert all(callable(getattr(fast_ops, name)) for name in want - {'RECOMMENDED'})
 
 
 def test_host_tensors_are_refused():
