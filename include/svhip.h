@@ -4,7 +4,8 @@
  * Every entry point takes caller-owned device pointers, plain sizes and strides (in elements), and a HIP stream
  * (`hipStream_t` passed as `void*`); it enqueues work on that stream and returns without synchronising, so calls
  * can be recorded into a HIP graph. No entry point allocates device memory: scratch space comes from a
- * caller-provided workspace whose size the matching `*_workspace_bytes` query returns.
+ * caller-provided workspace whose size the matching `*_workspace_bytes` query returns (svhip_ease_select_noalloc
+ * uses a fixed device array of the library instead).
  *
  * Return value: SVHIP_OK (0) on success, a negative status otherwise; `svhip_last_error()` then describes the
  * failure (thread-local string). No entry point aborts the process.
@@ -119,6 +120,23 @@ int svhip_ease_select(const void* logits, int dtype, int64_t classes, int64_t st
                       const int64_t* pos, const double* frac, const int64_t* n_total, const int64_t* committed,
                       uint8_t* chosen, uint8_t* bad, float* scores_out, void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/*
+ * svhip_ease_select with the scratch taken from a fixed device array of the library (48 MiB per GPU, held from
+ * the library's load until the process ends) instead of a workspace argument: the call allocates nothing, for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Rejects geometries whose svhip_ease_select_workspace_bytes exceed 48 MiB (up to 92 windows of
+ * 65 536 voxels at 4^3 blocks fit) with SVHIP_EINVAL, without a launch. Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (two streams, two threads) race and must be serialised by the caller. The first call on a device
+ * looks up the array's address on that device (outside graph capture, so make it once before capturing).
+ * No counterpart in the reference: an addition of this library for callers that cannot allocate.
+ */
+int svhip_ease_select_noalloc(const void* logits, int dtype, int64_t classes, int64_t stride_b, int64_t stride_c,
+                              int64_t stride_n, const int64_t* tokens, int64_t mask_token, const uint8_t* last,
+                              int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_t block, const int64_t* k,
+                              const int64_t* pos, const double* frac, const int64_t* n_total,
+                              const int64_t* committed, uint8_t* chosen, uint8_t* bad, float* scores_out,
+                              void* stream);
 
 /*
  * svhip_ease_select over logits in the class head's patch order (row map as in svhip_entropy_patches); tokens,

@@ -38,6 +38,9 @@ SIGNATURES = {
     'svhip_ease_select': (ctypes.c_int, [_c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
                                          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                          _c_p, _c_p, _c_p, _c_sz, _c_p]),
+    'svhip_ease_select_noalloc': (ctypes.c_int, [_c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
+                                                 _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
+                                                 _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     'svhip_ease_select_patches': (ctypes.c_int, [_c_p, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
                                                  _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
                                                  _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p]),

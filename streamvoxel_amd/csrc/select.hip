@@ -7,6 +7,9 @@
 //  * selections of "the `count` smallest (key, index)" use one workgroup per problem: an MSB-first 8-bit radix
 //    select on the key finds the threshold key T and how many of the T-ties to keep, then ties are taken in index
 //    order with a ballot prefix count over index-ordered rounds.
+#include <atomic>
+#include <mutex>
+
 #include "common.hpp"
 #include "stats.hpp"
 
@@ -1017,6 +1020,74 @@ extern "C" int svhip_ease_select_patches(const void* logits, int dtype, int64_t 
   return ease_select_impl(logits, dtype, classes, stride_b, 1, stride_n, tokens, mask_token, last, batch, Y, Z, X,
                           block, k, pos, frac, n_total, committed, chosen, bad, scores_out, workspace,
                           workspace_bytes, stream, rows, name);
+}
+
+// ------------------------------------------------------------------ fixed-scratch selection (allocates nothing)
+
+namespace svhip {
+
+// The selection's scratch (targets, quotas, keys, boundary candidates) for callers that cannot allocate: one
+// array per GPU, held until the process ends. 48 MiB covers 92 windows of 65 536 voxels at 4^3 blocks
+// (544 768 bytes per window).
+constexpr size_t kScratchBytes = size_t(48) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch`, looked up once per device with that device current. The array's
+// name is only a host-side handle; kernels get this address.
+static int scratch_address(void** out, const char* name) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("%s: hipGetDevice failed: %s", name, hipGetErrorString(e));
+    return SVHIP_ELAUNCH;
+  }
+  SVHIP_REQUIRE(dev >= 0 && dev < kMaxDevices, "%s: device %d beyond the %d supported", name, dev, kMaxDevices);
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr) {
+        set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev, hipGetErrorString(e));
+        return SVHIP_ELAUNCH;
+      }
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return SVHIP_OK;
+}
+
+}  // namespace svhip
+
+extern "C" int svhip_ease_select_noalloc(const void* logits, int dtype, int64_t classes, int64_t stride_b,
+                                         int64_t stride_c, int64_t stride_n, const int64_t* tokens,
+                                         int64_t mask_token, const uint8_t* last, int64_t batch, int64_t Y, int64_t Z,
+                                         int64_t X, int64_t block, const int64_t* k, const int64_t* pos,
+                                         const double* frac, const int64_t* n_total, const int64_t* committed,
+                                         uint8_t* chosen, uint8_t* bad, float* scores_out, void* stream) {
+  const char* name = "svhip_ease_select_noalloc";
+  clear_error();
+  Geometry g;
+  int rc = check_geometry(batch, Y, Z, X, block, name, &g);
+  if (rc != SVHIP_OK) return rc;
+  const size_t need = quota_ws_bytes(batch, g);
+  SVHIP_REQUIRE(need <= kScratchBytes, "%s: %lld windows of %lld voxels need %zu bytes of scratch, the fixed array "
+                "holds %zu", name, (long long)batch, (long long)g.n, need, kScratchBytes);
+  SVHIP_REQUIRE(logits && tokens && last && k && pos && frac && n_total && committed && chosen && bad,
+                "%s: null pointer", name);
+  void* ws = nullptr;
+  rc = scratch_address(&ws, name);
+  if (rc != SVHIP_OK) return rc;
+  // Every scratch word the kernels read is written earlier in the same call, so nothing needs clearing.
+  return ease_select_impl(logits, dtype, classes, stride_b, stride_c, stride_n, tokens, mask_token, last, batch, Y, Z,
+                          X, block, k, pos, frac, n_total, committed, chosen, bad, scores_out, ws, kScratchBytes,
+                          stream, kYzxRows, name);
 }
 
 extern "C" int svhip_top_mask(const float* scores, const uint8_t* eligible, int64_t batch, int64_t n,

@@ -58,6 +58,19 @@ def test_workspace_queries_and_argument_errors(lib):
     assert rc == -1
 
 
+def test_noalloc_select_rejects_on_the_host(lib):
+    # 200 windows of 65 536 voxels need about 104 MiB of scratch, more than the library's fixed 48 MiB array
+    assert lib.svhip_ease_select_workspace_bytes(200, 256, 16, 16, 4) > (48 << 20)
+    none = [None] * 9
+    rc = lib.svhip_ease_select_noalloc(None, 0, 256, 0, 1, 256, None, 256, None, 200, 256, 16, 16, 4, *none)
+    assert rc == -1 and b'scratch' in lib.svhip_last_error(), lib.svhip_last_error()
+    # a geometry that fits, with null pointers: refused before the device is touched
+    rc = lib.svhip_ease_select_noalloc(None, 0, 256, 0, 1, 256, None, 256, None, 8, 256, 16, 16, 4, *none)
+    assert rc == -1 and b'null pointer' in lib.svhip_last_error(), lib.svhip_last_error()
+    rc = lib.svhip_ease_select_noalloc(None, 0, 256, 0, 1, 256, None, 256, None, 8, 256, 16, 16, 3, *none)
+    assert rc == -1 and b'unsupported' in lib.svhip_last_error()
+
+
 def test_product_refuses_host_tensors():
     import torch
     from streamvoxel_amd.sampling.entropy import entropy_scores
