@@ -163,28 +163,21 @@ class Workload:
             self.sel.tokens.masked_fill_(self.sel.last, 0)     # finish: deferred voxels become air
 
     def capture(self):
-        import torch
-        stream = torch.cuda.Stream(self.dev)
-        stream.wait_stream(torch.cuda.current_stream(self.dev))
-        with torch.cuda.stream(stream):
-            self.marking_step()
-            for s in range(STEPS_PER_WINDOW - 1):
-                self.solid_step(s)
-        torch.cuda.current_stream(self.dev).wait_stream(stream)
-        torch.cuda.synchronize()
-        graphs = []
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            self.marking_step()
-        graphs.append(g)
-        for s in range(STEPS_PER_WINDOW - 1):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                self.solid_step(s)
-            graphs.append(g)
-        torch.cuda.synchronize()
+        """One HIP graph per step of the window (the marking step, then the 25 solid steps), captured by the
+        engine's `StepGraphs`; returns the callables that replay them."""
+        from streamvoxel_amd.stream.engine import StepGraphs
+
+        def body(step):
+            if step == 0:
+                self.marking_step()
+            else:
+                self.solid_step(step - 1)
+
+        graphs = StepGraphs(self.dev, body, range(STEPS_PER_WINDOW), warmup=1)
+        if not graphs.ok:
+            raise RuntimeError('the step graphs could not be captured')
         self.bad_seen.zero_()
-        return graphs
+        return [graphs.graphs[step].replay for step in range(STEPS_PER_WINDOW)]
 
 
 def time_events(fn, reps, warm=3):
@@ -303,65 +296,72 @@ def cpu_baseline(w, budget_s):
                 cpu_count=os.cpu_count(), wall_s=time.perf_counter() - began)
 
 
-def step_forward_component(dev, lengths_seed=7):
-    """Seconds per call of one whole generation step's forward at the shipped model's shape (random weights, the
-    trained ones are not published): gather patchify, 25 x 768 backbone blocks, 13 x 384 control blocks each with
-    cross attention over its cached context (L_b = 4384 + 1024 k_b keys of 12 672) and zero projection, final
-    AdaLN norm, class head to 304 classes in patch order; 8 windows, one graph."""
+def shipped_engine_component(dev, lengths_seed=7):
+    """The shipped model's shape through the slot engine (`SlotEngine`, random weights in the reference's layout:
+    the trained ones are not published): 8 slots of 256 x 16 x 16 voxels, 304 classes, 25 x 768 backbone blocks,
+    13 x 384 control blocks with cross attention over a cache of 4096 prefix + 288 + 1024 k_b local keys
+    (k_b ~ U{0..8}), synthetic conditions. Times (a) the captured step forward, `replay(timesteps, 8)`, with HIP
+    events around back-to-back replays, and (b) one whole window of the worker's loop (stream/worker.py:378-397):
+    26 forwards of `replay` + `consume_batch` over `SelectGraphs` of 8 slots (marking, 25 solid steps; the
+    counter-based sampler inside the captured selection), wall time per forward including the host's one wait per
+    forward and its bookkeeping."""
     import torch
     from streamvoxel_amd import synth
-    from streamvoxel_amd.stream.forward import StepForward
-    from streamvoxel_amd.stream.step import CachedContext
+    from streamvoxel_amd.stream.engine import SlotEngine
+    from streamvoxel_amd.stream.slot import LowEntropyLastSlot, SelectGraphs, consume_batch
     model = synth.StepModel(seed=1)
     for p in model.parameters():
         p.data = p.data.to(torch.bfloat16)
     model = model.to(dev)
+    spec = synth.WindowSpec()
+    engine = SlotEngine(model, spec, dev, SLOTS, l1_cap=8, l2_cap=256)
     g = torch.Generator().manual_seed(lengths_seed)
-    lengths = (256 * 16 + 288 + 1024 * torch.randint(0, 9, (SLOTS,), generator=g)).tolist()
-    ctx = CachedContext(len(model.cross), SLOTS, 8, 48, 12672, dev)
-    for j in range(ctx.layers):
-        ctx.k[j].normal_().mul_(0.3)
-        ctx.vt[j].normal_()
-    for b, L in enumerate(lengths):
-        ctx.set_length(b, L)
-    step = StepForward(model, ctx)
-    tokens = torch.randint(0, 305, (SLOTS, *SHAPE), device=dev, generator=torch.Generator(dev).manual_seed(3))
-    timestep = torch.full((SLOTS,), 0.5, device=dev)
-    origin = torch.tensor([[16.0 * i, -64.0, 0.0] for i in range(SLOTS)], device=dev)
-    group = torch.tensor([0.0, -64.0, 0.0], device=dev)
-    t = time_graph(lambda: step(tokens, timestep, origin, group), 1, replays=5)
-    # The whole solid step in one graph: the forward from the windows' token state, the EASE selection over the
-    # class head's bf16 rows in place (304 classes, 2 621 voxels per window of a fresh window) and the
-    # counter-based sampling tail drawing the chosen voxels into the same token state. The token state is reset to
-    # the mask token at the start of the step so that every replay does the same work.
-    from streamvoxel_amd.stream.sampler import sample_chosen
-    from streamvoxel_amd.stream.step import EaseSelect
-    classes = 304
-    sel = EaseSelect(SLOTS, SHAPE, classes, BLOCK, dev)
-    k = VOXELS // (STEPS_PER_WINDOW - 1)
-    for b in range(SLOTS):
-        sel.bind_window(b, torch.randperm(VOXELS // BLOCK ** 3, generator=torch.Generator().manual_seed(b)))
-        sel.set_step(b, k, 0, k / VOXELS)
-    state = sel.tokens.view(SLOTS, *SHAPE)
-    seeds = torch.arange(SLOTS, dtype=torch.int64, device=dev)
-    steps = torch.zeros(SLOTS, dtype=torch.int64, device=dev)
-    drawn = torch.empty(SLOTS, *SHAPE, dtype=torch.int16, device=dev)
-    err = torch.zeros(1, dtype=torch.int32, device=dev)
-
-    def whole_step():
-        state.fill_(classes)
-        logits = step(state, timestep, origin, group)
-        sel.run(logits)
-        sample_chosen(logits, sel.chosen.view(SLOTS, *SHAPE), seeds, steps, drawn, err, state)
-
-    t_whole = time_graph(whole_step, 1, replays=5)
+    neighbours = torch.randint(0, 9, (SLOTS,), generator=g).tolist()
+    for b, k in enumerate(neighbours):
+        engine.load_slot(b, synth.condition(model, 256 * 16, 288 + 1024 * k, seed=100 + b, device=dev, scale=0.3))
+    engine.wait_loads()
+    lengths = engine.packed.lengths.tolist()
+    engine.tokens.copy_(torch.randint(0, spec.num_classes + 1, engine.tokens.shape, device=dev,
+                                      generator=torch.Generator(dev).manual_seed(3)))
+    engine.replay(0.5, SLOTS)
     torch.cuda.synchronize()
-    filled = (state != classes).view(SLOTS, -1).sum(1).tolist()
-    if int(err) != 0 or bool(sel.bad.any()) or filled != [k] * SLOTS:
-        raise RuntimeError(f'whole-step check failed: err={int(err)} bad={sel.bad.tolist()} filled={filled}')
-    del step, ctx, model, sel
+    reps = 5
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        engine.replay(0.5, SLOTS)
+    end.record()
+    end.synchronize()
+    t_forward = start.elapsed_time(end) / reps / 1e3
+    slots = [LowEntropyLastSlot(engine.shape, spec.num_classes, (0,), air_token=0, last_eps=LAST_EPS, block_size=BLOCK,
+                                device=dev, sampler='philox') for _ in range(SLOTS)]
+    select = SelectGraphs(engine, slots)
+
+    def window(seed0):
+        for i, slot in enumerate(slots):
+            slot.arm(seed0 + i, STEPS_PER_WINDOW - 1, (i, 0))
+        engine.clear_tokens()
+        forwards = 0
+        while any(not slot.idle for slot in slots):
+            count = 1 + max(i for i, slot in enumerate(slots) if not slot.idle)
+            times = [slot.time() if i < count else 1.0 for i, slot in enumerate(slots)]
+            consume_batch(slots, engine.replay(times, count), engine.tokens, count, select)
+            forwards += 1
+        return forwards
+
+    window(0)                                   # warm: first replays of every select graph
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    forwards = window(1000)
+    torch.cuda.synchronize()
+    t_window = (time.perf_counter() - t0) / forwards
+    if bool((engine.tokens == spec.num_classes).any()):
+        raise RuntimeError('a window finished with uncommitted voxels')
+    del engine, select, slots, model
     torch.cuda.empty_cache()
-    return t, lengths, t_whole
+    return dict(forward_ms=t_forward * 1e3, kv_lengths=lengths, window_forwards=forwards,
+                window_ms_per_forward=t_window * 1e3,
+                window_voxels_per_s=SLOTS * VOXELS / (forwards * t_window))
 
 
 def sampling_tail_component(w, dev, s=12):
@@ -464,9 +464,9 @@ def main():
     streamvoxel_amd.load()
     dev = torch.device('cuda:0')
     if args.forward_only:
-        t_forward, lengths, t_whole = step_forward_component(dev)
-        print(json.dumps(dict(component='shipped_step_forward', ms=t_forward * 1e3, slots=SLOTS, kv_lengths=lengths,
-                              whole_step_ms=t_whole * 1e3, reference_fast_forward_rtx4090d_ms=44.0)), flush=True)
+        eng = shipped_engine_component(dev)
+        print(json.dumps(dict(component='shipped_engine', slots=SLOTS, reference_fast_forward_rtx4090d_ms=44.0, **eng)),
+              flush=True)
         return
     if args.kernel:
         print(json.dumps(kernel_only(dev, args)), flush=True)
@@ -478,13 +478,13 @@ def main():
     log('graphs captured')
     n_graphs = len(graphs)
     for i in range(args.warmup):
-        graphs[i % n_graphs].replay()
+        graphs[i % n_graphs]()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
     for i in range(args.steps):
-        graphs[i % n_graphs].replay()
+        graphs[i % n_graphs]()
     end.record()
     torch.cuda.synchronize()
     ms_per_step = start.elapsed_time(end) / args.steps
@@ -536,11 +536,11 @@ def main():
     log(f'sampling tail (8 windows, solid step {tail["solid_step"]}): multinomial eager '
         f'{tail["multinomial_eager_us"]:.1f} us, counter-based kernel {tail["philox_kernel_us"]:.1f} us '
         f'({tail["philox_with_d2h_us"]:.1f} us with its D2H copy)')
-    t_forward = forward_lengths = t_whole = None
+    eng = None
     if not args.no_forward:
-        t_forward, forward_lengths, t_whole = step_forward_component(dev)
-        log(f'whole step forward (shipped shape, 8 windows) {t_forward * 1e3:.2f} ms; forward + select + sampling '
-            f'in one graph {t_whole * 1e3:.2f} ms')
+        eng = shipped_engine_component(dev)
+        log(f'shipped model through the slot engine (8 slots): step forward {eng["forward_ms"]:.2f} ms; worker loop '
+            f'{eng["window_ms_per_forward"]:.2f} ms per forward = {eng["window_voxels_per_s"]:.0f} voxels/s')
     xattn_tflops = w.flops_per_layer / t_layer / 1e12
     select_gbs = w.select_bytes / t_select / 1e9
     entropy_bytes = SLOTS * VOXELS * (CLASSES * 4 + 4)
@@ -582,15 +582,9 @@ def main():
                         select_from_patch_order_ms_per_step=t_select_patches * 1e3,
                         class_major_permute_ms_avoided=t_permute * 1e3,
                         selection_bad_flag_seen=bad,
-                        shipped_step_forward_ms=None if t_forward is None else t_forward * 1e3,
-                        shipped_step_forward_kv_lengths=forward_lengths,
-                        shipped_step_forward_plus_select_ms=(None if t_forward is None else
-                                                             (t_forward + t_select304) * 1e3),
-                        shipped_model_voxels_per_s=(None if t_forward is None else
-                                                    SLOTS * VOXELS / (STEPS_PER_WINDOW * (t_forward + t_select304))),
-                        shipped_whole_step_one_graph_ms=None if t_whole is None else t_whole * 1e3,
-                        shipped_whole_step_voxels_per_s=(None if t_whole is None else
-                                                         SLOTS * VOXELS / (STEPS_PER_WINDOW * t_whole)),
+                        shipped_engine=eng,
+                        shipped_step_forward_plus_select_ms=(None if eng is None else
+                                                             eng['forward_ms'] + t_select304 * 1e3),
                         reference_fast_forward_rtx4090d_ms=44.0,
                         sampling_tail=tail),
         measured_peaks=peaks,
