@@ -97,8 +97,10 @@ int svhip_top_mask(const float* scores, const uint8_t* eligible, int64_t batch, 
  * (more than k) or top-up (fewer) by score. bad[b] is set to 1 when the result does not hold exactly k voxels.
  *   score fp32 [B,N]; mask bytes [B,N]; k, committed int64 [B]; frac fp64 [B]; pos, n_total int64 [B, nb];
  *   chosen bytes [B,N] (written); bad bytes [B] (written), nb = N / b^3.
+ * committed may be NULL: it is then derived per window on the device as sum(n_total[b]) - (non-zero mask bytes of
+ * window b), the already-committed non-deferred voxels.
  * Replaces: quota_select_nosync (streamvoxel/stream/fast_ops.py:442-473) and, with committed = the number of
- * committed non-deferred voxels, block_quota_select (streamvoxel/sampling/block_quota.py:20-38).
+ * committed non-deferred voxels (or NULL), block_quota_select (streamvoxel/sampling/block_quota.py:20-38).
  */
 size_t svhip_quota_select_workspace_bytes(int64_t batch, int64_t Y, int64_t Z, int64_t X, int64_t block);
 int svhip_quota_select(const float* score, const uint8_t* mask, int64_t batch, int64_t Y, int64_t Z, int64_t X,
@@ -172,6 +174,21 @@ int svhip_xattn_fwd(const void* q, const void* k, const void* v, void* o, int kv
                     int64_t Q, int64_t D, int64_t kv_cap, int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b,
                     int64_t sk_h, int64_t sk_k, int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d,
                     int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream);
+
+/*
+ * svhip_xattn_fwd with a boolean key mask: key j of window b is attended iff kv_mask[b * sm_b + j] != 0 (bytes,
+ * at least kv_cap per window; with cu_seqlens, j counts from the window's first row), within the window length
+ * (kv_len[b], or the cu_seqlens length, or kv_cap when both are NULL; clamped to kv_cap, the width of the mask
+ * rows). Any pattern of attended
+ * keys; a query with no attended key gets zeros. bf16 K/V only.
+ * Replaces: the boolean attn_mask of the masked SDPA in cross_sdpa (streamvoxel/stream/fast_ops.py:111-115) and
+ * SlotCrossAttention.forward (streamvoxel/stream/engine.py:28-47), whatever the mask's shape.
+ */
+int svhip_xattn_fwd_masked(const void* q, const void* k, const void* v, void* o, const uint8_t* kv_mask, int64_t sm_b,
+                           const int32_t* kv_len, const int32_t* cu_seqlens, int64_t B, int64_t H, int64_t Q,
+                           int64_t D, int64_t kv_cap, int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b,
+                           int64_t sk_h, int64_t sk_k, int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d,
+                           int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream);
 
 /*
  * AxialRoPE of bf16 activations: x [B,H,N,D] (element (b,h,n,d) at b*sx_b + h*sx_h + n*sx_n + d) -> out (same

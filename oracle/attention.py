@@ -60,6 +60,13 @@ def masked_sdpa(q, k, v, lengths, scale=None):
                                                             scale=scale)
 
 
+def masked_sdpa_mask(q, k, v, valid, scale=None):
+    """The reference's masked SDPA with any boolean key mask `valid` [B, K] (stream/fast_ops.py:111-115,
+    stream/engine.py:46), on the CPU in the inputs' dtype."""
+    return torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=valid[:, None, None, :], dropout_p=0.,
+                                                            scale=scale)
+
+
 def cross_attention_bruteforce(q, k, v, lengths, scale=None):
     """Scalar loops (tiny inputs only): the independent check of `cross_attention`."""
     B, H, Q, D = q.shape

@@ -751,10 +751,11 @@ static int64_t boundary_entries(int64_t batch, const Geometry& g) {
 
 static size_t quota_ws_bytes(int64_t batch, const Geometry& g) {
   // keys u64 [B,nb] + target i64 [B,nb] + bq i32 [B,nb] + ckey u32 [B,N] + bnd u64 [B,nb,2 kBoundary] (4^3
-  // blocks), each 256-byte aligned
+  // blocks) + derived committed counts i64 [B], each 256-byte aligned
   auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
   return al(sizeof(uint64_t) * batch * g.nb) + al(sizeof(int64_t) * batch * g.nb) + al(sizeof(int32_t) * batch * g.nb) +
-         al(sizeof(uint32_t) * batch * g.n) + al(sizeof(uint64_t) * boundary_entries(batch, g));
+         al(sizeof(uint32_t) * batch * g.n) + al(sizeof(uint64_t) * boundary_entries(batch, g)) +
+         al(sizeof(int64_t) * batch);
 }
 
 struct QuotaWs {
@@ -763,6 +764,7 @@ struct QuotaWs {
   int32_t* bq;
   uint32_t* ckey;
   uint64_t* bnd;  // null unless the blocks are 4^3
+  int64_t* committed;  // per-window committed counts derived on the device (svhip_quota_select without them)
 };
 
 static QuotaWs carve(void* ws, int64_t batch, const Geometry& g) {
@@ -778,7 +780,39 @@ static QuotaWs carve(void* ws, int64_t batch, const Geometry& g) {
   w.ckey = reinterpret_cast<uint32_t*>(p);
   p += al(sizeof(uint32_t) * batch * g.n);
   w.bnd = boundary_entries(batch, g) ? reinterpret_cast<uint64_t*>(p) : nullptr;
+  p += al(sizeof(uint64_t) * boundary_entries(batch, g));
+  w.committed = reinterpret_cast<int64_t*>(p);
   return w;
+}
+
+// committed[b] = sum of n_total[b, :] - number of non-zero mask bytes of window b (the non-deferred voxels that are
+// no longer selectable): block_quota_select's `already.sum()`. One workgroup per window.
+__global__ __launch_bounds__(256) void committed_kernel(const uint8_t* __restrict__ mask,
+                                                        const int64_t* __restrict__ n_total, int64_t nb, int64_t n,
+                                                        int64_t* __restrict__ committed) {
+  __shared__ int64_t red[4];
+  const int64_t b = blockIdx.x;
+  const uint8_t* m = mask + b * n;
+  int64_t local = 0;
+  for (int64_t j = threadIdx.x; j < nb; j += 256) local += n_total[b * nb + j];
+  // n is a multiple of 64: 16-byte loads while 16 bytes remain, single bytes for the rest (unaligned rows).
+  const bool vec = (reinterpret_cast<uintptr_t>(m) & 15) == 0;
+  const int64_t nv = vec ? n / 16 : 0;
+  for (int64_t i = threadIdx.x; i < nv; i += 256) {
+    const uint4 v = reinterpret_cast<const uint4*>(m)[i];
+    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t x = w4[q];
+      local -= ((x & 0xffu) != 0) + ((x & 0xff00u) != 0) + ((x & 0xff0000u) != 0) + ((x & 0xff000000u) != 0);
+    }
+  }
+  for (int64_t i = 16 * nv + threadIdx.x; i < n; i += 256) local -= m[i] != 0;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) local += __shfl_xor(local, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = local;
+  __syncthreads();
+  if (threadIdx.x == 0) committed[b] = red[0] + red[1] + red[2] + red[3];
 }
 
 // Apportionment alone (the fused entropy pass runs it on the side when the window has at most kWaveBlocks
@@ -972,7 +1006,7 @@ extern "C" int svhip_quota_select(const float* score, const uint8_t* mask, int64
   Geometry g;
   int rc = check_geometry(batch, Y, Z, X, block, name, &g);
   if (rc != SVHIP_OK) return rc;
-  SVHIP_REQUIRE(score && mask && k && pos && frac && n_total && committed && chosen && bad, "%s: null pointer", name);
+  SVHIP_REQUIRE(score && mask && k && pos && frac && n_total && chosen && bad, "%s: null pointer", name);
   const size_t need = quota_ws_bytes(batch, g);
   if (workspace == nullptr || workspace_bytes < need) {
     set_error("%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
@@ -980,6 +1014,11 @@ extern "C" int svhip_quota_select(const float* score, const uint8_t* mask, int64
   }
   const QuotaWs w = carve(workspace, batch, g);
   hipStream_t s = as_stream(stream);
+  if (committed == nullptr) {
+    committed_kernel<<<static_cast<unsigned>(batch), 256, 0, s>>>(mask, n_total, g.nb, g.n, w.committed);
+    SVHIP_LAUNCHED(name);
+    committed = w.committed;
+  }
   rc = launch_apportion(batch, g, k, pos, frac, n_total, committed, w, s, name);
   if (rc != SVHIP_OK) return rc;
   return launch_inblock_fix(KeyFromScore<MaskBytes>{score, MaskBytes{mask, g.n}, w.ckey}, batch, g, k, n_total,

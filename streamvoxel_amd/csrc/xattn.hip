@@ -87,6 +87,8 @@ struct XattnParams {
   const int32_t* cu_seqlens;
   const float* k_scale;
   const float* v_scale;
+  const uint8_t* kv_mask;  // optional key mask: key j of window b is attended iff kv_mask[b * sm_b + j] != 0
+  int64_t sm_b;
   int64_t B, H, Q, D, kv_cap;
   int64_t sq_b, sq_h, sq_q;
   int64_t sk_b, sk_h, sk_k;
@@ -288,10 +290,13 @@ __device__ __forceinline__ int window_length(const XattnParams& p, int64_t b) {
   int64_t L;
   if (p.cu_seqlens) {
     L = static_cast<int64_t>(p.cu_seqlens[b + 1]) - p.cu_seqlens[b];
-  } else {
+  } else if (p.kv_len) {
     L = p.kv_len[b];
     if (L > p.kv_cap) L = p.kv_cap;
+  } else {
+    L = p.kv_cap;  // key-mask form without lengths: every key up to the capacity, the mask decides
   }
+  if (p.kv_mask && L > p.kv_cap) L = p.kv_cap;  // the mask rows hold kv_cap keys
   return L < 0 ? 0 : static_cast<int>(L);
 }
 
@@ -379,9 +384,11 @@ enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2 };
 // ONES: head_dim below 32 DT, the row sum comes from the matrix cores (V^T row D of ones). The e4m3 V^T kernel up
 // to head_dim 64 is held to 168 VGPRs (three waves per SIMD; it needs 170 unbounded, without spilling at 168); the
 // bf16 direct-staged ones fit by themselves.
-template <bool FP8, bool VT, int STAGING, int DT, bool ONES>
+// KMASK: a key mask (p.kv_mask) on top of the window length; every block then masks its keys.
+template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false>
 __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
   constexpr bool DIRECT = STAGING != kRegister;
+  static_assert(!KMASK || !DIRECT, "the key-mask path stages through registers");
   static_assert(!ONES || STAGING != kDirectFull, "a full-width head has no padding row");
   constexpr int kSubTiles = Width<DT>::kSubTiles;
   // Four distinct LDS objects (not one indexed array): the compiler can then tell the direct loads into one
@@ -547,6 +554,18 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
   };
 
 
+  // The key mask of the block starting at kv0 as 64 bits (bit i: key kv0 + i is attended), wave-uniform.
+  const uint8_t* mrow = KMASK ? p.kv_mask + b * p.sm_b : nullptr;
+  auto block_bits = [&](int kv0) __attribute__((always_inline)) -> uint64_t {
+    if constexpr (KMASK) {
+      const int j = kv0 + lane;
+      const bool on = j < L && mrow[j] != 0;
+      return __builtin_amdgcn_ballot_w64(on);
+    } else {
+      return ~0ull;
+    }
+  };
+
   // One key block from (Ks, Vt), as two 32-key halves that each run the whole online-softmax step (scores,
   // running max, exponentials, second product): a half's scores take 16 registers, which keeps four waves per
   // SIMD resident. MASKED: the partial block (keys >= L masked out).
@@ -554,6 +573,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
     constexpr bool MASKED = decltype(masked)::value;
     const char* kp = reinterpret_cast<const char*>(Ks);
     const char* vp = reinterpret_cast<const char*>(Vt);
+    const uint64_t bits = block_bits(kv0);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       // S^T of keys 32 t .. 32 t + 31 (LDS rows 32 t + col); k-steps past head_dim (zero in Q) are skipped.
@@ -566,12 +586,15 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
           s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], k == 0 ? negm : s, 0, 0, 0);
         }
       }
-      if constexpr (MASKED) {
-        // Entry i is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8).
+      if constexpr (MASKED || KMASK) {
+        // Entry i is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8); with a key mask, bit i of `mine`.
+        const uint32_t hb = static_cast<uint32_t>(bits >> (32 * t));
+        const uint32_t mine = ((hb >> (8 * hh)) & 0xffu) | (((hb >> (16 + 8 * hh)) & 0xffu) << 8);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int kin = (i < 8) ? (8 * hh + i) : (16 + 8 * hh + (i - 8));
-          if (kv0 + 32 * t + kin >= L) s[i] = -INFINITY;
+          const int kin = 32 * t + ((i < 8) ? (8 * hh + i) : (16 + 8 * hh + (i - 8)));
+          if (MASKED && kv0 + kin >= L) s[i] = -INFINITY;
+          if (KMASK && !((mine >> i) & 1u)) s[i] = -INFINITY;
         }
       }
       // P^T = exp2(S^T - m) against the running max m as it stands (the accumulators already hold S - mc, mc = m
@@ -610,7 +633,10 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
         const float mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
         const float cand = mr + mc;
-        const float mn = cand > m ? cand : m;
+        float mn = cand > m ? cand : m;
+        // Only with a key mask can a query have seen no attended key yet (every score -inf): its running max is
+        // then set to 0, with O and l still 0, so that later scores are taken against a finite bias.
+        if (KMASK) mn = mn == -INFINITY ? 0.f : mn;
         const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first half
         m = mn;
         l *= alpha;
@@ -727,7 +753,8 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(lsum), __float_as_int(lsum), false, false);
     lsum = __int_as_float(sw[0]) + __int_as_float(sw[1]);
   }
-  const float inv = vscale / lsum;
+  // A query with no attended key (only possible with a key mask) has l = 0 and O = 0: it gets zeros.
+  const float inv = (KMASK && !(lsum > 0.f)) ? 0.f : vscale / lsum;
   if (q_ok) {
     // O^T entry i of tile t: d = 32 t + 8 (i / 4) + 4 hh + i % 4 ; four consecutive d per group.
 #pragma unroll
@@ -756,6 +783,14 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
 // directly to LDS (head_dim 32 DT without exec masking).
 template <int DT, bool ONES>
 void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool vt, bool direct) {
+  if (p.kv_mask) {  // bf16 only (checked by the entry point), through registers
+    if (vt) {
+      xattn_fwd_kernel<false, true, kRegister, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
+    } else {
+      xattn_fwd_kernel<false, false, kRegister, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
+    }
+    return;
+  }
   if (fp8) {
     if (vt) {
       xattn_fwd_kernel<true, true, kRegister, DT, ONES><<<g, kThreads, 0, s>>>(p);
@@ -784,20 +819,13 @@ void launch(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool vt, 
   }
 }
 
-}  // namespace svhip
-
-using namespace svhip;
-
-extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void* o, int kv_dtype,
-                               const int32_t* kv_len, const int32_t* cu_seqlens, const float* k_scale,
-                               const float* v_scale, int64_t B, int64_t H, int64_t Q, int64_t D, int64_t kv_cap,
-                               int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b, int64_t sk_h, int64_t sk_k,
-                               int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d, int64_t so_b, int64_t so_h,
-                               int64_t so_q, float scale, void* stream) {
-  const char* name = "svhip_xattn_fwd";
-  clear_error();
+static int xattn_impl(const void* q, const void* k, const void* v, void* o, int kv_dtype, const int32_t* kv_len,
+                      const int32_t* cu_seqlens, const float* k_scale, const float* v_scale, const uint8_t* kv_mask,
+                      int64_t sm_b, int64_t B, int64_t H, int64_t Q, int64_t D, int64_t kv_cap, int64_t sq_b,
+                      int64_t sq_h, int64_t sq_q, int64_t sk_b, int64_t sk_h, int64_t sk_k, int64_t sv_b,
+                      int64_t sv_h, int64_t sv_k, int64_t sv_d, int64_t so_b, int64_t so_h, int64_t so_q,
+                      float scale, void* stream, const char* name) {
   SVHIP_REQUIRE(q && k && v && o, "%s: null pointer", name);
-  SVHIP_REQUIRE(kv_len || cu_seqlens, "%s: need kv_len or cu_seqlens", name);
   SVHIP_REQUIRE(B >= 0 && H >= 1 && Q >= 0, "%s: bad sizes", name);
   SVHIP_REQUIRE(D >= 8 && D <= kMaxD && D % 8 == 0, "%s: head_dim %lld unsupported (multiple of 8, <= %d)", name,
                 (long long)D, kMaxD);
@@ -805,6 +833,7 @@ extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void
   SVHIP_REQUIRE(kv_dtype == SVHIP_BF16 || kv_dtype == SVHIP_FP8_E4M3, "%s: kv dtype %d unsupported", name, kv_dtype);
   const bool fp8 = kv_dtype == SVHIP_FP8_E4M3;
   SVHIP_REQUIRE(!fp8 || (k_scale && v_scale), "%s: fp8 K/V need k_scale and v_scale", name);
+  SVHIP_REQUIRE(!kv_mask || !fp8, "%s: the key mask takes bf16 K/V", name);
   SVHIP_REQUIRE(sv_k == 1 || sv_d == 1, "%s: V needs a unit stride along keys or head_dim", name);
   const bool vt = sv_k == 1 && sv_d != 1;
   const size_t eb = fp8 ? 1 : 2;
@@ -835,6 +864,8 @@ extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void
   p.cu_seqlens = cu_seqlens;
   p.k_scale = k_scale;
   p.v_scale = v_scale;
+  p.kv_mask = kv_mask;
+  p.sm_b = sm_b;
   p.B = B;
   p.H = H;
   p.Q = Q;
@@ -873,4 +904,35 @@ extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void
   }
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;
+}
+
+}  // namespace svhip
+
+using namespace svhip;
+
+extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void* o, int kv_dtype,
+                               const int32_t* kv_len, const int32_t* cu_seqlens, const float* k_scale,
+                               const float* v_scale, int64_t B, int64_t H, int64_t Q, int64_t D, int64_t kv_cap,
+                               int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b, int64_t sk_h, int64_t sk_k,
+                               int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d, int64_t so_b, int64_t so_h,
+                               int64_t so_q, float scale, void* stream) {
+  const char* name = "svhip_xattn_fwd";
+  clear_error();
+  SVHIP_REQUIRE(kv_len || cu_seqlens, "%s: need kv_len or cu_seqlens", name);
+  return xattn_impl(q, k, v, o, kv_dtype, kv_len, cu_seqlens, k_scale, v_scale, nullptr, 0, B, H, Q, D, kv_cap, sq_b,
+                    sq_h, sq_q, sk_b, sk_h, sk_k, sv_b, sv_h, sv_k, sv_d, so_b, so_h, so_q, scale, stream, name);
+}
+
+extern "C" int svhip_xattn_fwd_masked(const void* q, const void* k, const void* v, void* o, const uint8_t* kv_mask,
+                                      int64_t sm_b, const int32_t* kv_len, const int32_t* cu_seqlens, int64_t B,
+                                      int64_t H, int64_t Q, int64_t D, int64_t kv_cap, int64_t sq_b, int64_t sq_h,
+                                      int64_t sq_q, int64_t sk_b, int64_t sk_h, int64_t sk_k, int64_t sv_b,
+                                      int64_t sv_h, int64_t sv_k, int64_t sv_d, int64_t so_b, int64_t so_h,
+                                      int64_t so_q, float scale, void* stream) {
+  const char* name = "svhip_xattn_fwd_masked";
+  clear_error();
+  SVHIP_REQUIRE(kv_mask, "%s: null key mask", name);
+  SVHIP_REQUIRE(!(kv_len && cu_seqlens), "%s: kv_len and cu_seqlens are exclusive", name);
+  return xattn_impl(q, k, v, o, SVHIP_BF16, kv_len, cu_seqlens, nullptr, nullptr, kv_mask, sm_b, B, H, Q, D, kv_cap,
+                    sq_b, sq_h, sq_q, sk_b, sk_h, sk_k, sv_b, sv_h, sv_k, sv_d, so_b, so_h, so_q, scale, stream, name);
 }

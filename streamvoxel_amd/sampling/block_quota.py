@@ -19,13 +19,26 @@ def _bytes(mask):
     return mask.contiguous().view(torch.uint8)
 
 
+_TOP_OUT = {}
+
+
+def _top_out(shape, device):
+    key = (torch.device(device), tuple(shape))
+    out = _TOP_OUT.get(key)
+    if out is None:
+        out = _TOP_OUT[key] = torch.empty(shape, dtype=torch.bool, device=device)
+    return out
+
+
 def top_mask(scores, eligible, count):
     """The `count` largest scores among `eligible`, ties to the lower flat index
-    (streamvoxel/sampling/block_quota.py:4-12). `count` is a host int or a 0-dim device int64 tensor."""
+    (streamvoxel/sampling/block_quota.py:4-12). `count` is a host int or a 0-dim device int64 tensor. The result
+    lives in a buffer of this module that the next call of the same shape on the device overwrites (clone it to
+    keep it); calls with contiguous fp32 scores and a device int64 count allocate nothing."""
     _lib.require_gpu(scores, eligible)
     s = scores.contiguous().float().reshape(-1)
     e = _bytes(eligible).reshape(-1)
-    out = torch.empty(eligible.shape, dtype=torch.bool, device=scores.device)
+    out = _top_out(eligible.shape, scores.device)
     lib = _lib.load()
     if torch.is_tensor(count):
         cnt = count.to(device=scores.device, dtype=torch.int64).reshape(1)
@@ -58,7 +71,7 @@ def quota_select_into(score, mask, k, b, pos, frac, n_total, committed, chosen, 
     """Batched no-sync selection writing `chosen` [B,Y,Z,X] bool and `bad` [B] bool in place.
 
     score fp32 [B,Y,Z,X]; mask bool [B,Y,Z,X]; k, committed int64 [B]; frac float64 [B]; pos, n_total int64 [B,nb]
-    (all device tensors)."""
+    (all device tensors). committed None: derived on the device as sum(n_total) - sum(mask) per window."""
     _lib.require_gpu(score, mask, k, pos, frac, n_total, committed, chosen, bad)
     B, Y, Z, X = score.shape
     lib = _lib.load()
@@ -68,36 +81,68 @@ def quota_select_into(score, mask, k, b, pos, frac, n_total, committed, chosen, 
         _lib.ptr(workspace.buffer), workspace.buffer.numel(), _lib.stream_of(score)), 'svhip_quota_select')
 
 
-def _device_scalar(v, dtype, device):
+class _SelectBuffers:
+    """Per (device, window shape, block size): the workspace, the outputs and the per-call scalars of the one-window
+    functions below, so that repeated calls allocate nothing (the reference keeps the same buffers static,
+    fast_ops.py:501-510)."""
+
+    def __init__(self, shape, b, device):
+        nb = (shape[0] // b) * (shape[1] // b) * (shape[2] // b)
+        self.ws = QuotaWorkspace(1, shape, b, device)
+        self.chosen = torch.empty((1, *shape), dtype=torch.bool, device=device)
+        self.bad = torch.empty(1, dtype=torch.bool, device=device)
+        self.k = torch.empty(1, dtype=torch.int64, device=device)
+        self.committed = torch.empty(1, dtype=torch.int64, device=device)
+        self.frac = torch.empty(1, dtype=torch.float64, device=device)
+        self.pos = torch.empty(nb, dtype=torch.int64, device=device)
+        self.arange = torch.arange(nb, dtype=torch.int64, device=device)
+
+
+_BUFFERS = {}
+
+
+def _buffers(shape, b, device):
+    key = (torch.device(device), tuple(shape), int(b))
+    buf = _BUFFERS.get(key)
+    if buf is None:
+        buf = _BUFFERS[key] = _SelectBuffers(tuple(shape), int(b), device)
+    return buf
+
+
+def _set_scalar(dst, v):
+    """A host number or a 0-dim / one-element device tensor into the one-element device buffer `dst`, without an
+    allocation and without a host read."""
     if torch.is_tensor(v):
-        return v.to(device=device, dtype=dtype).reshape(1)
-    return torch.full((1,), v, dtype=dtype, device=device)
+        dst.copy_(v.reshape(1))
+    else:
+        dst.fill_(v)
+    return dst
 
 
 def quota_select(score, mask, k, b, pos, frac, n_total, committed):
     """One window, like `quota_select_nosync` (streamvoxel/stream/fast_ops.py:442-473): k, frac and committed are
-    host numbers or 0-dim device tensors; pos is the inverse block order."""
+    host numbers or 0-dim device tensors (committed None: derived on the device as sum(n_total) - sum(mask)); pos
+    is the inverse block order. The returned mask lives in a buffer of
+    this module that the next call for the same (device, window shape, block size) overwrites, as the reference's
+    static `chosen` is (clone it to keep it); with fp32 contiguous scores, int64 pos / n_total and a contiguous
+    mask, a call allocates nothing."""
     _lib.require_gpu(score, mask)
     device = score.device
     shape = tuple(score.shape)
-    chosen = torch.empty((1, *shape), dtype=torch.bool, device=device)
-    bad = torch.empty(1, dtype=torch.bool, device=device)
-    ws = QuotaWorkspace(1, shape, b, device)
+    buf = _buffers(shape, b, device)
     quota_select_into(score.contiguous().float().reshape(1, *shape), mask.contiguous().reshape(1, *shape),
-                      _device_scalar(k, torch.int64, device), b, pos.to(device=device, dtype=torch.int64).reshape(1, -1),
-                      _device_scalar(frac, torch.float64, device),
-                      n_total.to(device=device, dtype=torch.int64).reshape(1, -1),
-                      _device_scalar(committed, torch.int64, device), chosen, bad, ws)
-    return chosen[0]
+                      _set_scalar(buf.k, k), b, pos.to(device=device, dtype=torch.int64).reshape(1, -1),
+                      _set_scalar(buf.frac, frac), n_total.to(device=device, dtype=torch.int64).reshape(1, -1),
+                      None if committed is None else _set_scalar(buf.committed, committed), buf.chosen, buf.bad,
+                      buf.ws)
+    return buf.chosen[0]
 
 
 def block_quota_select(score, mask, k, b, order, frac, n_total):
     """Exactly k voxels of `mask`, balanced over b^3 blocks (streamvoxel/sampling/block_quota.py:20-38). `order` is
-    the seeded block order; the committed count is derived on the device as sum(n_total) - sum(mask)."""
+    the seeded block order; the committed count is derived on the device as sum(n_total) - sum(mask). The result
+    is the reused buffer of `quota_select`."""
     _lib.require_gpu(score, mask, order, n_total)
-    device = score.device
-    pos = torch.empty_like(order)
-    pos[order] = torch.arange(len(order), device=device, dtype=order.dtype)
-    n_total = n_total.to(dtype=torch.int64)
-    committed = (n_total.sum() - mask.sum()).reshape(1)
-    return quota_select(score, mask, k, b, pos, frac, n_total, committed)
+    buf = _buffers(tuple(score.shape), b, score.device)
+    pos = buf.pos.scatter_(0, order.to(torch.int64), buf.arange)
+    return quota_select(score, mask, k, b, pos, frac, n_total, None)

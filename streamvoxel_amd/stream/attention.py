@@ -23,8 +23,13 @@ def _kv_code(t):
     raise TypeError(f'K/V dtype {t.dtype} unsupported (bfloat16, float8_e4m3fn or uint8 e4m3 codes)')
 
 
-def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scale=None, v_scale=None, out=None):
+def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scale=None, v_scale=None, out=None,
+              key_mask=None):
     """softmax(scale * Q K^T) V over the first L_b keys of every window b.
+
+    `key_mask` (optional, bf16 K/V): bool [B, Kcap] (padded) or [B, max L] (packed); key j of window b is attended
+    only where it is True (any pattern; a query with no attended key gets zeros). `lengths` / `cu_seqlens` may then
+    be omitted (every key up to the capacity, the mask decides).
 
     query [B,H,Q,D] bf16 (head_dim contiguous; any other strides). key, val: padded [B,H,Kcap,D] with
     lengths int32 [B] (device), or packed [H, sum L, D] with cu_seqlens int32 [B+1] (device). `val` may be a
@@ -36,8 +41,14 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
     if query.dtype != torch.bfloat16:
         raise TypeError('query must be bfloat16')
     B, H, Q, D = query.shape
-    if (lengths is None) == (cu_seqlens is None):
-        raise ValueError('pass exactly one of lengths / cu_seqlens')
+    if lengths is not None and cu_seqlens is not None:
+        raise ValueError('pass at most one of lengths / cu_seqlens')
+    if lengths is None and cu_seqlens is None and key_mask is None:
+        raise ValueError('pass lengths, cu_seqlens or key_mask')
+    if key_mask is not None:
+        _lib.require_gpu(key_mask)
+        if key_mask.dtype != torch.bool or key_mask.dim() != 2 or key_mask.shape[0] != B or key_mask.stride(1) != 1:
+            raise ValueError('key_mask must be bool [B, keys] with contiguous keys')
     code = _kv_code(key)
     if _kv_code(val) != code:
         raise TypeError('key and val must share a dtype')
@@ -60,7 +71,7 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
     else:
         if key.dim() != 4 or key.shape[:2] != (B, H) or val.shape != key.shape:
             raise ValueError('padded K/V are [B,H,Kcap,D] like the query')
-        if lengths.dtype != torch.int32 or lengths.numel() != B:
+        if lengths is not None and (lengths.dtype != torch.int32 or lengths.numel() != B):
             raise ValueError('lengths must be int32 [B]')
         kcap = key.shape[2]
         sk = (key.stride(0), key.stride(1), key.stride(2))
@@ -69,6 +80,18 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
         raise ValueError('head_dim mismatch')
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     lib = _lib.load()
+    if key_mask is not None:
+        if code != _lib.SVHIP_BF16:
+            raise TypeError('the key mask takes bf16 K/V')
+        if cu_seqlens is None and key_mask.shape[1] < kcap:
+            raise ValueError(f'key_mask holds {key_mask.shape[1]} keys per window, the cache {kcap}')
+        _lib.check(lib.svhip_xattn_fwd_masked(
+            _lib.ptr(query), _lib.ptr(key), _lib.ptr(val), _lib.ptr(out), _lib.ptr(key_mask.view(torch.uint8)),
+            key_mask.stride(0), _lib.ptr(lengths), _lib.ptr(cu_seqlens), B, H, Q, D,
+            kcap if cu_seqlens is None else key_mask.shape[1], query.stride(0), query.stride(1), query.stride(2),
+            *sk, *sv, out.stride(0), out.stride(1), out.stride(2), scale, _lib.stream_of(query)),
+            'svhip_xattn_fwd_masked')
+        return out
     kp = key.view(torch.uint8) if code == _lib.SVHIP_FP8_E4M3 else key
     vp = val.view(torch.uint8) if code == _lib.SVHIP_FP8_E4M3 else val
     _lib.check(lib.svhip_xattn_fwd(

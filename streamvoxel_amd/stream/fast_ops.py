@@ -38,11 +38,11 @@ def cross_flex(cross, value, positions, key, val, lengths):
 
 
 def cross_sdpa(cross, value, positions, key, val, valid):
-    """fast_ops.py:111-115 with `valid` [n, Kcap] bool, the key-validity mask `PackedKeys` keeps (valid keys
-    first, fast_ops.py:139-147): the window lengths are its row sums."""
+    """fast_ops.py:111-115 with `valid` [n, Kcap] bool, the key mask of the masked SDPA (any pattern: the
+    kernel attends exactly the True keys of each window)."""
     batch, queries, width = value.shape
     query = cross_query(cross, value, positions)
-    out = attention(query, key, val, lengths=valid.sum(-1, dtype=torch.int32))
+    out = attention(query, key, val, key_mask=valid.contiguous())
     return _project(cross, out, batch, queries, width)
 
 

@@ -292,3 +292,71 @@ def test_many_windows(dev, B, H):
     out = attention(q.to(dev), k.to(dev), v.to(dev), lengths=torch.tensor(lengths, dtype=torch.int32, device=dev))
     torch.cuda.synchronize()
     check(out, ref, BF16_ATOL, BF16_RTOL)
+
+
+def _masked_reference(q, k, v, mask, lengths=None):
+    """float64 attention of every window over exactly its attended keys (mask True, below the length): the
+    oracle's attention over the gathered keys; a window-query with no attended key gets zeros."""
+    B, H, Q, D = q.shape
+    out = torch.zeros((B, H, Q, D), dtype=torch.float64)
+    for b in range(B):
+        keep = mask[b].clone()
+        if lengths is not None:
+            keep[int(lengths[b]):] = False
+        idx = keep.nonzero().squeeze(1)
+        if len(idx) == 0:
+            continue
+        out[b:b + 1] = A.cross_attention(q[b:b + 1], k[b:b + 1, :, idx], v[b:b + 1, :, idx], [len(idx)])
+    return out
+
+
+@pytest.mark.parametrize('D', [64, 48, 96, 128])
+@pytest.mark.parametrize('transposed', [False, True])
+def test_key_mask_any_pattern(dev, D, transposed):
+    """svhip_xattn_fwd_masked: random masks, a first block wholly masked, a window wholly masked (zeros), with and
+    without lengths, V row-major and transposed."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, kcap = 4, 3, 200, 300
+    _case(f'xattn key mask D={D} transposed={transposed}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=100 + D)
+    g = torch.Generator().manual_seed(D)
+    mask = torch.rand(B, kcap, generator=g) < 0.5
+    mask[1, :70] = False                     # the first block and a half without an attended key
+    mask[2] = False                          # nothing attended: zeros
+    mask[3, :] = False
+    mask[3, 299] = True                      # one key, in the partial last block
+    vd = v.to(dev)
+    if transposed:
+        vd = vd.transpose(2, 3).contiguous().transpose(2, 3)
+    for lengths in (None, [300, 250, 10, 300]):
+        lt = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=dev)
+        out = attention(q.to(dev), k.to(dev), vd, lengths=lt, key_mask=mask.to(dev))
+        torch.cuda.synchronize()
+        ref = _masked_reference(q, k, v, mask, lengths)
+        check(out, ref, BF16_ATOL, BF16_RTOL)
+        assert torch.all(out[2] == 0)
+
+
+def test_key_mask_prefix_equals_lengths_and_packed(dev):
+    """A prefix mask gives the bits of the length form; the packed cu_seqlens layout takes the mask per window."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, kcap, D = 3, 4, 130, 520, 64
+    lengths = [520, 77, 1]
+    _case('xattn key mask prefix == lengths; packed + mask')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=7)
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    prefix = torch.arange(kcap, device=dev)[None] < lt[:, None]
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    a = attention(qd, kd, vd, lengths=lt)
+    b = attention(qd, kd, vd, key_mask=prefix)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    # packed: window b's keys at rows cu[b] .. cu[b + 1], a random mask per window
+    cu = torch.tensor([0, 520, 597, 598], dtype=torch.int32)
+    kp = torch.cat([k[i, :, :lengths[i]] for i in range(B)], 1)
+    vp = torch.cat([v[i, :, :lengths[i]] for i in range(B)], 1)
+    mask = torch.rand(B, kcap, generator=torch.Generator().manual_seed(3)) < 0.7
+    mask[2, 0] = True
+    out = attention(qd, kp.to(dev), vp.to(dev), cu_seqlens=cu.to(dev), key_mask=mask.to(dev))
+    torch.cuda.synchronize()
+    check(out, _masked_reference(q, k, v, mask, lengths), BF16_ATOL, BF16_RTOL)

@@ -281,6 +281,19 @@ def test_attention_matches_bruteforce_and_ignores_padding():
     assert torch.all(zero[0] == 0)
 
 
+def test_masked_sdpa_with_any_mask_is_attention_over_the_kept_keys():
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(2, 2, 3, 4, generator=g, dtype=torch.float64)
+    k = torch.randn(2, 2, 9, 4, generator=g, dtype=torch.float64)
+    v = torch.randn(2, 2, 9, 4, generator=g, dtype=torch.float64)
+    valid = torch.tensor([[1, 0, 1, 1, 0, 0, 1, 0, 1], [0, 0, 0, 0, 1, 0, 0, 0, 0]], dtype=torch.bool)
+    got = A.masked_sdpa_mask(q, k, v, valid)
+    for b in range(2):
+        idx = valid[b].nonzero().squeeze(1)
+        want = A.cross_attention_bruteforce(q[b:b + 1], k[b:b + 1, :, idx], v[b:b + 1, :, idx], [len(idx)])
+        torch.testing.assert_close(got[b:b + 1], want, rtol=0, atol=1e-12)
+
+
 def test_attention_packed_equals_padded():
     g = torch.Generator().manual_seed(3)
     lengths = [7, 1, 12]
