@@ -69,7 +69,7 @@ def rotary_attention(x, positions, params, heads, prefix='attn.'):
     D = w // heads
     qkv = linear(x, params[prefix + 'qkv.weight'], params[prefix + 'qkv.bias']).reshape(b, n, 3, heads, D)
     q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
-    freq = P.rope_frequencies(D)
+    freq = params.get(prefix + 'rope.frequencies', P.rope_frequencies(D))
     q = P.axial_rope(q, positions, freq)
     k = P.axial_rope(k, positions, freq)
     o = A.cross_attention(q, k, v, [n] * b)
@@ -119,25 +119,30 @@ def _sub(params, prefix):
     return {k[len(prefix):]: v for k, v in params.items() if k.startswith(prefix)}
 
 
-def time_encoding(t, params, time_dim):
-    """UnconditionalMD4DiT.time_encoding (unconditional_md4_timefree.py:119-125) in float64: sinusoidal features
-    of t, time_mlp (Linear, GELU, Linear), time_projection (SiLU, Linear)."""
+def time_encoding(t, params, time_dim, time_free=False):
+    """UnconditionalMD4DiT.time_encoding (unconditional_md4_timefree.py:119-125): sinusoidal features of t formed
+    in fp32 as the module forms them, then time_mlp (Linear, GELU, Linear) and time_projection (SiLU, Linear) in
+    float64; a time-free model returns its `constant_time` for every window."""
+    if time_free:
+        return _d(params['constant_time'])[None].expand(len(t), -1)
     half = time_dim // 8
-    freq = torch.exp(-math.log(10000.0) * torch.arange(half, dtype=F64) / half)
-    phase = _d(t)[:, None] * freq
-    h = torch.cat((phase.sin(), phase.cos()), -1)
+    # The module forms the frequencies, the phases and their sines and cosines in fp32.
+    freq = torch.exp(-math.log(10000.0) * torch.arange(half).float() / half)
+    phase = torch.as_tensor(t).float()[:, None] * freq
+    h = _d(torch.cat((phase.sin(), phase.cos()), -1))
     h = linear(gelu(linear(h, params['time_mlp.0.weight'], params['time_mlp.0.bias'])), params['time_mlp.2.weight'],
                params['time_mlp.2.bias'])
     return linear(silu(h), params['time_projection.1.weight'], params['time_projection.1.bias'])
 
 
 def step_forward(params, tokens, timestep, origin, group_origin, keys, values, lengths, *, depth, heads,
-                 control_heads, layer_map, patch, y_range, time_dim, voxel_shape):
+                 control_heads, layer_map, patch, y_range, time_dim, voxel_shape, timed=True, time_free=False):
     """FastSlotForward.forward (stream/fast_ops.py:274-308) in float64 from the model's state dict `params`
     (backbone.*, control.*, cross.*, zero.*): gather patchify + height embedding, the backbone blocks with the
     control block, cross attention over keys[j] / values[j] [n, H, Kcap, D] (first lengths[b] keys of window b)
-    and zero projection at every mapped block, final AdaLN LayerNorm, class head. Returns the head's rows
-    [n, N, p^3 C]."""
+    and zero projection at every mapped block, final LayerNorm (AdaLN-modulated when `timed`, affine otherwise),
+    class head. timed: the AdaLN blocks of unconditional_md4_timefree.py (time_free: the constant time), else the
+    affine blocks of unconditional_md4.py. Returns the head's rows [n, N, p^3 C]."""
     bb, cc = _sub(params, 'backbone.'), _sub(params, 'control.')
     centers = _d(bb['patch_centers_xyz'])[None] + _d(origin)[:, None]
     positions = (centers - _d(group_origin)[None, None]) / 4
@@ -152,7 +157,8 @@ def step_forward(params, tokens, timestep, origin, group_origin, keys, values, l
         return x + e
 
     b, c = embed(bb), embed(cc)
-    bt, ct = time_encoding(timestep, bb, time_dim), time_encoding(timestep, cc, time_dim)
+    bt = time_encoding(timestep, bb, time_dim, time_free) if timed else None
+    ct = time_encoding(timestep, cc, time_dim, time_free) if timed else None
     for i in range(depth):
         b_next = block(b, bt, sa_positions.float(), _sub(bb, f'blocks.{i}.'), heads)
         j = layer_map.get(i)
@@ -163,11 +169,14 @@ def step_forward(params, tokens, timestep, origin, group_origin, keys, values, l
             D = W // control_heads
             q = linear(layer_norm(c, 1e-6), cp['query.weight'], cp['query.bias'])
             q = q.reshape(n, -1, control_heads, D).transpose(1, 2)
-            q = P.axial_rope(q, positions.float(), P.rope_frequencies(D))
+            q = P.axial_rope(q, positions.float(), cp.get('rope.frequencies', P.rope_frequencies(D)))
             o = A.cross_attention(q, keys[j], values[j], lengths)
             c = c + linear(o.transpose(1, 2).reshape(n, -1, W), cp['proj.weight'], cp['proj.bias'])
             b_next = b_next + linear(c, params[f'zero.{j}.weight'], params[f'zero.{j}.bias'])
         b = b_next
-    shift, gain = linear(silu(bt), bb['final_ada.1.weight'], bb['final_ada.1.bias']).chunk(2, -1)
-    h = modulate(layer_norm(b, 1e-6), shift, gain)
+    if timed:
+        shift, gain = linear(silu(bt), bb['final_ada.1.weight'], bb['final_ada.1.bias']).chunk(2, -1)
+        h = modulate(layer_norm(b, 1e-6), shift, gain)
+    else:
+        h = layer_norm(b, 1e-6, bb.get('final_norm.weight'), bb.get('final_norm.bias'))
     return linear(h, bb['class_head.weight'], bb['class_head.bias'])

@@ -23,14 +23,18 @@ def rope_frequencies(head_dim, base=10000.0):
 
 
 def axial_rope(x, positions, frequencies):
-    """x [B,H,N,D] (float dtype), positions [B,N,3] -> rotated x in x's dtype (unconditional_md4.py:18-24)."""
+    """x [B,H,N,D] (float dtype), positions [B,N,3] -> rotated x in x's dtype (unconditional_md4.py:18-24). The
+    phases are the fp32 positions times the frequencies buffer in the promotion of fp32 and the buffer's dtype, as
+    the module computes them: fp32 for the fp32 buffer, fp64 for a module cast to double."""
     n_freq = frequencies.numel()
     D = x.shape[-1]
     if D != 6 * n_freq:
         raise ValueError((D, n_freq))
     out = torch.empty_like(x)
+    if not frequencies.is_floating_point() or frequencies.dtype.itemsize < 4:
+        frequencies = frequencies.float()
     for axis in range(3):
-        theta = positions[..., axis].float()[..., None] * frequencies.float()      # [B, N, n_freq], fp32
+        theta = positions[..., axis].float()[..., None] * frequencies      # [B, N, n_freq]
         s = theta.sin()[:, None].to(x.dtype)
         c = theta.cos()[:, None].to(x.dtype)
         lo = axis * 2 * n_freq

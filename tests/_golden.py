@@ -58,3 +58,31 @@ def tiny_logits(step, shape, classes, ground):
     logits = torch.randn((classes, *shape), generator=generator)
     logits[0, ground:] += 30.
     return logits
+
+
+def hash_fill(shape, seed, scale=1.0):
+    """Deterministic values in [-scale, scale) for the forward fixtures: splitmix64 of (index, seed), top 24 bits,
+    u / 2^23 - 1, times `scale` (a power of two, so every value is exact in fp32 and fp64). The fixture script and
+    the tests draw weights and inputs from it by name, so the vectors carry no weights."""
+    n = int(np.prod(shape)) if len(shape) else 1
+    with np.errstate(over='ignore'):
+        z = np.arange(n, dtype=np.uint64) + np.uint64(seed) * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    u = (z >> np.uint64(40)).astype(np.float64)
+    return ((u / 2.0 ** 23 - 1.0) * scale).reshape(shape)
+
+
+def name_seed(name, salt=0):
+    """A stable per-name seed (CRC-32 of the name) for hash_fill."""
+    import zlib
+    return zlib.crc32(name.encode()) + 7919 * salt
+
+
+def forward_meta():
+    return _json('forward.json')
+
+
+def forward_arrays():
+    return np.load(os.path.join(GOLDEN, 'forward.npz'))

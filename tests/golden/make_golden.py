@@ -2,7 +2,7 @@
 
 Run in the build container only (the reference checkout is not present where the tests run):
 
-    python tests/golden/make_golden.py /root/reference [sampling|rope]
+    python tests/golden/make_golden.py /root/reference [sampling|rope|forward]
 
 It imports the reference's pure-torch sampling functions and slot state machine, on the CPU, for the functions that
 closed forms, brute force and invariants do not pin literally:
@@ -11,7 +11,11 @@ closed forms, brute force and invariants do not pin literally:
   * low_entropy_last_update (streamvoxel/sampling/low_entropy_last.py:8-17) at the fp32 threshold;
   * LowEntropyLastSlot trajectories (streamvoxel/stream/slot.py:50-176);
   * AxialRoPE (streamvoxel/models/unconditional_md4.py:10-24) on bf16 activations - the exact bf16 bits, which
-    depend on the module's rounding order.
+    depend on the module's rounding order;
+  * UnconditionalBlock with non-zero AdaLN shifts / scales / gates and the affine block, the time encoding, and one
+    step forward of a tiny CompactStreamingControlNet through its own forward (models/compact_controlnet.py,
+    models/unconditional_md4*.py) - what the step's oracle composes, with every weight and the zero projections
+    non-zero.
 Only data is written (inputs and expected outputs); no reference source is copied.
 """
 from __future__ import annotations
@@ -24,6 +28,7 @@ import numpy as np
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(HERE))      # tests/: the fixtures' own fill helper (_golden.hash_fill)
 
 
 def tie_state(seed, shape, b):
@@ -205,6 +210,97 @@ def rope_cases(AxialRoPE):
         json.dump(meta, f, indent=1)
 
 
+FWD_SCALE = 2.0 ** -3        # weights in [-1/8, 1/8): exact in fp32 and fp64
+FWD_SHAPE = (16, 8, 8)        # window of the step fixtures (patch 4: 4 x 2 x 2 patch tokens)
+
+
+def _fill(module, prefix):
+    """Every parameter of `module` from hash_fill by its prefixed name (buffers keep the module's values)."""
+    from _golden import hash_fill, name_seed
+    names = []
+    with torch.no_grad():
+        for name, p in module.named_parameters():
+            p.copy_(torch.from_numpy(hash_fill(tuple(p.shape), name_seed(prefix + name), FWD_SCALE)).to(p.dtype))
+            names.append([name, list(p.shape)])
+    return names
+
+
+def _positions(shape, seed, span):
+    """Multiples of 1/8 in [-span, span) (exact in fp32)."""
+    from _golden import hash_fill
+    return torch.from_numpy(np.round(hash_fill(shape, seed, span) * 8) / 8)
+
+
+def forward_cases(ada_block, affine_block, ada_dit, plain_dit, compact):
+    """The forward of the streaming ControlNet's pieces from the reference modules, weights and inputs drawn from
+    hash_fill by name: UnconditionalBlock with AdaLN (non-zero shifts, scales and gates) and the affine one, in
+    float64; the time encoding of the time-conditioned model (its sinusoidal features are fp32 in the module, so
+    the model runs in fp32); and one step of a tiny CompactStreamingControlNet (5 x 48 backbone, 3 x 24 control,
+    4 heads, a 16 x 8 x 8 window of 3 classes) through its own forward (the unpadded reference of the slot
+    engines, stream/engine.py:87-102) in three variants: affine blocks (float64), time-free AdaLN (float64) and
+    time-conditioned AdaLN (float32)."""
+    from _golden import hash_fill, name_seed
+    arrays, meta = {}, dict(blocks=[], step=[])
+    W, H, N, B = 24, 2, 7, 2
+    for kind, cls in (('ada', ada_block), ('affine', affine_block)):
+        blk = cls(W, H, 4.0).double().eval()
+        names = _fill(blk, f'block_{kind}.')
+        x = torch.from_numpy(hash_fill((B, N, W), name_seed(f'block_{kind}.x'), 1.0))
+        t = torch.from_numpy(hash_fill((B, W), name_seed(f'block_{kind}.t'), 1.0))
+        pos = _positions((B, N, 3), name_seed(f'block_{kind}.pos'), 8.0)
+        with torch.no_grad():
+            out = blk(x, t, pos) if kind == 'ada' else blk(x, pos)
+        arrays[f'block_{kind}/out'] = out.numpy()
+        meta['blocks'].append(dict(kind=kind, width=W, heads=H, tokens=N, batch=B, params=names))
+    # time encoding (fp32 module)
+    dit = ada_dit(num_classes=3, voxel_shape=FWD_SHAPE, hidden_dim=48, depth=1, num_heads=4, time_dim=256).eval()
+    names = _fill(dit, 'time.')
+    ts = torch.tensor([0.0, 0.1, 0.37, 0.5, 0.999, 1.0])
+    with torch.no_grad():
+        arrays['time/out'] = dit.time_encoding(ts).double().numpy()
+    meta['time'] = dict(t=ts.tolist(), time_dim=256, hidden=48,
+                        params=[n for n in names if n[0].startswith(('time_mlp.', 'time_projection.'))])
+    # one step of the tiny compact ControlNet
+    C, P, L = 3, 5, 37
+    for variant, dtype in (('affine', torch.float64), ('time_free', torch.float64), ('timed', torch.float32)):
+        torch.manual_seed(0)
+        if variant == 'affine':
+            base = plain_dit(num_classes=C, voxel_shape=FWD_SHAPE, hidden_dim=48, depth=5, num_heads=4)
+        else:
+            base = ada_dit(num_classes=C, voxel_shape=FWD_SHAPE, hidden_dim=48, depth=5, num_heads=4,
+                           time_free=variant == 'time_free')
+        model = compact(base, control_depth=3, control_hidden_dim=24, checkpointing=False, biome_halo=4,
+                        biome_patch=2, struct_classes=0).to(dtype).eval()
+        names = _fill(model, f'step_{variant}.')
+        pre = f'step_{variant}.'
+        u = hash_fill((1, *FWD_SHAPE), name_seed(pre + 'tokens'), 1.0)
+        tokens = torch.from_numpy(np.minimum(np.floor((u + 1.0) * 2.0), 3).astype(np.int64))
+        heads, cw = 4, 24
+        prefix = [(torch.from_numpy(hash_fill((1, heads, P, cw // heads), name_seed(pre + f'pk{j}'), 1.0)).to(dtype),
+                   torch.from_numpy(hash_fill((1, heads, P, cw // heads), name_seed(pre + f'pv{j}'), 1.0)).to(dtype))
+                  for j in range(3)]
+        local = torch.from_numpy(hash_fill((1, L, cw), name_seed(pre + 'local'), 1.0)).to(dtype)
+        lpos = _positions((1, L, 3), name_seed(pre + 'local_pos'), 16.0).to(dtype)
+        t = torch.tensor([0.37])
+        origin = torch.tensor([[16.0, -48.0, 8.0]], dtype=dtype)
+        group = torch.tensor([0.0, -64.0, 0.0], dtype=dtype)
+        with torch.no_grad():
+            out = model(tokens, timestep=t, origin_xyz=origin, group_origin_xyz=group, prefix_kv=prefix, local=local,
+                        local_positions=lpos)
+        arrays[f'step_{variant}/out'] = out.double().numpy()
+        arrays[f'step_{variant}/patch_centers_xyz'] = model.backbone.patch_centers_xyz.double().numpy()
+        keep = [n for n in names if n[0].split('.')[0] in ('backbone', 'control', 'cross', 'zero')]
+        meta['step'].append(dict(variant=variant, dtype=str(dtype).replace('torch.', ''), classes=C, prefix=P,
+                                 local=L, depth=5, heads=heads, control_heads=heads, width=48, control_width=cw,
+                                 layer_map={str(k): v for k, v in model.layer_map.items()}, patch=4,
+                                 y_range=list(model.backbone.y_range), time_dim=256, voxel_shape=list(FWD_SHAPE),
+                                 timestep=t.tolist(), origin=origin.tolist(), group_origin=group.tolist(),
+                                 params=keep))
+    np.savez_compressed(os.path.join(HERE, 'forward.npz'), **arrays)
+    with open(os.path.join(HERE, 'forward.json'), 'w') as f:
+        json.dump(meta, f)
+
+
 def main(reference, only=None):
     sys.path.insert(0, reference)
     from streamvoxel.sampling.block_quota import block_quota_select, block_view
@@ -220,6 +316,13 @@ def main(reference, only=None):
         slot_cases(LowEntropyLastSlot)
     if only in (None, 'rope'):
         rope_cases(AxialRoPE)
+    if only in (None, 'forward'):
+        from streamvoxel.models.compact_controlnet import CompactStreamingControlNet
+        from streamvoxel.models.unconditional_md4 import UnconditionalBlock as AffineBlock
+        from streamvoxel.models.unconditional_md4 import UnconditionalMD4DiT as PlainDiT
+        from streamvoxel.models.unconditional_md4_timefree import UnconditionalBlock as AdaBlock
+        from streamvoxel.models.unconditional_md4_timefree import UnconditionalMD4DiT as AdaDiT
+        forward_cases(AdaBlock, AffineBlock, AdaDiT, PlainDiT, CompactStreamingControlNet)
     with open(os.path.join(HERE, 'provenance.json'), 'w') as f:
         json.dump(dict(torch=torch.__version__, numpy=np.__version__, reference=reference,
                        script='tests/golden/make_golden.py'), f, indent=1)

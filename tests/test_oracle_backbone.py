@@ -1,6 +1,8 @@
 """Pins of the transformer-block oracle (oracle/backbone.py) by closed forms and invariants, on the CPU."""
 import math
 
+import numpy as np
+
 import torch
 
 from oracle import attention as A
@@ -177,3 +179,124 @@ def test_step_forward_with_identity_blocks_is_the_head_of_the_embedding():
     shift, gain = O.linear(O.silu(bt), bb['final_ada.1.weight'], bb['final_ada.1.bias']).chunk(2, -1)
     want = O.linear(O.modulate(O.layer_norm(x, 1e-6), shift, gain), bb['class_head.weight'], bb['class_head.bias'])
     assert torch.allclose(out, want, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------------------------------- reference vectors
+
+def _fixture_params(names, prefix, dtype):
+    """The fixture's weights, drawn by name from the same fill as tests/golden/make_golden.py, in `dtype` (the dtype
+    the reference module ran in) and then float64 (exact: every value is a multiple of 2^-26)."""
+    import _golden
+    scale = 2.0 ** -3
+    return {n: torch.from_numpy(_golden.hash_fill(tuple(shape), _golden.name_seed(prefix + n), scale)).to(dtype)
+            .to(F64) for n, shape in names}
+
+
+def test_blocks_match_the_reference_vectors():
+    """UnconditionalBlock with non-zero AdaLN shifts, scales and gates, and the affine block, against the
+    reference modules' float64 outputs; a swap of shift and scale (or of the two gates) misses by far more."""
+    import _golden
+    meta, data = _golden.forward_meta(), _golden.forward_arrays()
+    for m in meta['blocks']:
+        kind, W, H, N, B = m['kind'], m['width'], m['heads'], m['tokens'], m['batch']
+        params = _fixture_params(m['params'], f'block_{kind}.', F64)
+        x = torch.from_numpy(_golden.hash_fill((B, N, W), _golden.name_seed(f'block_{kind}.x'), 1.0))
+        t = torch.from_numpy(_golden.hash_fill((B, W), _golden.name_seed(f'block_{kind}.t'), 1.0))
+        pos = torch.from_numpy(np.round(_golden.hash_fill((B, N, 3), _golden.name_seed(f'block_{kind}.pos'), 8.0) * 8) / 8)
+        params['attn.rope.frequencies'] = P.rope_frequencies(W // H).double()
+        want = torch.from_numpy(data[f'block_{kind}/out'])
+        got = O.block(x, t if kind == 'ada' else None, pos, params, H)
+        torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+        if kind == 'ada':
+            w, bias = params['ada.1.weight'], params['ada.1.bias']
+            for a, b in ((0, 1), (2, 5)):          # (shift1, scale1), (gate1, gate2)
+                perm = list(range(6))
+                perm[a], perm[b] = b, a
+                swapped = dict(params, **{'ada.1.weight': w.view(6, W, W)[perm].reshape(6 * W, W),
+                                          'ada.1.bias': bias.view(6, W)[perm].reshape(6 * W)})
+                assert (O.block(x, t, pos, swapped, H) - want).abs().max() > 1e-3
+
+
+def test_time_encoding_matches_the_reference_vectors():
+    """The time-conditioned model's time encoding (sinusoidal features in fp32, then the MLP; the module ran in
+    fp32): within fp32 rounding of the reference, and far from it with the sines and cosines swapped."""
+    import _golden
+    meta, data = _golden.forward_meta(), _golden.forward_arrays()
+    m = meta['time']
+    params = _fixture_params(m['params'], 'time.', torch.float32)
+    want = torch.from_numpy(data['time/out'])
+    got = O.time_encoding(torch.tensor(m['t']), params, m['time_dim'])
+    err = (got - want).abs().max().item()
+    assert err <= 2e-6 * max(1.0, want.abs().max().item()), err
+    w = params['time_mlp.0.weight']
+    half = w.shape[1] // 2
+    swapped = dict(params, **{'time_mlp.0.weight': torch.cat((w[:, half:], w[:, :half]), 1)})
+    assert (O.time_encoding(torch.tensor(m['t']), swapped, m['time_dim']) - want).abs().max() > 1e-3
+
+
+def _step_inputs(m):
+    import _golden
+    pre = f"step_{m['variant']}."
+    dt = torch.float64 if m['dtype'] == 'float64' else torch.float32
+    hf = lambda shape, name, scale: torch.from_numpy(_golden.hash_fill(shape, _golden.name_seed(pre + name), scale))
+    u = _golden.hash_fill((1, *m['voxel_shape']), _golden.name_seed(pre + 'tokens'), 1.0)
+    tokens = torch.from_numpy(np.minimum(np.floor((u + 1.0) * 2.0), 3).astype(np.int64))
+    H, cw = m['control_heads'], m['control_width']
+    D = cw // H
+    prefix = [(hf((1, H, m['prefix'], D), f'pk{j}', 1.0), hf((1, H, m['prefix'], D), f'pv{j}', 1.0))
+              for j in range(len(m['layer_map']))]
+    local = hf((1, m['local'], cw), 'local', 1.0)
+    lpos = torch.round(hf((1, m['local'], 3), 'local_pos', 16.0) * 8) / 8
+    return tokens, prefix, local, lpos, dt
+
+
+def _oracle_step(m, params, tokens, prefix, local, lpos, dt):
+    """The step oracle fed the reference forward's condition: per cross layer, prefix K / V followed by the local
+    K / V (the layer's key_value projection of `local`, K rotated at the local positions)."""
+    H, cw = m['control_heads'], m['control_width']
+    D = cw // H
+    freq = P.rope_frequencies(D).to(dt)
+    keys, values = [], []
+    for j in range(len(m['layer_map'])):
+        kv = O.linear(local, params[f'cross.{j}.key_value.weight'], params[f'cross.{j}.key_value.bias'])
+        kv = kv.reshape(1, m['local'], 2, H, D)
+        k = P.axial_rope(kv[:, :, 0].transpose(1, 2).contiguous(), lpos.to(dt), freq)
+        keys.append(torch.cat((prefix[j][0], k), 2))
+        values.append(torch.cat((prefix[j][1], kv[:, :, 1].transpose(1, 2)), 2))
+    return O.step_forward(params, tokens, torch.tensor(m['timestep']), torch.tensor(m['origin'], dtype=F64),
+                          torch.tensor(m['group_origin'], dtype=F64), keys, values, [m['prefix'] + m['local']],
+                          depth=m['depth'], heads=m['heads'], control_heads=H,
+                          layer_map={int(k): v for k, v in m['layer_map'].items()}, patch=m['patch'],
+                          y_range=tuple(m['y_range']), time_dim=m['time_dim'], voxel_shape=tuple(m['voxel_shape']),
+                          timed=m['variant'] != 'affine', time_free=m['variant'] == 'time_free')
+
+
+def test_step_forward_matches_the_reference_vectors():
+    """One step of the tiny CompactStreamingControlNet (affine, time-free and time-conditioned variants, every zero
+    projection non-zero so the control -> cross attention -> injection path counts) against the reference
+    forward's logits: float64 variants to 1e-10, the fp32 one to its rounding. Dropping the injections misses."""
+    import _golden
+    from oracle import patches as PT
+    meta, data = _golden.forward_meta(), _golden.forward_arrays()
+    for m in meta['step']:
+        tokens, prefix, local, lpos, dt = _step_inputs(m)
+        params = _fixture_params(m['params'], f"step_{m['variant']}.", dt)
+        params['backbone.patch_centers_xyz'] = torch.from_numpy(data[f"step_{m['variant']}/patch_centers_xyz"])
+        for j in range(len(m['layer_map'])):
+            params[f'cross.{j}.rope.frequencies'] = P.rope_frequencies(m['control_width'] // m['heads']).to(dt)
+        for i in range(m['depth']):
+            params[f'backbone.blocks.{i}.attn.rope.frequencies'] = P.rope_frequencies(m['width'] // m['heads']).to(dt)
+        for j in range(len(m['layer_map'])):
+            params[f'control.blocks.{j}.attn.rope.frequencies'] = P.rope_frequencies(
+                m['control_width'] // m['heads']).to(dt)
+        rows = _oracle_step(m, params, tokens, prefix, local, lpos, dt)
+        got = PT.to_class_major(rows.numpy(), tuple(m['voxel_shape']), m['patch'], m['classes'])
+        want = data[f"step_{m['variant']}/out"]
+        scale = np.abs(want).max()
+        tol = 1e-10 if m['dtype'] == 'float64' else 1e-4
+        err = np.abs(got - want).max()
+        assert err <= tol * scale, (m['variant'], err, scale)
+        cut = dict(params, **{k: torch.zeros_like(v) for k, v in params.items() if k.startswith('zero.')})
+        rows = _oracle_step(m, cut, tokens, prefix, local, lpos, dt)
+        missed = np.abs(PT.to_class_major(rows.numpy(), tuple(m['voxel_shape']), m['patch'], m['classes']) - want).max()
+        assert missed > 100 * tol * scale, (m['variant'], missed)
