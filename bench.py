@@ -52,7 +52,7 @@ def parse():
     p.add_argument('--no-forward', action='store_true', help='skip the whole-step forward component')
     p.add_argument('--forward-only', action='store_true',
                    help='time only the whole-step forward (shipped shape) and print its line')
-    p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'select'],
+    p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'select', 'select_planes'],
                    help='build only that kernel\'s inputs (the step\'s layer-0 attention or its first solid '
                         'selection), time 20 back-to-back launches and print one line: the run to profile')
     return p.parse_args()
@@ -423,7 +423,8 @@ def sampling_tail_component(w, dev, s=12):
 def kernel_only(dev, args):
     """One kernel of the step alone, on the step's own inputs: the cross-attention layer (8 windows, 12 x 64 heads,
     1024 queries, the step's key lengths; bf16 or e4m3 cache) or the first solid selection (8 windows, fp32 logits
-    [8 x 65536, 256], fresh token state). 20 launches in one graph, replayed 5 times."""
+    [8 x 65536, 256] as voxel rows, or as class planes [8, 256, 65536] for `select_planes`; fresh token state). 20
+    launches in one graph, replayed 5 times."""
     import torch
     from streamvoxel_amd import synth
     from streamvoxel_amd.stream.step import CachedContext, EaseSelect
@@ -449,6 +450,8 @@ def kernel_only(dev, args):
     for b in range(SLOTS):
         sel.bind_window(b, torch.randperm(VOXELS // BLOCK ** 3, generator=torch.Generator().manual_seed(b)))
         sel.set_step(b, k, 0, k / VOXELS)
+    if args.kernel == 'select_planes':       # the same logits as contiguous class planes [8, C, N]
+        logits = logits.view(SLOTS, VOXELS, CLASSES).transpose(1, 2).contiguous()
     t = time_graph(lambda: sel.run(logits), 20)
     nbytes = SLOTS * VOXELS * (CLASSES * 4 + 8 + 1 + 1)
     return dict(kernel=args.kernel, us_per_call=t * 1e6, GBps=nbytes / t / 1e9, bytes_per_call=nbytes)

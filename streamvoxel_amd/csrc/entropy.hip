@@ -32,6 +32,19 @@ __global__ __launch_bounds__(256) void stats_class_major(const T* __restrict__ x
   class_major_pass<T, VEC, MODE>(x, batch, n, C, sb, sc, sn, air_bits, o, blockIdx.x, gridDim.x);
 }
 
+template <typename T, int LPV, bool VEC, int MODE, int CMAX>
+__global__ __launch_bounds__(256) void stats_canonical(const T* __restrict__ x, int64_t batch, int64_t n, int64_t C,
+                                                       int64_t sb, int64_t sc, int64_t sn, int nv,
+                                                       const int32_t* __restrict__ air_ids, int n_air,
+                                                       float* __restrict__ out) {
+  extern __shared__ float tile[];
+  __shared__ uint32_t air_bits[MODE == kAirProb ? kMaxAirClasses / 32 : 1];
+  if constexpr (MODE == kAirProb) load_air_bits(air_bits, air_ids, n_air, C);
+  StoreF32 o{out};
+  canonical_tile_pass<T, LPV, VEC, MODE, CMAX>(x, batch, n, C, sb, sc, sn, nv, air_bits, o, blockIdx.x, gridDim.x,
+                                               tile);
+}
+
 template <typename T, int MODE>
 static int launch_stats(const T* x, int64_t batch, int64_t C, int64_t n, int64_t sb, int64_t sc, int64_t sn,
                         const int32_t* air_ids, int n_air, float* out, hipStream_t stream, VoxelRows rows,
@@ -67,6 +80,28 @@ static int launch_stats(const T* x, int64_t batch, int64_t C, int64_t n, int64_t
         break;
     }
 #undef SVHIP_VM
+  }
+  if (plan.layout == kCanonVec || plan.layout == kCanonScalar) {
+    const bool vec = plan.layout == kCanonVec;
+    const size_t lds = plan.lds;
+#define SVHIP_CANON(LPVV, VECV, CM)                                                                         \
+  stats_canonical<T, LPVV, VECV, MODE, CM><<<grid, 256, lds, stream>>>(x, batch, n, C, sb, sc, sn, plan.nv,    \
+                                                                       air_ids, n_air, out)
+    if (C <= 256) {
+      if (plan.lpv == 8) {
+        if (vec) SVHIP_CANON(8, true, 256); else SVHIP_CANON(8, false, 256);
+      } else {
+        if (vec) SVHIP_CANON(16, true, 256); else SVHIP_CANON(16, false, 256);
+      }
+    } else {
+      if (plan.lpv == 8) {
+        if (vec) SVHIP_CANON(8, true, kCanonMaxC); else SVHIP_CANON(8, false, kCanonMaxC);
+      } else {
+        if (vec) SVHIP_CANON(16, true, kCanonMaxC); else SVHIP_CANON(16, false, kCanonMaxC);
+      }
+    }
+#undef SVHIP_CANON
+    return SVHIP_OK;
   }
   if (plan.layout == kClassMajorVec) {
     stats_class_major<T, true, MODE><<<grid, 256, 0, stream>>>(x, batch, n, C, sb, sc, sn, air_ids, n_air, out);

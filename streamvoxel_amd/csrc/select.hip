@@ -885,10 +885,10 @@ struct KeyStore {
 
 // Workgroups [0, side) apportion window blockIdx.x (one wave); the rest run the entropy pass over the logits and
 // write the keys. The apportionment depends only on the selection state, so it runs alongside the HBM-bound pass.
-template <typename T, int LAYOUT, int NV, int LPV = 16>
+template <typename T, int LAYOUT, int NV, int LPV = 16, int CMAX = 256>
 __global__ __launch_bounds__(256) void ease_stats_kernel(const T* __restrict__ x, int64_t batch, int64_t n, int64_t C,
                                                          int64_t sb, int64_t sc, int64_t sn, KeyStore ks,
-                                                         ApportionArgs ap, int side, VoxelRows rows) {
+                                                         ApportionArgs ap, int side, VoxelRows rows, int nv = 0) {
   __shared__ uint64_t skey[kWaveBlocks];
   __shared__ uint32_t hist[256];
   if (static_cast<int>(blockIdx.x) < side) {
@@ -898,6 +898,10 @@ __global__ __launch_bounds__(256) void ease_stats_kernel(const T* __restrict__ x
   const int64_t blk = blockIdx.x - side, nblk = gridDim.x - side;
   if constexpr (LAYOUT == kVoxelMajor) {
     voxel_major_pass<T, NV, kEntropy, KeyStore, LPV>(x, batch * n, n, C, sb, sn, nullptr, ks, blk, nblk, rows);
+  } else if constexpr (LAYOUT == kCanonVec || LAYOUT == kCanonScalar) {
+    extern __shared__ float tile[];
+    canonical_tile_pass<T, LPV, LAYOUT == kCanonVec, kEntropy, CMAX>(x, batch, n, C, sb, sc, sn, nv, nullptr, ks, blk,
+                                                                     nblk, tile);
   } else {
     class_major_pass<T, LAYOUT == kClassMajorVec, kEntropy>(x, batch, n, C, sb, sc, sn, nullptr, ks, blk, nblk);
   }
@@ -937,6 +941,35 @@ static int launch_ease_stats(const T* x, int64_t batch, int64_t C, int64_t n, in
         break;
     }
 #undef SVHIP_EVM
+  }
+  if (plan.layout == kCanonVec || plan.layout == kCanonScalar) {
+    // NV is passed at run time here (the tile pass loops over it); the template slot carries 0.
+    const size_t lds = plan.lds;
+    const int nv = plan.nv;
+#define SVHIP_ECANON(LAY, LPVV, CM)                                                                          \
+  ease_stats_kernel<T, LAY, 0, LPVV, CM><<<grid, 256, lds, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side, rows, nv)
+#define SVHIP_ECANON_C(LAY, LPVV)           \
+  if (C <= 256) {                           \
+    SVHIP_ECANON(LAY, LPVV, 256);           \
+  } else {                                  \
+    SVHIP_ECANON(LAY, LPVV, kCanonMaxC);    \
+  }
+    if (plan.layout == kCanonVec) {
+      if (plan.lpv == 8) {
+        SVHIP_ECANON_C(kCanonVec, 8)
+      } else {
+        SVHIP_ECANON_C(kCanonVec, 16)
+      }
+    } else {
+      if (plan.lpv == 8) {
+        SVHIP_ECANON_C(kCanonScalar, 8)
+      } else {
+        SVHIP_ECANON_C(kCanonScalar, 16)
+      }
+    }
+#undef SVHIP_ECANON_C
+#undef SVHIP_ECANON
+    return SVHIP_OK;
   }
   if (plan.layout == kClassMajorVec) {
     ease_stats_kernel<T, kClassMajorVec, 0><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side, rows);

@@ -2,13 +2,20 @@
 // passes that a kernel runs over its share of the voxels and hands to an output functor.
 //
 // HBM-bound: every logit is read exactly once; all arithmetic is fp32.
-//  * voxel-major rows ([B,N,C], stride_c == 1): a 16-lane DPP row owns one voxel. Each lane loads NV 16-byte
-//    vectors of the voxel's row (coalesced 256-byte segments per row), keeps them in registers, and the row does
-//    an exact two-pass softmax (max, then sum e and sum e*(x-max)) with 16-lane DPP all-reduces.
-//  * class-major planes ([B,C,N], stride_n == 1, the layout the class head produces): each lane owns a 16-byte
-//    run of consecutive voxels and streams the classes in chunks of CH rows with an online (running max)
-//    softmax, so the plane is also read once and fully coalesced across the wave.
-//  * anything else: the class-major pass with scalar loads.
+//
+// The canonical per-voxel order. When C is a multiple of E = 16 / sizeof(T) elements and C / E <= 128, a voxel's
+// statistics are one fixed function of its C values (and of the element type), whatever the layout: LPV lanes
+// (8 or 16, `row_plan`), lane g holding the classes (g + LPV j) E + e for j < NV, e < E; the row max; per-lane
+// sums of p = exp(x - max) and of fma(p, x - max, .) (or of the air classes' p) in (j, e) order; then a balanced
+// tree over the lanes (DPP). The passes that follow it:
+//  * voxel-major rows ([B,N,C], stride_c == 1, 16-byte aligned): the LPV lanes load the voxel's row as NV 16-byte
+//    vectors each (coalesced segments per row) and keep it in registers;
+//  * any other layout with C <= kCanonMaxC (class-major planes [B,C,N] as the reference's permute leaves them,
+//    views, odd strides): a workgroup stages 32 voxels x C classes into LDS (16-byte loads along the voxels when
+//    stride_n == 1), transposed to voxel rows, and runs the same per-voxel function on them.
+// So the scores (and the selections ranked by them) of the same logits are bit-identical in every layout.
+// Other class counts: a class-major pass with an online (running max) softmax, each lane owning a 16-byte run of
+// voxels (stride_n == 1) or one voxel (scalar loads), streaming the classes.
 // Loads are issued unconditionally with clamped indices and masked afterwards: a load inside a branch is waited
 // for before the branch ends, which would serialise them.
 //
@@ -66,6 +73,45 @@ template <typename T>
 __device__ __forceinline__ void load16(const T* p, float* dst) {
   unpack16<T>(*reinterpret_cast<const uint4*>(p), dst);
 }
+
+// One logit of the canonical order into a lane's sums (the same instructions in every pass).
+template <int MODE>
+__device__ __forceinline__ void accumulate(float x, float m, int c, const uint32_t* air_bits, float& s, float& w) {
+  const float t = x - m;
+  const float p = fast_exp(t);
+  s += p;
+  if constexpr (MODE == kEntropy) {
+    w = __builtin_fmaf(p, t, w);
+  } else {
+    if (is_air(air_bits, c)) w += p;
+  }
+}
+
+// Lanes per voxel and 16-byte vectors per lane of the canonical order for C classes of T, or false when C has no
+// canonical order (not a multiple of the vector, or more than 128 vectors). Eight lanes when that leaves fewer
+// vector slots idle (e.g. 304 bf16 classes: 38 vectors, 5 per lane with 8 lanes, 3 with 16) and fits in eight
+// vectors per lane.
+struct RowPlan {
+  int lpv, nv;
+};
+
+template <typename T>
+__host__ __device__ inline bool row_plan(int64_t C, RowPlan* rp) {
+  constexpr int E = Vec16<T>::kElems;
+  if (C < E || C % E != 0) return false;
+  const int64_t vecs = C / E;
+  if (cdiv(vecs, 16) > 8) return false;
+  const bool eight = cdiv(vecs, 8) <= 8 && cdiv(vecs, 8) * 8 - vecs < cdiv(vecs, 16) * 16 - vecs;
+  rp->lpv = eight ? 8 : 16;
+  rp->nv = static_cast<int>(cdiv(vecs, rp->lpv));
+  return true;
+}
+
+constexpr int64_t kCanonMaxC = 384;  // classes the LDS-staged canonical pass takes: 32 x (C + 1) floats, under 64 KB with
+                                     // the selection kernel's own LDS
+constexpr int kCanonTile = 32;       // voxels per LDS tile
+
+__host__ inline size_t canon_lds_bytes(int64_t C) { return sizeof(float) * kCanonTile * (C + 1); }
 
 template <int MODE>
 __device__ __forceinline__ float finish_stat(float s, float w) {
@@ -138,21 +184,123 @@ __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int c = (g + LPV * j) * E + e;
-        if (c < C) {
-          const float t = v[j * E + e] - m;
-          const float p = fast_exp(t);
-          s += p;
-          if constexpr (MODE == kEntropy) {
-            w += p * t;
-          } else {
-            if (is_air(air_bits, c)) w += p;
-          }
-        }
+        if (c < C) accumulate<MODE>(v[j * E + e], m, c, air_bits, s, w);
       }
     }
     s = group_sum<LPV>(s);
     w = group_sum<LPV>(w);
     if (g == 0) out.store(voxel, finish_stat<MODE>(s, w), pre);
+  }
+}
+
+// The canonical order over any layout, staged through LDS: workgroup `blk` of `nblk` takes tiles of kCanonTile
+// voxels of one window, loads their C x kCanonTile logits into `tile` (kCanonTile rows of C + 1 floats, the odd
+// row length keeps the transposed writes conflict-free), then LPV lanes per voxel run the canonical per-voxel
+// function over the rows. VEC: stride_n == 1 with 16-byte aligned class rows (16-byte loads along the voxels).
+// Requires 256-thread workgroups and row_plan<T>(C) = (LPV, nv).
+// CMAX: a bound on C (256 or kCanonMaxC) that fixes the number of loads per thread and tile.
+template <typename T, int LPV, bool VEC, int MODE, int CMAX, typename Out>
+__device__ __forceinline__ void canonical_tile_pass(const T* __restrict__ x, int64_t batch, int64_t n, int64_t C,
+                                                    int64_t sb, int64_t sc, int64_t sn, int nv,
+                                                    const uint32_t* air_bits, Out& out, int64_t blk, int64_t nblk,
+                                                    float* tile) {
+  constexpr int E = Vec16<T>::kElems;
+  constexpr int TV = kCanonTile;
+  constexpr int VPR = 256 / LPV;  // voxels per round of the workgroup
+  static_assert(TV % VPR == 0 && TV % E == 0, "tile shape");
+  constexpr int CPV = TV / E;                              // 16-byte chunks per class row of a tile
+  constexpr int CLS = 256 / CPV;                           // classes per 16-byte load of the workgroup
+  constexpr int kLoads = (CMAX + CLS - 1) / CLS;           // a thread's loads per tile
+  const int64_t ld = C + 1;
+  const int64_t tiles = cdiv(n, TV);
+  const int64_t total = batch * tiles;
+  const int g = threadIdx.x & (LPV - 1);
+  const int v0 = (threadIdx.x % CPV) * E;
+  const int crow = threadIdx.x / CPV;
+  // VEC: the next tile's logits are loaded into registers while the current one is computed (n is a multiple of
+  // E, so a chunk lies wholly inside or outside the window; outside ones load a valid chunk and are not written).
+  float pf[VEC ? kLoads : 1][E];
+  auto issue = [&](int64_t id) __attribute__((always_inline)) {
+    const int64_t b = id / tiles;
+    const int64_t i0 = (id - b * tiles) * TV;
+    const int64_t iv = i0 + v0 < n ? i0 + v0 : n - E;
+    const T* base = x + b * sb + iv;
+    // Every load is issued unconditionally (class index clamped; the repeats of row C - 1 are served by the
+    // cache): a load under a branch would be waited for at the branch's end.
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+      const int64_t c = u * CLS + crow;
+      load16<T>(base + (c < C ? c : C - 1) * sc, pf[u]);
+    }
+  };
+  if constexpr (VEC) {
+    if (blk < total) issue(blk);
+  }
+  for (int64_t id = blk; id < total; id += nblk) {
+    const int64_t b = id / tiles;
+    const int64_t i0 = (id - b * tiles) * TV;
+    decltype(out.prefetch(0)) pre[TV / VPR];
+#pragma unroll
+    for (int r = 0; r < TV / VPR; ++r) {
+      const int64_t i = i0 + r * VPR + threadIdx.x / LPV;
+      pre[r] = out.prefetch(b * n + (i < n ? i : n - 1));
+    }
+    __syncthreads();  // the previous tile's rows have been read
+    if constexpr (VEC) {
+      // Unconditional writes too: classes past C land in the row's padding column C, which is never read, and
+      // voxels past the window in rows that are not stored.
+#pragma unroll
+      for (int u = 0; u < kLoads; ++u) {
+        const int64_t c = u * CLS + crow < C ? u * CLS + crow : C;
+#pragma unroll
+        for (int e = 0; e < E; ++e) tile[(v0 + e) * ld + c] = pf[u][e];
+      }
+    } else {
+      const T* base = x + b * sb;
+      for (int64_t idx = threadIdx.x; idx < C * TV; idx += 256) {
+        const int64_t c = idx / TV;
+        const int v = static_cast<int>(idx - c * TV);
+        const int64_t i = i0 + v < n ? i0 + v : n - 1;
+        tile[v * ld + c] = to_float<T>(base[c * sc + i * sn]);
+      }
+    }
+    __syncthreads();
+    // Issued after the barrier (which waits for outstanding loads): they land while this tile is computed.
+    if constexpr (VEC) {
+      if (id + nblk < total) issue(id + nblk);
+    }
+#pragma unroll
+    for (int r = 0; r < TV / VPR; ++r) {
+      const int vi = r * VPR + threadIdx.x / LPV;
+      const float* row = tile + vi * ld;
+      // The lane's classes in registers (at most 8 vectors), -inf past C, then the canonical arithmetic.
+      float v[8 * E];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int c = (g + LPV * j) * E + e;
+          v[j * E + e] = (j < nv && c < C) ? row[c] : -INFINITY;
+        }
+      }
+      float m = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 8 * E; ++e) m = fmaxf(m, v[e]);
+      m = group_max<LPV>(m);
+      float s = 0.f, w = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int c = (g + LPV * j) * E + e;
+          if (j < nv && c < C) accumulate<MODE>(v[j * E + e], m, c, air_bits, s, w);
+        }
+      }
+      s = group_sum<LPV>(s);
+      w = group_sum<LPV>(w);
+      const int64_t i = i0 + vi;
+      if (g == 0 && i < n) out.store(b * n + i, finish_stat<MODE>(s, w), pre[r]);
+    }
   }
 }
 
@@ -237,14 +385,22 @@ __device__ __forceinline__ void class_major_pass(const T* __restrict__ x, int64_
   }
 }
 
-// How a logits tensor is walked: 0 voxel-major vectors, 1 class-major vectors, 2 class-major scalars.
-enum StatsLayout { kVoxelMajor = 0, kClassMajorVec = 1, kClassMajorScalar = 2 };
+// How a logits tensor is walked: 0 voxel-major vectors, 1 class-major vectors, 2 class-major scalars (both
+// online), 3 / 4 the canonical order through LDS tiles (16-byte loads along the voxels / scalar loads).
+enum StatsLayout {
+  kVoxelMajor = 0,
+  kClassMajorVec = 1,
+  kClassMajorScalar = 2,
+  kCanonVec = 3,
+  kCanonScalar = 4
+};
 
 struct StatsPlan {
   int layout;
-  int nv;        // voxel-major: 16-byte vectors per lane
-  int lpv;       // voxel-major: lanes per voxel (8 when a row fits in 8 vectors per lane, else 16)
+  int nv;        // canonical order: 16-byte vectors per lane
+  int lpv;       // canonical order: lanes per voxel (8 or 16)
   int64_t grid;  // workgroups of 256 threads
+  size_t lds;    // dynamic LDS bytes (the canonical tile passes)
 };
 
 __host__ inline int64_t stats_grid(int64_t work_items) {
@@ -263,24 +419,25 @@ __host__ inline StatsPlan plan_stats(const T* x, int64_t batch, int64_t C, int64
   constexpr int E = Vec16<T>::kElems;
   const bool aligned_base = (reinterpret_cast<uintptr_t>(x) % 16) == 0;
   const int64_t bytes = sizeof(T);
-  if (sc == 1 && aligned_base && (C % E) == 0 && ((sn * bytes) % 16) == 0 && ((sb * bytes) % 16) == 0 &&
-      cdiv(C / E, 16) <= 8) {
-    // Eight lanes per row when that leaves fewer vector slots idle (e.g. 304 bf16 classes: 38 vectors, 5 per lane
-    // with 8 lanes, 3 with 16) and the row fits in eight vectors per lane.
-    const int64_t vecs = C / E;
-    const bool eight = cdiv(vecs, 8) <= 8 && cdiv(vecs, 8) * 8 - vecs < cdiv(vecs, 16) * 16 - vecs;
-    const int lpv = eight ? 8 : 16;
+  RowPlan rp;
+  const bool canon = row_plan<T>(C, &rp);
+  if (canon && sc == 1 && aligned_base && ((sn * bytes) % 16) == 0 && ((sb * bytes) % 16) == 0) {
     // Short rows run faster from a grid of 8 workgroups per CU that loops over the voxels (measured: 304 bf16
     // classes 99 -> 93 us per 8-window selection); long rows from one pass of workgroups over all voxels (256 fp32
     // classes: 100 us, 113 us with the capped grid).
-    const int64_t grid = eight ? std::min<int64_t>(stats_grid(batch * n * lpv), kShortRowWorkgroups)
-                               : stats_grid(batch * n * lpv);
-    return StatsPlan{kVoxelMajor, static_cast<int>(cdiv(C / E, lpv)), lpv, grid};
+    const int64_t grid = rp.lpv == 8 ? std::min<int64_t>(stats_grid(batch * n * rp.lpv), kShortRowWorkgroups)
+                                     : stats_grid(batch * n * rp.lpv);
+    return StatsPlan{kVoxelMajor, rp.nv, rp.lpv, grid, 0};
   }
-  if (sn == 1 && aligned_base && (n % E) == 0 && ((sc * bytes) % 16) == 0 && ((sb * bytes) % 16) == 0) {
-    return StatsPlan{kClassMajorVec, 0, 0, stats_grid(batch * (n / E))};
+  const bool vec = sn == 1 && aligned_base && (n % E) == 0 && ((sc * bytes) % 16) == 0 && ((sb * bytes) % 16) == 0;
+  if (canon && C <= kCanonMaxC) {
+    // A resident grid (the tile pass prefetches each workgroup's next tile): 4 workgroups per CU.
+    const int64_t tiles = batch * cdiv(n, kCanonTile);
+    return StatsPlan{vec ? kCanonVec : kCanonScalar, rp.nv, rp.lpv, std::min<int64_t>(std::max<int64_t>(tiles, 1), 1024),
+                     canon_lds_bytes(C)};
   }
-  return StatsPlan{kClassMajorScalar, 0, 0, stats_grid(batch * n)};
+  if (vec) return StatsPlan{kClassMajorVec, 0, 0, stats_grid(batch * (n / E)), 0};
+  return StatsPlan{kClassMajorScalar, 0, 0, stats_grid(batch * n), 0};
 }
 
 // VoxelRows of a [Y, Z, X] window whose logits are in the class head's patch order with patch size `patch`

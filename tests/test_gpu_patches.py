@@ -151,7 +151,7 @@ def test_slot_window_from_patch_logits(dev):
             flat[i].copy_(x)
         out.rows[:, out.row_index(torch.arange(N, device=dev))] = flat
         got_a = consume_batch(a, out, engine.tokens, slots_n, graphs)
-        permuted = flat.transpose(1, 2).reshape(slots_n, C, *SHAPE)          # the reference's [n, C, Y, Z, X]
+        permuted = out.class_major()                # the reference's permuted copy: contiguous class planes
         got_b = consume_batch(b, permuted, tokens_b, slots_n)
         assert sorted(got_a) == sorted(got_b), step
         for i in got_a:

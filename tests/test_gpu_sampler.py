@@ -168,8 +168,9 @@ def test_graph_replays_equal_eager_draws(dev):
 
 
 def test_philox_slot_window_eager_equals_graph_and_oracle_draws(dev):
-    """A whole window on the 'philox' sampler: the per-slot eager `consume` and the graph-staged batch (selection
-    and sampling captured together through SelectGraphs) commit the same positions and values at every step, every
+    """A whole window on the 'philox' sampler: the per-slot eager `consume` over voxel-row views and the graph-staged
+    batch over class planes (selection and sampling captured together through SelectGraphs) commit the same
+    positions and values at every step, every
     step commits exactly its quota, and the committed values are the oracle's counter-based draws on that step's
     logits."""
     from streamvoxel_amd.stream.slot import LowEntropyLastSlot, SelectGraphs, consume_batch
@@ -191,7 +192,11 @@ def test_philox_slot_window_eager_equals_graph_and_oracle_draws(dev):
     N = SHAPE[0] * SHAPE[1] * SHAPE[2]
     for step in range(CAP + 1):
         out[0].copy_(marking_logits(3, dev) if step == 0 else solid_logits(50 + step, step, CAP + 1, dev))
-        r_e, c_e = eager.consume(out[0], tok_e)
+        # the eager slot reads the same logits as a view of voxel rows (class stride 1), the staged ones the class
+        # planes: the scores, selections and draws do not depend on the layout
+        rows_view = out[0].permute(1, 2, 3, 0).contiguous().permute(3, 0, 1, 2)
+        assert rows_view.stride(0) == 1
+        r_e, c_e = eager.consume(rows_view, tok_e)
         got = consume_batch(staged, out, engine.tokens, 2, graphs)
         r_s, c_s = got.get(0, (None, None))
         _compare_commit(c_e, c_s, f'step={step}')

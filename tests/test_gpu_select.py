@@ -319,3 +319,72 @@ def test_quota_select_window_trajectories_trim_and_top_up(dev):
         assert np.array_equal(res.cpu().numpy(), expect), (seed, step, d)
     print('trajectory correction cases', seen, flush=True)
     assert seen['trim_small'] > 0 and seen['topup_small'] > 0 and seen['large'] > 0, seen
+
+
+@pytest.mark.parametrize('dtype,classes', [(torch.float32, 256), (torch.bfloat16, 304), (torch.float32, 64),
+                                           (torch.bfloat16, 48), (torch.float32, 384)])
+def test_scores_are_bit_identical_in_every_layout(dev, dtype, classes):
+    """Entropy and air probability of the same logits from voxel rows, contiguous class planes (what the reference's
+    permute leaves), a voxel-row view, a strided class-plane view and the class head's patch order: one per-voxel
+    order, the same bits."""
+    from streamvoxel_amd.sampling.entropy import air_prob, entropy_batched, entropy_scores
+    from streamvoxel_amd.stream.patches import PatchLogits
+    B, shape = 2, (32, 16, 16)
+    N = 32 * 16 * 16
+    _case(f'layout-independent scores {dtype} C={classes}')
+    rows = torch.stack([bimodal_logits(N, classes, seed=40 + i, dtype=dtype) for i in range(B)]).to(dev)  # [B,N,C]
+    planes = rows.transpose(1, 2).contiguous()                                                  # [B,C,N]
+    view = rows.transpose(1, 2)                                                                 # class stride 1
+    wide = torch.zeros(B, classes, N + 64, dtype=dtype, device=dev)
+    wide[:, :, :N] = planes
+    strided = wide[:, :, :N]                                                                    # row stride N + 64
+    odd = torch.zeros(B, classes, N + 1, dtype=dtype, device=dev)
+    odd[:, :, :N] = planes
+    unaligned = odd[:, :, :N]                               # class rows not 16-byte aligned: scalar tile loads
+    want = entropy_batched(rows, layout='voxel_major')
+    for x in (planes, view, strided, unaligned):
+        assert torch.equal(entropy_batched(x, layout='class_major'), want)
+    pl = PatchLogits(torch.empty(B, N // 64, 64 * classes, dtype=dtype, device=dev), shape, 4, classes)
+    pl.rows[:, pl.row_index(torch.arange(N, device=dev))] = rows
+    assert torch.equal(entropy_scores(pl).reshape(B, N), want)
+    air = torch.tensor([0, 3, classes - 1], dtype=torch.int32, device=dev)
+    a_rows = torch.stack([air_prob(rows[i].t().reshape(classes, *shape), air) for i in range(B)])
+    a_planes = torch.stack([air_prob(planes[i].reshape(classes, *shape), air) for i in range(B)])
+    torch.cuda.synchronize()
+    assert torch.equal(a_rows, a_planes)
+    err = (want.double().cpu() - torch.as_tensor(np.stack([S.entropy_scores_f64(rows[i].float().cpu().numpy().T)
+                                                             for i in range(B)]))).abs().max().item()
+    assert err < ENTROPY_ATOL, err
+
+
+def test_ease_select_bit_identical_from_class_planes_and_voxel_rows(dev):
+    """The fused selection from contiguous class planes and from voxel rows of the same logits: the same scores,
+    the same chosen voxels (mid-window state with deferred voxels and committed tokens)."""
+    from streamvoxel_amd import _lib
+    from streamvoxel_amd.stream.step import EaseSelect
+    g = np.random.default_rng(5)
+    B, shape, C = 3, (256, 16, 16), 256
+    N = 256 * 16 * 16
+    _case('ease_select class planes vs voxel rows')
+    rows = torch.stack([bimodal_logits(N, C, seed=70 + i) for i in range(B)]).to(dev)
+    planes = rows.transpose(1, 2).contiguous()
+    sels = []
+    for x in (rows, planes):
+        sel = EaseSelect(B, shape, C, 4, dev)
+        for i in range(B):
+            rng = np.random.default_rng(i)
+            tops = rng.integers(128, 257, (16, 16))
+            last = torch.from_numpy((np.arange(256)[:, None, None] >= tops[None]).reshape(-1)).to(dev)
+            sel.last[i].copy_(last)
+            done = torch.from_numpy(rng.random(N) < 0.2).to(dev) & ~last
+            sel.tokens[i][done] = 1
+            sel.bind_window(i, torch.from_numpy(rng.permutation(1024)).to(dev))
+            k = 2000 - 300 * i
+            committed = int(done.sum())
+            sel.set_step(i, k, committed, (committed + k) / int((~last).sum()))
+        sel.run(x, keep_scores=True)
+        sels.append(sel)
+    torch.cuda.synchronize()
+    assert torch.equal(sels[0].scores.view(torch.int32), sels[1].scores.view(torch.int32))
+    assert torch.equal(sels[0].chosen, sels[1].chosen)
+    assert not bool(sels[0].bad.any())
