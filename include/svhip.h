@@ -296,7 +296,8 @@ int svhip_patch_embed(const int64_t* tokens, const void* table, const void* bias
  * class of every chosen voxel, other entries untouched. seed, step: device int64 [batch]. Voxel v of window b draws
  * u = (floor(w0 / 2^41) + 1/2) / 2^23 from Philox4x64-10 at counter (v, step[b], 0, 0) under key
  * (seed[b], 0x53414D504C455631) and takes the first class whose softmax CDF passes u (fp32 sums). A chosen row with
- * no finite maximum or a NaN sets *err (device int). classes <= 1024.
+ * no finite maximum or a NaN sets *err (device int) and draws nothing: its value reads -1 and its token is left as
+ * it was. classes <= 1024.
  * Replaces (as a counter-based alternative with its own random stream): the tail of
  * FastLowEntropyLastSlot.stage (streamvoxel/stream/fast_ops.py:548-553: nonzero_static -> gather -> softmax ->
  * torch.multinomial -> index_copy_), whose sizes depend on the step's k.

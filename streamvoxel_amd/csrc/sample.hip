@@ -128,8 +128,9 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
     const float u = (static_cast<float>(w0 >> 41) + 0.5f) * (1.0f / 8388608.0f);
     int cls;
     if (!(mx > -INFINITY && mx < INFINITY) || !(total > 0.f && total < INFINITY)) {
+      // No class is drawn (the reference's multinomial raises here): the voxel keeps its token and reads -1.
       if (lane == 0) atomicOr(a.err, 1);
-      cls = 0;
+      cls = -1;
     } else {
       const float target = u * total;
       const uint64_t past = __ballot(incl > target);
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
   }
   if (in) {
     a.values[b * a.N + v] = static_cast<int16_t>(ch ? mine : -1);
-    if (ch && a.tokens) a.tokens[b * a.N + v] = mine;
+    if (ch && mine >= 0 && a.tokens) a.tokens[b * a.N + v] = mine;
   }
 }
 

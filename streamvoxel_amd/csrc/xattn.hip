@@ -17,11 +17,12 @@
 // Because O^T's columns are queries too, the per-query rescale and the final 1/l are lane-local.
 //
 // The softmax is VALU-bound at head_dim 64 (one exp per score against 2 x 64 MACs), so per score it costs one
-// exp, half a bf16 pack and one fp32 add (the row sum; v_dot2c_f32_bf16 over the packed P would need half the
-// instructions but does not co-execute with the matrix cores), and no scaling, subtraction or max:
-//   * Q is loaded once, multiplied by scale * log2(e) (and the e4m3 K scale) and rounded to bf16, so the scores
-//     come out in log2 units; the first MFMA of every score chain takes -m (16 registers holding the running
-//     max, negated) as its C operand, so the accumulators hold S - m and P = exp2(S^T) directly.
+// multiply, one exp, half a bf16 pack and one fp32 add (the row sum; v_dot2c_f32_bf16 over the packed P would need
+// half the instructions but does not co-execute with the matrix cores), and no subtraction or max:
+//   * Q enters the score product as given (bf16); the scores are scaled in fp32 by sl2 = scale * log2(e) (and the
+//     e4m3 K scale), so that the only roundings of the query are the caller's. The first MFMA of every score chain
+//     takes -m / sl2 (16 registers holding the running max m in log2 units, negated and unscaled) as its C
+//     operand, so the accumulators hold S - m / sl2 and P = exp2(sl2 * S^T) directly.
 //   * P is formed against the running max m as it stands. The half's row sum tells whether m still bounds the
 //     half's scores: only a sum above 2^20 (and always the window's first half) makes the wave take the half's
 //     max (16 three-input maxes and the partner's over v_permlane32_swap), raise m, rescale O and l and redo P
@@ -386,7 +387,7 @@ enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2 };
 // bf16 direct-staged ones fit by themselves.
 // KMASK: a key mask (p.kv_mask) on top of the window length; every block then masks its keys.
 template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false>
-__global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
+__global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kRegister)) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
   constexpr bool DIRECT = STAGING != kRegister;
   static_assert(!KMASK || !DIRECT, "the key-mask path stages through registers");
   static_assert(!ONES || STAGING != kDirectFull, "a full-width head has no padding row");
@@ -456,7 +457,9 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
     kscale = p.k_scale[b * p.H + h];
     vscale = p.v_scale[b * p.H + h];
   }
-  const float sl2 = p.scale_log2 * kscale;
+  const float sl2 = p.scale_log2 * kscale;   // scores -> log2 units
+  const float inv_sl2 = 1.f / sl2;
+  const float max_high_acc = kMaxHigh * inv_sl2;   // kMaxHigh in accumulator units
 
   if (L == 0) {
     if (q_ok) {
@@ -472,11 +475,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
     const int d0 = 16 * s + 8 * hh;
     uint4 raw = make_uint4(0u, 0u, 0u, 0u);
     if (q_ok && d0 < p.D) raw = *reinterpret_cast<const uint4*>(Qp + q * p.sq_q + d0);
-    // Q pre-scaled by scale * log2(e) (and the e4m3 K scale), rounded to bf16: the scores come out in log2 units.
-    const bf16x8_t qb = __builtin_bit_cast(bf16x8_t, raw);
-    typedef float f32x8_t __attribute__((ext_vector_type(8)));
-    const f32x8_t qs = __builtin_convertvector(qb, f32x8_t) * sl2;
-    qf[s] = __builtin_convertvector(qs, bf16x8_t);
+    qf[s] = __builtin_bit_cast(bf16x8_t, raw);
   }
 
   using T = typename Elem<FP8>::T;
@@ -526,7 +525,8 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
   for (int j = 0; j < DT; ++j) o[j] = f32x16_t{0};
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
   float l = 0.f;                // row-sum partial of this lane's keys
-  // The score accumulators start at -mc (the MFMA's C operand), so they hold S - mc; mc = m after the first half.
+  // The score accumulators start at -mc / sl2 (the MFMA's C operand), so they hold S - mc / sl2; mc = m after the
+  // first half.
   float mc = 0.f;
   f32x16_t negm = {0};
   bool first = true;            // uniform: the window's first half always takes the max
@@ -597,8 +597,9 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
           if (KMASK && !((mine >> i) & 1u)) s[i] = -INFINITY;
         }
       }
-      // P^T = exp2(S^T - m) against the running max m as it stands (the accumulators already hold S - mc, mc = m
-      // after the first half), as B operands: k-step ks (keys 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7.
+      // P^T = exp2(sl2 S^T - m) against the running max m as it stands (the accumulators already hold S - mc / sl2,
+      // mc = m after the first half), as B operands: k-step ks (keys 32 t + 16 ks + 8 hh + 0..7) = entries
+      // 8 ks + 0..7.
       // The row sum is taken over the fp32 P (unless the matrix cores form it).
       bf16x8_t pb[2];
       float lb;
@@ -609,8 +610,9 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
           for (int j = 0; j < 8; j += 2) {
-            f32x2_t two = {__builtin_amdgcn_exp2f(SHIFT ? s[8 * ks + j] - d : s[8 * ks + j]),
-                           __builtin_amdgcn_exp2f(SHIFT ? s[8 * ks + j + 1] - d : s[8 * ks + j + 1])};
+            f32x2_t two = {__builtin_amdgcn_exp2f(SHIFT ? __builtin_fmaf(s[8 * ks + j], sl2, -d) : s[8 * ks + j] * sl2),
+                           __builtin_amdgcn_exp2f(SHIFT ? __builtin_fmaf(s[8 * ks + j + 1], sl2, -d)
+                                                        : s[8 * ks + j + 1] * sl2)};
             const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
             pair[4 * ks + j / 2] = two[0] + two[1];
             pb[ks][j] = c[0];
@@ -621,18 +623,18 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
         // co-execute with the matrix cores on gfx950).
         lb = ((pair[0] + pair[1]) + (pair[2] + pair[3])) + ((pair[4] + pair[5]) + (pair[6] + pair[7]));
       };
-      // The slow path: the half's max (S - mc; the chain opens with a compiler-visible v_med3_f32, med3(a, b,
+      // The slow path: the half's max (S - mc / sl2, accumulator units; the chain opens with a compiler-visible v_med3_f32, med3(a, b,
       // FLT_MAX) = max(a, b) for scores below +inf, before which the compiler inserts the wait states a VALU read
       // of an MFMA result needs; the inline v_max3_f32 that follow, which the compiler does not check for that
       // hazard, read the same, by then complete, accumulator) joined with the partner lane's over
       // v_permlane32_swap, which gives (x[l % 32], x[l % 32 + 32]) in every lane; m raised to it, O and l
-      // rescaled, P redone shifted by the rise, the C operand moved to -m. Every query has a key below L in the
-      // first half, so m is finite after it.
+      // rescaled, P redone shifted by the rise, the C operand moved to -m / sl2. Every query has a key below L in
+      // the first half, so m is finite after it.
       auto raise = [&](float mx) __attribute__((always_inline)) {
         first = false;
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
         const float mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
-        const float cand = mr + mc;
+        const float cand = __builtin_fmaf(mr, sl2, mc);
         float mn = cand > m ? cand : m;
         // Only with a key mask can a query have seen no attended key yet (every score -inf): its running max is
         // then set to 0, with O and l still 0, so that later scores are taken against a finite bias.
@@ -648,7 +650,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
         exps(std::true_type{}, mn - mc);
         mc = mn;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) negm[i] = -mn;
+        for (int i = 0; i < 16; ++i) negm[i] = -mn * inv_sl2;
       };
       auto half_max = [&]() __attribute__((always_inline)) {
         float mx = __builtin_amdgcn_fmed3f(s[0], s[1], kFltMax);
@@ -661,7 +663,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && FP8) ? 3 : 2) void xatt
         // below 2^kMaxHigh); the row sum accumulates in O^T row D.
         const float mx = half_max();
         exps(std::false_type{}, 0.f);
-        if (first || __builtin_amdgcn_ballot_w64(mx > kMaxHigh) != 0ull) raise(mx);
+        if (first || __builtin_amdgcn_ballot_w64(mx > max_high_acc) != 0ull) raise(mx);
       } else {
         // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN) some
         // score passed m by about 20 (log2 units). Only then (and on the window's first half, where m is -inf)

@@ -126,8 +126,13 @@ def test_non_finite_rows_set_the_error_flag(dev):
         sample_chosen(logits, chosen, seeds, steps, values, err)       # the bad voxel not chosen: no error
         assert int(err) == 0
         chosen[1, 2, 3] = True
-        sample_chosen(logits, chosen, seeds, steps, values, err)
+        chosen[0, 0, 0] = True
+        tokens = torch.full(shape, C, dtype=torch.int64, device=dev)
+        sample_chosen(logits, chosen, seeds, steps, values, err, tokens)
         assert int(err) != 0, bad
+        # the bad row draws nothing: its token stays the mask token and its value reads -1; the good one is drawn
+        assert int(tokens[1, 2, 3]) == C and int(values.view(shape)[1, 2, 3]) == -1, bad
+        assert 0 <= int(tokens[0, 0, 0]) < C and int(values.view(shape)[0, 0, 0]) == int(tokens[0, 0, 0])
         # A -inf class among finite ones is a zero-probability class, not an error.
     logits = torch.randn(C, *shape, device=dev)
     logits[:5] = float('-inf')
