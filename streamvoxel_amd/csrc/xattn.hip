@@ -17,12 +17,11 @@
 // Because O^T's columns are queries too, the per-query rescale and the final 1/l are lane-local.
 //
 // The softmax is VALU-bound at head_dim 64 (one exp per score against 2 x 64 MACs), so per score it costs one
-// multiply, one exp, half a bf16 pack and one fp32 add (the row sum; v_dot2c_f32_bf16 over the packed P would need
-// half the instructions but does not co-execute with the matrix cores), and no subtraction or max:
-//   * Q enters the score product as given (bf16); the scores are scaled in fp32 by sl2 = scale * log2(e) (and the
-//     e4m3 K scale), so that the only roundings of the query are the caller's. The first MFMA of every score chain
-//     takes -m / sl2 (16 registers holding the running max m in log2 units, negated and unscaled) as its C
-//     operand, so the accumulators hold S - m / sl2 and P = exp2(sl2 * S^T) directly.
+// FMA, one exp, half a bf16 pack and one fp32 add (the row sum; v_dot2c_f32_bf16 over the packed P would need half
+// the instructions but does not co-execute with the matrix cores), and no max:
+//   * Q enters the score product as given (bf16) and the fp32 scores are scaled by sl2 = scale * log2(e) (and the
+//     e4m3 K scale) inside the exponent's FMA, P = exp2(fma(S, sl2, -m)) with m the running max in log2 units, so
+//     the only roundings of the query are the caller's.
 //   * P is formed against the running max m as it stands. The half's row sum tells whether m still bounds the
 //     half's scores: only a sum above 2^20 (and always the window's first half) makes the wave take the half's
 //     max (16 three-input maxes and the partner's over v_permlane32_swap), raise m, rescale O and l and redo P
@@ -458,8 +457,6 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
     vscale = p.v_scale[b * p.H + h];
   }
   const float sl2 = p.scale_log2 * kscale;   // scores -> log2 units
-  const float inv_sl2 = 1.f / sl2;
-  const float max_high_acc = kMaxHigh * inv_sl2;   // kMaxHigh in accumulator units
 
   if (L == 0) {
     if (q_ok) {
@@ -525,10 +522,6 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
   for (int j = 0; j < DT; ++j) o[j] = f32x16_t{0};
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
   float l = 0.f;                // row-sum partial of this lane's keys
-  // The score accumulators start at -mc / sl2 (the MFMA's C operand), so they hold S - mc / sl2; mc = m after the
-  // first half.
-  float mc = 0.f;
-  f32x16_t negm = {0};
   bool first = true;            // uniform: the window's first half always takes the max
 
   // Full block `blk` into (sK, sV): issued now, complete at the next vmem wait (direct) or at `stage_commit`
@@ -583,7 +576,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
         if (k == 0 || k < ksteps) {
           const bf16x8_t a =
               *reinterpret_cast<const bf16x8_t*>(kp + (k >> 2) * (kKTile * 2) + rd[k & 3] + t * (32 * kRow * 2));
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], k == 0 ? negm : s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], k == 0 ? f32x16_t{0} : s, 0, 0, 0);
         }
       }
       if constexpr (MASKED || KMASK) {
@@ -597,22 +590,21 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
           if (KMASK && !((mine >> i) & 1u)) s[i] = -INFINITY;
         }
       }
-      // P^T = exp2(sl2 S^T - m) against the running max m as it stands (the accumulators already hold S - mc / sl2,
-      // mc = m after the first half), as B operands: k-step ks (keys 32 t + 16 ks + 8 hh + 0..7) = entries
-      // 8 ks + 0..7.
+      // P^T = exp2(sl2 S^T - m) against the running max m as it stands, as B operands: k-step ks (keys
+      // 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7. On the window's first half m is -inf and the fast pass
+      // gives inf or NaN, which the slow path always taken there replaces.
       // The row sum is taken over the fp32 P (unless the matrix cores form it).
       bf16x8_t pb[2];
       float lb;
-      auto exps = [&](auto shifted, float d) __attribute__((always_inline)) {
-        constexpr bool SHIFT = decltype(shifted)::value;
+      auto exps = [&]() __attribute__((always_inline)) {
+        const float nm = -m;
         float pair[8];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
           for (int j = 0; j < 8; j += 2) {
-            f32x2_t two = {__builtin_amdgcn_exp2f(SHIFT ? __builtin_fmaf(s[8 * ks + j], sl2, -d) : s[8 * ks + j] * sl2),
-                           __builtin_amdgcn_exp2f(SHIFT ? __builtin_fmaf(s[8 * ks + j + 1], sl2, -d)
-                                                        : s[8 * ks + j + 1] * sl2)};
+            f32x2_t two = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j], sl2, nm)),
+                           __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j + 1], sl2, nm))};
             const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
             pair[4 * ks + j / 2] = two[0] + two[1];
             pb[ks][j] = c[0];
@@ -623,18 +615,18 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
         // co-execute with the matrix cores on gfx950).
         lb = ((pair[0] + pair[1]) + (pair[2] + pair[3])) + ((pair[4] + pair[5]) + (pair[6] + pair[7]));
       };
-      // The slow path: the half's max (S - mc / sl2, accumulator units; the chain opens with a compiler-visible v_med3_f32, med3(a, b,
+      // The slow path: the half's max (raw scores; the chain opens with a compiler-visible v_med3_f32, med3(a, b,
       // FLT_MAX) = max(a, b) for scores below +inf, before which the compiler inserts the wait states a VALU read
       // of an MFMA result needs; the inline v_max3_f32 that follow, which the compiler does not check for that
       // hazard, read the same, by then complete, accumulator) joined with the partner lane's over
-      // v_permlane32_swap, which gives (x[l % 32], x[l % 32 + 32]) in every lane; m raised to it, O and l
-      // rescaled, P redone shifted by the rise, the C operand moved to -m / sl2. Every query has a key below L in
-      // the first half, so m is finite after it.
+      // v_permlane32_swap, which gives (x[l % 32], x[l % 32 + 32]) in every lane, scaled to log2 units; m raised to
+      // it, O and l rescaled, P redone against the new m. Every query has a key below L in the first half, so m is
+      // finite after it.
       auto raise = [&](float mx) __attribute__((always_inline)) {
         first = false;
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
         const float mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
-        const float cand = __builtin_fmaf(mr, sl2, mc);
+        const float cand = mr * sl2;
         float mn = cand > m ? cand : m;
         // Only with a key mask can a query have seen no attended key yet (every score -inf): its running max is
         // then set to 0, with O and l still 0, so that later scores are taken against a finite bias.
@@ -647,10 +639,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
 #pragma unroll
           for (int j = 0; j < DT; ++j) o[j][i] *= alpha;
         }
-        exps(std::true_type{}, mn - mc);
-        mc = mn;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) negm[i] = -mn * inv_sl2;
+        exps();
       };
       auto half_max = [&]() __attribute__((always_inline)) {
         float mx = __builtin_amdgcn_fmed3f(s[0], s[1], kFltMax);
@@ -662,13 +651,13 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
         // The half's own max decides: a score more than kMaxHigh above m raises it (P of the fast path stays
         // below 2^kMaxHigh); the row sum accumulates in O^T row D.
         const float mx = half_max();
-        exps(std::false_type{}, 0.f);
-        if (first || __builtin_amdgcn_ballot_w64(mx > max_high_acc) != 0ull) raise(mx);
+        exps();
+        if (first || __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, sl2, -m) > kMaxHigh) != 0ull) raise(mx);
       } else {
         // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN) some
         // score passed m by about 20 (log2 units). Only then (and on the window's first half, where m is -inf)
         // is the slow path taken.
-        exps(std::false_type{}, 0.f);
+        exps();
         if (first || __builtin_amdgcn_ballot_w64(!(lb <= kSumHigh)) != 0ull) raise(half_max());
         l += lb;
       }
