@@ -23,7 +23,8 @@
 extern "C" {
 #endif
 
-enum svhip_dtype { SVHIP_F32 = 0, SVHIP_BF16 = 1, SVHIP_FP8_E4M3 = 3 };
+/* SVHIP_FP8_E4M3_PBF16: e4m3 K/V whose attention keeps P in bf16 (see svhip_xattn_fwd). */
+enum svhip_dtype { SVHIP_F32 = 0, SVHIP_BF16 = 1, SVHIP_FP8_E4M3 = 3, SVHIP_FP8_E4M3_PBF16 = 4 };
 
 enum svhip_status { SVHIP_OK = 0, SVHIP_EINVAL = -1, SVHIP_ELAUNCH = -2, SVHIP_EWORKSPACE = -3 };
 
@@ -161,9 +162,12 @@ int svhip_ease_select_patches(const void* logits, int dtype, int64_t classes, in
  * b*sk_b + h*sk_h + row*sk_k + d; V: at b*sv_b + h*sv_h + row*sv_k + d*sv_d, where either sv_d == 1 (rows of
  * head_dim, the reference layout) or sv_k == 1 (V stored transposed, keys contiguous: the fast staging path);
  * row = j, or cu_seqlens[b] + j in the packed layout (sk_b / sv_b are then ignored). kv_dtype SVHIP_BF16, or
- * SVHIP_FP8_E4M3 (OCP e4m3fn bytes) with per-(window, head) fp32 dequantisation scales k_scale/v_scale [B,H].
- * head_dim: a multiple of 8 up to 128 (zero-padded inside the kernel to 64, 96 or 128: the 384-wide model's 48,
- * the 768-wide model's 96). fp32 accumulation.
+ * e4m3 (OCP e4m3fn bytes) with per-(window, head) fp32 dequantisation scales k_scale/v_scale [B,H]:
+ * SVHIP_FP8_E4M3 takes P . V on the fp8 matrix cores with P rounded to e4m3 (relative rounding 2^-4 on every
+ * softmax weight, the row sum taken over the rounded weights), SVHIP_FP8_E4M3_PBF16 keeps P in bf16 on the bf16
+ * matrix cores (the reference's in-kernel dequantisation). Q . K^T is a bf16 product of the exactly decoded keys
+ * in both. head_dim: a multiple of 8 up to 128 (zero-padded inside the kernel to 64, 96 or 128: the 384-wide
+ * model's 48, the 768-wide model's 96). fp32 accumulation.
  * scale: the softmax scale, > 0 (the reference uses 1/sqrt(head_dim)).
  * Replaces: flex_attention over PackedKeys' block mask in cross_flex (streamvoxel/stream/fast_ops.py:104-108,
  * 122-159) and the masked SDPA in SlotCrossAttention.forward / cross_sdpa (streamvoxel/stream/engine.py:28-47,

@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, 'libsvhip.so')
 
-SVHIP_F32, SVHIP_BF16, SVHIP_FP8_E4M3 = 0, 1, 3
+SVHIP_F32, SVHIP_BF16, SVHIP_FP8_E4M3, SVHIP_FP8_E4M3_PBF16 = 0, 1, 3, 4
 SVHIP_LEL_LAYER, SVHIP_LEL_BAND, SVHIP_LEL_COLUMN = 0, 1, 2
 
 _c_i64, _c_i32, _c_p, _c_sz, _c_f, _c_d = (ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t,

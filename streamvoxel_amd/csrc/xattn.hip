@@ -32,6 +32,15 @@
 //     trigger becomes the half's own max (8 three-input maxes): a score more than 20 above m.
 //   * key masking runs only in the last, partial block; padding keys are staged as zeros.
 //
+// e4m3 K/V (PV8, the default for an e4m3 cache): the second product runs on the fp8 matrix cores,
+// v_mfma_f32_32x32x64_f8f6f4 over a whole 64-key block per output tile (half the bf16 product's matrix-core time).
+// V^T stays e4m3 in LDS (its per-head scale applied at the end); P is formed 2^4 above the running max and rounded
+// to e4m3 as it is packed, a lane's 32 weights being exactly the B operand's 32 k slots (K rows are placed by
+// pv8_row for that); the row sum is taken over the rounded weights (decoded, or from the ones row), so a dominant
+// key's rounding cancels in O / l. The score product stays bf16 over the exactly decoded keys. The price is a 2^-4
+// relative rounding of every softmax weight; SVHIP_FP8_E4M3_PBF16 keeps P in bf16 (PV8 off) for the reference's
+// numerics.
+//
 // Staging. An LDS tile holds 64 rows of 128 bytes, the eight 16-byte chunks of row r XOR-swizzled by (r / 2) % 8
 // so that the 16-byte operand reads are bank-conflict-free; a K row is one key's head_dim, a V^T row one
 // head_dim element's 64 keys. bf16 K and V^T of the padded [B,H,Kcap,*] layout with 16-byte aligned rows take
@@ -62,6 +71,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kQTile = 128;   // queries per workgroup
 constexpr int kKB = 64;       // keys per block
@@ -73,6 +83,12 @@ constexpr int kThreads = 256;
 constexpr float kSumHigh = 1048576.0f;  // 2^20: a half's row sum above it makes the running max be raised
 constexpr float kMaxHigh = 20.0f;       // the same bound on a single score above the running max (log2 units)
 constexpr float kFltMax = 3.40282347e38f;
+// e4m3 second product: P is formed 2^4 above the running max and packed only while it stays below 448, the
+// largest e4m3 value: a half's lane sum of its e4m3 P of 448 or more (or, with the ones row, a score more than
+// 4.8 above the running max, 2^8.8 < 448) raises the max first.
+constexpr float kPv8Lift = 4.0f;
+constexpr float kPv8SumHigh = 448.0f;
+constexpr float kPv8MaxHigh = 4.8f;  // 2^(4 + 4.8) = 445.7 <= 448
 // Windows are ranked by length inside every workgroup (each thread compares its candidates against all windows);
 // beyond this many windows that quadratic cost is not worth the balance and the grid keeps the window order.
 constexpr int kMaxRankWindows = 256;
@@ -110,6 +126,19 @@ __device__ __forceinline__ int sigma_row(int key) {
   const int swapped = (g == 1) ? y + 4 : (g == 2 ? y - 4 : y);
   return (key & ~15) | swapped;
 }
+
+// e4m3 second product (PV8): row of key `key` (0..63) of a block inside the LDS K tile. Key bits
+// [hh t a1 a0 b1 b0] go to row bits [t a1 a0 hh b1 b0], so that score entry i of half t in lane half hh is key
+// 32 hh + 16 t + i: a lane's 32 P values are then the 32 consecutive keys that byte j of its B operand of
+// v_mfma_f32_32x32x64_f8f6f4 pairs with in the A operand (keys 32 hh + j of a V^T row in natural order).
+__device__ __forceinline__ int pv8_row(int key) {
+  return (((key >> 4) & 1) << 5) | (((key >> 2) & 3) << 3) | ((key >> 5) << 2) | (key & 3);
+}
+
+// The e4m3 V^T tile of PV8: rows of 64 bytes (one head_dim element's 64 keys), the four 16-byte chunks of row r
+// XOR-swizzled by (r / 4) % 4, so that 16 consecutive rows read at one logical chunk hit 16 distinct bank groups.
+constexpr int kRow8 = 64;
+__device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 2) & 3); }
 
 // 8 OCP e4m3fn bytes (two dwords) -> 8 bf16 packed in a uint4 (exact: every e4m3 value is a bf16 value).
 __device__ __forceinline__ uint4 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
@@ -221,7 +250,21 @@ __device__ __forceinline__ typename Raw<FP8>::type raw_one_first() {
   }
 }
 
+template <bool FP8>
+__device__ __forceinline__ typename Raw<FP8>::type raw_select(bool keep, const typename Raw<FP8>::type& v,
+                                                             const typename Raw<FP8>::type& other) {
+  if constexpr (FP8) {
+    return make_uint2(keep ? v.x : other.x, keep ? v.y : other.y);
+  } else {
+    return make_uint4(keep ? v.x : other.x, keep ? v.y : other.y, keep ? v.z : other.z, keep ? v.w : other.w);
+  }
+}
+
 // ONES: V^T row D (the first padding row) is staged as ones, so that the second product forms the row sum.
+// A full block (TAIL false) issues every load without a branch, lanes outside head_dim reading the window's first
+// row instead: a load under a per-lane condition makes the compiler merge its result with the other arm's value
+// right away, which waits for the load and exposes its latency in the prefetch. stage_store then puts zeros (and
+// the ones row) where head_dim ends. The partial block masks its loads (keys >= L read nothing).
 template <bool FP8, bool VT, int DT, bool TAIL, bool ONES = false>
 __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnParams& p,
                                            const typename Elem<FP8>::T* K, const typename Elem<FP8>::T* V, int L,
@@ -231,11 +274,14 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnPa
     const int c = threadIdx.x + kThreads * (r & 1);  // 0..511
     const int key = c >> 3, dc = 8 * (r >> 1) + (c & 7);
     const int kg = kv0 + key;
-    const bool ok = dc < dchunks && (!TAIL || kg < L);
-    st.k[r] = ok ? load8_vec<FP8>(K + kg * p.sk_k + dc * 8) : raw_zero<FP8>();
-    if constexpr (!VT) {
-      st.v[r] = ok ? load8_vec<FP8>(V + kg * p.sv_k + dc * 8)
-                   : ((ONES && dc == dchunks) ? raw_one_first<FP8>() : raw_zero<FP8>());
+    if constexpr (TAIL) {
+      const bool ok = dc < dchunks && kg < L;
+      st.k[r] = ok ? load8_vec<FP8>(K + kg * p.sk_k + dc * 8) : raw_zero<FP8>();
+      if constexpr (!VT) st.v[r] = ok ? load8_vec<FP8>(V + kg * p.sv_k + dc * 8) : raw_zero<FP8>();
+    } else {
+      const bool ok = dc < dchunks;
+      st.k[r] = load8_vec<FP8>(K + (ok ? static_cast<int64_t>(kg) * p.sk_k + dc * 8 : 0));
+      if constexpr (!VT) st.v[r] = load8_vec<FP8>(V + (ok ? static_cast<int64_t>(kg) * p.sv_k + dc * 8 : 0));
     }
   }
   if constexpr (VT) {
@@ -244,34 +290,58 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnPa
       const int c = threadIdx.x + kThreads * r;
       const int d = c >> 3, kc = c & 7;
       const int kg = kv0 + kc * 8;
-      const auto* src = V + d * p.sv_d + kg;
-      if (d < p.D && (!TAIL || kg < L)) {
+      if (!TAIL && vt_vec) {
+        st.v[r] = load8_vec<FP8>(V + (d < p.D ? d * p.sv_d : 0) + kg);
+      } else if (d < p.D && (!TAIL || kg < L)) {
         const int valid = TAIL ? ((L - kg) < 8 ? (L - kg) : 8) : 8;
+        const auto* src = V + d * p.sv_d + kg;
         st.v[r] = (vt_vec && valid == 8) ? load8_vec<FP8>(src) : load8_scalar<FP8>(src, valid);
       } else {
-        st.v[r] = (ONES && d == p.D) ? raw_one<FP8>() : raw_zero<FP8>();
+        st.v[r] = raw_zero<FP8>();
       }
     }
   }
 }
 
-// Registers -> LDS (K rows under sigma in their sub-tile; V as V^T [d][key]; both swizzled).
-template <bool FP8, bool VT, int DT>
-__device__ __forceinline__ void stage_store(const Stage<FP8, VT, DT>& st, uint16_t* sK, uint16_t* sV) {
+// Registers -> LDS (K rows under sigma in their sub-tile; V as V^T [d][key]; both swizzled), with zeros past
+// head_dim and, with ONES, the ones row D. PV8: K rows under pv8_row, V^T kept in e4m3 in its own tile (keys in
+// natural order).
+template <bool FP8, bool VT, int DT, bool ONES, bool PV8 = false>
+__device__ __forceinline__ void stage_store(const Stage<FP8, VT, DT>& st, uint16_t* sK, uint16_t* sV, int dchunks,
+                                            int D) {
+  static_assert(!PV8 || FP8, "the e4m3 second product takes e4m3 V");
+  using R8 = typename Raw<FP8>::type;
 #pragma unroll
   for (int r = 0; r < Width<DT>::kKPasses; ++r) {
     const int c = threadIdx.x + kThreads * (r & 1);
-    const int R = sigma_row(c >> 3), dc = c & 7;
-    *reinterpret_cast<uint4*>(sK + (r >> 1) * kKTile + R * kRow + swz(R, dc) * 8) = to_bf16x8<FP8>(st.k[r]);
+    const int R = PV8 ? pv8_row(c >> 3) : sigma_row(c >> 3), dc = c & 7;
+    const bool ok = 8 * (r >> 1) + dc < dchunks;
+    *reinterpret_cast<uint4*>(sK + (r >> 1) * kKTile + R * kRow + swz(R, dc) * 8) =
+        to_bf16x8<FP8>(raw_select<FP8>(ok, st.k[r], raw_zero<FP8>()));
     if constexpr (!VT) {
+      const R8 pad = (ONES && 8 * (r >> 1) + dc == dchunks) ? raw_one_first<FP8>() : raw_zero<FP8>();
+      const R8 vv = raw_select<FP8>(ok, st.v[r], pad);
       const int key = c >> 3;
-      const uint4 vb = to_bf16x8<FP8>(st.v[r]);
-      const uint32_t w[4] = {vb.x, vb.y, vb.z, vb.w};
+      if constexpr (PV8) {
+        // Row-major V transposed byte by byte: key c / 8, head_dim 64 (r / 2) + 8 dc + e.
+        uint8_t* sV8 = reinterpret_cast<uint8_t*>(sV);
+        const uint32_t w[2] = {vv.x, vv.y};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = kSub * (r >> 1) + dc * 8 + e;
-        if (d < 32 * DT) {
-          sV[d * kRow + swz(d, key >> 3) * 8 + (key & 7)] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+        for (int e = 0; e < 8; ++e) {
+          const int d = kSub * (r >> 1) + dc * 8 + e;
+          if (d < 32 * DT) {
+            sV8[d * kRow8 + swz8(d, key >> 4) * 16 + (key & 15)] = static_cast<uint8_t>(w[e >> 2] >> (8 * (e & 3)));
+          }
+        }
+      } else {
+        const uint4 vb = to_bf16x8<FP8>(vv);
+        const uint32_t w[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = kSub * (r >> 1) + dc * 8 + e;
+          if (d < 32 * DT) {
+            sV[d * kRow + swz(d, key >> 3) * 8 + (key & 7)] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+          }
         }
       }
     }
@@ -281,7 +351,13 @@ __device__ __forceinline__ void stage_store(const Stage<FP8, VT, DT>& st, uint16
     for (int r = 0; r < DT; ++r) {
       const int c = threadIdx.x + kThreads * r;
       const int d = c >> 3, kc = c & 7;
-      *reinterpret_cast<uint4*>(sV + d * kRow + swz(d, kc) * 8) = to_bf16x8<FP8>(st.v[r]);
+      const R8 vv = raw_select<FP8>(d < D, st.v[r], (ONES && d == D) ? raw_one<FP8>() : raw_zero<FP8>());
+      if constexpr (PV8) {
+        uint8_t* sV8 = reinterpret_cast<uint8_t*>(sV);
+        *reinterpret_cast<R8*>(sV8 + d * kRow8 + swz8(d, kc >> 1) * 16 + (kc & 1) * 8) = vv;
+      } else {
+        *reinterpret_cast<uint4*>(sV + d * kRow + swz(d, kc) * 8) = to_bf16x8<FP8>(vv);
+      }
     }
   }
 }
@@ -378,23 +454,30 @@ __device__ __forceinline__ void stage_direct(const DirectLanes<DT>& dl, uint32_t
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // STAGING: kRegister (registers for every block), kDirect (direct loads for full blocks, any head_dim),
-// kDirectFull (the same at head_dim 32 DT). The last, partial block of a window always goes through registers.
-enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2 };
+// kDirectFull (the same at head_dim 32 DT), kRegisterFull (registers at head_dim 32 DT). The last, partial block
+// of a window always goes through registers. At head_dim 32 DT the score product's k-steps are all known at
+// compile time, so its operand reads are issued together instead of one wait per step.
+enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2, kRegisterFull = 3 };
 
 // ONES: head_dim below 32 DT, the row sum comes from the matrix cores (V^T row D of ones). The e4m3 V^T kernel up
 // to head_dim 64 is held to 168 VGPRs (three waves per SIMD; it needs 170 unbounded, without spilling at 168); the
 // bf16 direct-staged ones fit by themselves.
 // KMASK: a key mask (p.kv_mask) on top of the window length; every block then masks its keys.
-template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false>
-__global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kRegister)) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
-  constexpr bool DIRECT = STAGING != kRegister;
+// PV8: e4m3 K/V take the second product on the fp8 matrix cores (see the comment at the top).
+template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false, bool PV8 = false>
+__global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDirect || STAGING == kDirectFull)) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
+  constexpr bool DIRECT = STAGING == kDirect || STAGING == kDirectFull;
+  constexpr bool FULLK = STAGING == kDirectFull || STAGING == kRegisterFull;  // head_dim 32 DT
   static_assert(!KMASK || !DIRECT, "the key-mask path stages through registers");
-  static_assert(!ONES || STAGING != kDirectFull, "a full-width head has no padding row");
+  static_assert(!ONES || !FULLK, "a full-width head has no padding row");
+  static_assert(!PV8 || (FP8 && !DIRECT && !KMASK), "the e4m3 second product stages e4m3 K/V through registers");
   constexpr int kSubTiles = Width<DT>::kSubTiles;
+  // V^T tile: 32 DT rows of 64 keys, bf16 (kRow elements a row) or e4m3 (kRow8 bytes a row).
+  constexpr int kVTile = PV8 ? 32 * DT * kRow8 / 2 : 32 * DT * kRow;
   // Four distinct LDS objects (not one indexed array): the compiler can then tell the direct loads into one
   // buffer from the operand reads of the other and does not wait for the loads in flight before those reads.
   __shared__ __attribute__((aligned(16))) uint16_t sK0[kSubTiles * kKTile], sK1[kSubTiles * kKTile];
-  __shared__ __attribute__((aligned(16))) uint16_t sV0[32 * DT * kRow], sV1[32 * DT * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t sV0[kVTile], sV1[kVTile];
   __shared__ int s_window;
 
   // Workgroup -> (rank, head, query tile): XCD x (= id % 8) takes the (rank, head) units x, x + 8, ... with all
@@ -479,6 +562,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
   const T* K = static_cast<const T*>(p.k) + (p.cu_seqlens ? 0 : b * p.sk_b) + h * p.sk_h + off * p.sk_k;
   const T* V = static_cast<const T*>(p.v) + (p.cu_seqlens ? 0 : b * p.sv_b) + h * p.sv_h + off * p.sv_k;
   const int dchunks = static_cast<int>(p.D / 8);
+  const int Dv = static_cast<int>(p.D);
   // V^T rows allow vector loads when every 8-key run starts aligned (the base, the row stride and the offset).
   const bool vt_vec = VT && ((reinterpret_cast<uintptr_t>(V) & (FP8 ? 7 : 15)) == 0) && (p.sv_d % 8 == 0);
   const int nfull = L / kKB;           // full key blocks
@@ -513,10 +597,18 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
   uint32_t rd[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) rd[s] = static_cast<uint32_t>(col * kRow * 2 + swz(col, 2 * s + hh) * 16);
+  // PV8: lane (col, hh) reads keys 32 hh .. 32 hh + 31 of e4m3 V^T row 32 j + col, logical chunks 2 hh and
+  // 2 hh + 1 (the swizzle depends on col only).
+  [[maybe_unused]] uint32_t rdv[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) rdv[s] = static_cast<uint32_t>(col * kRow8 + swz8(col, 2 * hh + s) * 16);
   // 16-wide k-steps of the score product that head_dim reaches (2 DT at head_dim 32 DT).
-  const int ksteps =
-      STAGING == kDirectFull ? 2 * DT : __builtin_amdgcn_readfirstlane(static_cast<int>((p.D + 15) / 16));
+  const int ksteps = FULLK ? 2 * DT : __builtin_amdgcn_readfirstlane(static_cast<int>((p.D + 15) / 16));
 
+  // PV8: the E8M0 scale 127 (1.0) of the V^T operand, in a register (a constant scale operand would be encoded
+  // as a float inline constant).
+  [[maybe_unused]] int unit_scale = 0;
+  if constexpr (PV8) asm volatile("v_mov_b32 %0, 0x7f" : "=v"(unit_scale));
   f32x16_t o[DT];  // O^T tiles: d in [32 j, 32 j + 32)
 #pragma unroll
   for (int j = 0; j < DT; ++j) o[j] = f32x16_t{0};
@@ -537,13 +629,13 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
     }
   };
   auto stage_commit = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
-    if constexpr (!DIRECT) stage_store<FP8, VT, DT>(st, sK, sV);
+    if constexpr (!DIRECT) stage_store<FP8, VT, DT, ONES, PV8>(st, sK, sV, dchunks, Dv);
   };
   // The partial block, synchronously through registers.
   auto stage_tail = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
     Stage<FP8, VT, DT> tmp;
     stage_load<FP8, VT, DT, true, ONES>(tmp, p, K, V, L, nfull * kKB, dchunks, vt_vec);
-    stage_store<FP8, VT, DT>(tmp, sK, sV);
+    stage_store<FP8, VT, DT, ONES, PV8>(tmp, sK, sV, dchunks, Dv);
   };
 
 
@@ -562,33 +654,123 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
   // One key block from (Ks, Vt), as two 32-key halves that each run the whole online-softmax step (scores,
   // running max, exponentials, second product): a half's scores take 16 registers, which keeps four waves per
   // SIMD resident. MASKED: the partial block (keys >= L masked out).
+  // PV8, the softmax of half t of a block, packed as it is formed: P = exp2(fma(S, sl2, 4 - m)), the running max
+  // lifted by 2^4 so that P of scores from 2^-10 of the max upwards keeps a normal e4m3 value, straight into the
+  // e4m3 B operand (v_cvt_pk_fp8_f32, round to nearest even). The same lazy max as above with an e4m3 bound: a half
+  // whose lane sum (or, with the ones row, whose largest score) shows a P above 448 takes the slow path, so every
+  // packed P is at most 448 and in range. The running max is kept an integer: a raise in half 1 then rescales
+  // half 0, already packed, by an exact power of two through its E8M0 scale (byte block 0, bytes 0..15 of lanes c
+  // and c + 32, takes the scale of lane c): `drop` counts the halvings.
+  auto half_pv8 = [&](int t, f32x16_t& s, uint32_t(&pf)[8], int& drop) __attribute__((always_inline)) {
+    float lb = 0.f;
+    auto exps8 = [&]() __attribute__((always_inline)) {
+      const float nm = kPv8Lift - m;
+      float pair[8];
+#pragma unroll
+      for (int j = 0; j < 16; j += 4) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, nm));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j + 1], sl2, nm));
+        const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j + 2], sl2, nm));
+        const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j + 3], sl2, nm));
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(p0, p1, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(p2, p3, w, true);
+        pf[4 * t + j / 4] = static_cast<uint32_t>(w);
+        if constexpr (!ONES) {
+          // The row sum of the e4m3 P the matrix cores multiply (decoded exactly), so that a dominant key's
+          // rounding cancels in O / l; an e4m3 NaN (P past the range) makes the sum NaN, which the trigger catches.
+          const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+          const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+          pair[j / 2] = lo[0] + lo[1];
+          pair[j / 2 + 1] = hi[0] + hi[1];
+        }
+      }
+      if constexpr (!ONES) {
+        lb = ((pair[0] + pair[1]) + (pair[2] + pair[3])) + ((pair[4] + pair[5]) + (pair[6] + pair[7]));
+      }
+    };
+    auto hmax = [&]() __attribute__((always_inline)) {
+      float mx = __builtin_amdgcn_fmed3f(s[0], s[1], kFltMax);
+#pragma unroll
+      for (int i = 2; i < 16; i += 2) mx = max3(mx, s[i], s[i + 1]);
+      return mx;
+    };
+    auto raise8 = [&](float mx) __attribute__((always_inline)) {
+      first = false;
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
+      const float mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
+      const float cand = __builtin_ceilf(mr * sl2);
+      const float mn = cand > m ? cand : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first half, else an exact power of two
+      if (t == 1) {
+        const float rise = mn - m;  // m is finite after the window's first half
+        drop += rise < 256.f ? static_cast<int>(rise) : 256;
+      }
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+#pragma unroll
+        for (int j = 0; j < DT; ++j) o[j][i] *= alpha;
+      }
+      exps8();
+    };
+    if constexpr (ONES) {
+      const float mx = hmax();
+      exps8();
+      if (first || __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, sl2, -m) > kPv8MaxHigh) != 0ull) raise8(mx);
+    } else {
+      exps8();
+      if (first || __builtin_amdgcn_ballot_w64(!(lb < kPv8SumHigh)) != 0ull) raise8(hmax());
+      l += lb;
+    }
+  };
+
   auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vt, int kv0) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked)::value;
     const char* kp = reinterpret_cast<const char*>(Ks);
     const char* vp = reinterpret_cast<const char*>(Vt);
     const uint64_t bits = block_bits(kv0);
+    [[maybe_unused]] uint32_t pf[8];  // PV8: e4m3 P, bytes 16 t + i
+    [[maybe_unused]] int drop = 0;    // PV8: halvings of half 0 since it was packed
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       // S^T of keys 32 t .. 32 t + 31 (LDS rows 32 t + col); k-steps past head_dim (zero in Q) are skipped.
       f32x16_t s;
+      if constexpr (FULLK) {
+        bf16x8_t a[2 * DT];
 #pragma unroll
-      for (int k = 0; k < 2 * DT; ++k) {
-        if (k == 0 || k < ksteps) {
-          const bf16x8_t a =
-              *reinterpret_cast<const bf16x8_t*>(kp + (k >> 2) * (kKTile * 2) + rd[k & 3] + t * (32 * kRow * 2));
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], k == 0 ? f32x16_t{0} : s, 0, 0, 0);
+        for (int k = 0; k < 2 * DT; ++k) {
+          a[k] = *reinterpret_cast<const bf16x8_t*>(kp + (k >> 2) * (kKTile * 2) + rd[k & 3] + t * (32 * kRow * 2));
+        }
+#pragma unroll
+        for (int k = 0; k < 2 * DT; ++k) {
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[k], qf[k], k == 0 ? f32x16_t{0} : s, 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 2 * DT; ++k) {
+          if (k == 0 || k < ksteps) {
+            const bf16x8_t a =
+                *reinterpret_cast<const bf16x8_t*>(kp + (k >> 2) * (kKTile * 2) + rd[k & 3] + t * (32 * kRow * 2));
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[k], k == 0 ? f32x16_t{0} : s, 0, 0, 0);
+          }
         }
       }
       if constexpr (MASKED || KMASK) {
-        // Entry i is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8); with a key mask, bit i of `mine`.
+        // Entry i is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8) (PV8: 32 hh + 16 t + i); with a key mask,
+        // bit i of `mine`.
         const uint32_t hb = static_cast<uint32_t>(bits >> (32 * t));
         const uint32_t mine = ((hb >> (8 * hh)) & 0xffu) | (((hb >> (16 + 8 * hh)) & 0xffu) << 8);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int kin = 32 * t + ((i < 8) ? (8 * hh + i) : (16 + 8 * hh + (i - 8)));
+          const int kin = PV8 ? 32 * hh + 16 * t + i : 32 * t + ((i < 8) ? (8 * hh + i) : (16 + 8 * hh + (i - 8)));
           if (MASKED && kv0 + kin >= L) s[i] = -INFINITY;
           if (KMASK && !((mine >> i) & 1u)) s[i] = -INFINITY;
         }
+      }
+      if constexpr (PV8) {
+        half_pv8(t, s, pf, drop);
+        continue;
       }
       // P^T = exp2(sl2 S^T - m) against the running max m as it stands, as B operands: k-step ks (keys
       // 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7. On the window's first half m is -inf and the fast pass
@@ -672,9 +854,44 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
         for (int j = 0; j < DT; ++j) o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], pb[ks], o[j], 0, 0, 0);
       }
     }
+    if constexpr (PV8) {
+      // O^T += V^T . P^T over the block's 64 keys on the fp8 matrix cores; A: V^T rows 32 j + col, keys
+      // 32 hh + 0..31 (scale 1: E8M0 127); B: the packed P, half 0 scaled by 2^-drop.
+      const int sb = hh ? 127 : (drop < 127 ? 127 - drop : 0);
+      const i32x8_t bp = {static_cast<int>(pf[0]), static_cast<int>(pf[1]), static_cast<int>(pf[2]),
+                          static_cast<int>(pf[3]), static_cast<int>(pf[4]), static_cast<int>(pf[5]),
+                          static_cast<int>(pf[6]), static_cast<int>(pf[7])};
+#pragma unroll
+      for (int j = 0; j < DT; ++j) {
+        const uint4 lo = *reinterpret_cast<const uint4*>(vp + rdv[0] + j * (32 * kRow8));
+        const uint4 hi = *reinterpret_cast<const uint4*>(vp + rdv[1] + j * (32 * kRow8));
+        const i32x8_t a = {static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z),
+                           static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
+                           static_cast<int>(hi.z), static_cast<int>(hi.w)};
+        o[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bp, o[j], 0, 0, 0, unit_scale, 0, sb);
+      }
+    }
   };
   using Full = std::false_type;
   using Partial = std::true_type;
+  // After the window's last block: the fp8 products write O^T over 16 passes, the final rows last, and this
+  // toolchain places too few wait states between them and the first VALU reads of O (the rows written last were
+  // read stale on the GPU, in windows whose last block is the partial one). The reads wait here explicitly, right
+  // after the products and before any copy of O: 64 wait states, once per window. The asm takes O as an operand
+  // so that no read of it moves above the wait. (Between blocks the next block's score products and exponentials
+  // come first, far more than the wait a 16-pass product needs.)
+  auto settle = [&]() __attribute__((always_inline)) {
+#define SVHIP_WAIT64 "s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+    if constexpr (PV8 && DT == 2) {
+      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]));
+    } else if constexpr (PV8 && DT == 3) {
+      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]));
+    } else if constexpr (PV8) {
+      static_assert(DT == 4, "head widths are 2, 3 or 4 tiles");
+      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]));
+    }
+#undef SVHIP_WAIT64
+  };
 
   // Full block blk from (Ks, Vt) while full block blk + 1 is staged into (nK, nV).
   auto full_step = [&](int blk, const uint16_t* Ks, const uint16_t* Vt, uint16_t* nK, uint16_t* nV) __attribute__((always_inline)) {
@@ -715,14 +932,17 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
       Stage<FP8, VT, DT> tl;
       if (tail) stage_load<FP8, VT, DT, true, ONES>(tl, p, K, V, L, nfull * kKB, dchunks, vt_vec);
       compute(Full{}, cK, cV, blk * kKB);
+      settle();
       if (tail) {
-        stage_store<FP8, VT, DT>(tl, nK, nV);
+        stage_store<FP8, VT, DT, ONES, PV8>(tl, nK, nV, dchunks, Dv);
         wait_vmem();
         __syncthreads();
         compute(Partial{}, nK, nV, nfull * kKB);
+        settle();
       }
     } else {
       compute(Partial{}, cK, cV, 0);
+      settle();
     }
   }
 
@@ -773,40 +993,47 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING != kReg
 // The instantiation for DT = head_dim / 32 rounded up: e4m3 and row-major forms through registers, bf16 V^T
 // directly to LDS (head_dim 32 DT without exec masking).
 template <int DT, bool ONES>
-void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool vt, bool direct) {
+void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool pv8, bool vt, bool direct) {
+  constexpr int RS = ONES ? kRegister : kRegisterFull;
   if (p.kv_mask) {  // bf16 only (checked by the entry point), through registers
     if (vt) {
-      xattn_fwd_kernel<false, true, kRegister, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<false, true, RS, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
     } else {
-      xattn_fwd_kernel<false, false, kRegister, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<false, false, RS, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
     }
     return;
   }
-  if (fp8) {
+  if (fp8 && pv8) {
     if (vt) {
-      xattn_fwd_kernel<true, true, kRegister, DT, ONES><<<g, kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<true, true, RS, DT, ONES, false, true><<<g, kThreads, 0, s>>>(p);
     } else {
-      xattn_fwd_kernel<true, false, kRegister, DT, ONES><<<g, kThreads, 0, s>>>(p);
+      xattn_fwd_kernel<true, false, RS, DT, ONES, false, true><<<g, kThreads, 0, s>>>(p);
+    }
+  } else if (fp8) {
+    if (vt) {
+      xattn_fwd_kernel<true, true, RS, DT, ONES, false, false><<<g, kThreads, 0, s>>>(p);
+    } else {
+      xattn_fwd_kernel<true, false, RS, DT, ONES, false, false><<<g, kThreads, 0, s>>>(p);
     }
   } else if (direct && !ONES) {
     xattn_fwd_kernel<false, true, kDirectFull, DT, false><<<g, kThreads, 0, s>>>(p);
   } else if (direct) {
     xattn_fwd_kernel<false, true, kDirect, DT, true><<<g, kThreads, 0, s>>>(p);
   } else if (vt) {
-    xattn_fwd_kernel<false, true, kRegister, DT, ONES><<<g, kThreads, 0, s>>>(p);
+    xattn_fwd_kernel<false, true, RS, DT, ONES><<<g, kThreads, 0, s>>>(p);
   } else {
-    xattn_fwd_kernel<false, false, kRegister, DT, ONES><<<g, kThreads, 0, s>>>(p);
+    xattn_fwd_kernel<false, false, RS, DT, ONES><<<g, kThreads, 0, s>>>(p);
   }
 }
 
 // The instantiation for DT = head_dim / 32 rounded up: e4m3 and row-major forms through registers, bf16 V^T
 // directly to LDS; head_dim below 32 DT takes the row sum from the matrix cores.
 template <int DT>
-void launch(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool vt, bool direct) {
+void launch(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool pv8, bool vt, bool direct) {
   if (p.D < 32 * DT) {
-    launch_dt<DT, true>(p, g, s, fp8, vt, direct);
+    launch_dt<DT, true>(p, g, s, fp8, pv8, vt, direct);
   } else {
-    launch_dt<DT, false>(p, g, s, fp8, vt, direct);
+    launch_dt<DT, false>(p, g, s, fp8, pv8, vt, direct);
   }
 }
 
@@ -821,8 +1048,10 @@ static int xattn_impl(const void* q, const void* k, const void* v, void* o, int 
   SVHIP_REQUIRE(D >= 8 && D <= kMaxD && D % 8 == 0, "%s: head_dim %lld unsupported (multiple of 8, <= %d)", name,
                 (long long)D, kMaxD);
   SVHIP_REQUIRE(scale > 0.f && scale < 3.0e38f, "%s: softmax scale must be positive and finite", name);
-  SVHIP_REQUIRE(kv_dtype == SVHIP_BF16 || kv_dtype == SVHIP_FP8_E4M3, "%s: kv dtype %d unsupported", name, kv_dtype);
-  const bool fp8 = kv_dtype == SVHIP_FP8_E4M3;
+  SVHIP_REQUIRE(kv_dtype == SVHIP_BF16 || kv_dtype == SVHIP_FP8_E4M3 || kv_dtype == SVHIP_FP8_E4M3_PBF16,
+                "%s: kv dtype %d unsupported", name, kv_dtype);
+  const bool fp8 = kv_dtype != SVHIP_BF16;
+  const bool pv8 = kv_dtype == SVHIP_FP8_E4M3;
   SVHIP_REQUIRE(!fp8 || (k_scale && v_scale), "%s: fp8 K/V need k_scale and v_scale", name);
   SVHIP_REQUIRE(!kv_mask || !fp8, "%s: the key mask takes bf16 K/V", name);
   SVHIP_REQUIRE(sv_k == 1 || sv_d == 1, "%s: V needs a unit stride along keys or head_dim", name);
@@ -887,11 +1116,11 @@ static int xattn_impl(const void* q, const void* k, const void* v, void* o, int 
   hipStream_t s = as_stream(stream);
   const unsigned g = static_cast<unsigned>(grid);
   if (D <= 64) {
-    launch<2>(p, g, s, fp8, vt, direct);
+    launch<2>(p, g, s, fp8, pv8, vt, direct);
   } else if (D <= 96) {
-    launch<3>(p, g, s, fp8, vt, direct);
+    launch<3>(p, g, s, fp8, pv8, vt, direct);
   } else {
-    launch<4>(p, g, s, fp8, vt, direct);
+    launch<4>(p, g, s, fp8, pv8, vt, direct);
   }
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;

@@ -24,7 +24,7 @@ def _kv_code(t):
 
 
 def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scale=None, v_scale=None, out=None,
-              key_mask=None):
+              key_mask=None, p_dtype='e4m3'):
     """softmax(scale * Q K^T) V over the first L_b keys of every window b.
 
     `key_mask` (optional, bf16 K/V): bool [B, Kcap] (padded) or [B, max L] (packed); key j of window b is attended
@@ -34,7 +34,9 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
     query [B,H,Q,D] bf16 (head_dim contiguous; any other strides). key, val: padded [B,H,Kcap,D] with
     lengths int32 [B] (device), or packed [H, sum L, D] with cu_seqlens int32 [B+1] (device). `val` may be a
     transposed view (keys contiguous, e.g. `vt.transpose(-1, -2)` of a [B,H,D,Kcap] buffer), which the kernel
-    stages fastest. K/V in float8_e4m3fn (or uint8 codes) need k_scale / v_scale fp32 [B,H] (device).
+    stages fastest. K/V in float8_e4m3fn (or uint8 codes) need k_scale / v_scale fp32 [B,H] (device); with them
+    `p_dtype` 'e4m3' (default) takes P . V on the fp8 matrix cores with the softmax weights rounded to e4m3, 'bf16'
+    keeps them in bf16 (the reference's in-kernel dequantisation, slower).
     `out` (optional) [B,H,Q,D] bf16 with head_dim contiguous, e.g. a [B,Q,H,D] buffer's transpose(1, 2) view.
     Returns out."""
     _lib.require_gpu(query, key, val, lengths, cu_seqlens, k_scale, v_scale, out)
@@ -54,6 +56,11 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
         raise TypeError('key and val must share a dtype')
     if code == _lib.SVHIP_FP8_E4M3 and (k_scale is None or v_scale is None):
         raise ValueError('fp8 K/V need k_scale and v_scale')
+    if p_dtype not in ('e4m3', 'bf16'):
+        raise ValueError("p_dtype is 'e4m3' or 'bf16'")
+    fp8 = code == _lib.SVHIP_FP8_E4M3
+    if fp8 and p_dtype == 'bf16':
+        code = _lib.SVHIP_FP8_E4M3_PBF16
     if query.stride(-1) != 1 or key.stride(-1) != 1:
         raise ValueError('query and key need a contiguous head_dim')
     if out is None:
@@ -81,7 +88,7 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     lib = _lib.load()
     if key_mask is not None:
-        if code != _lib.SVHIP_BF16:
+        if fp8:
             raise TypeError('the key mask takes bf16 K/V')
         if cu_seqlens is None and key_mask.shape[1] < kcap:
             raise ValueError(f'key_mask holds {key_mask.shape[1]} keys per window, the cache {kcap}')
@@ -92,8 +99,8 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
             *sk, *sv, out.stride(0), out.stride(1), out.stride(2), scale, _lib.stream_of(query)),
             'svhip_xattn_fwd_masked')
         return out
-    kp = key.view(torch.uint8) if code == _lib.SVHIP_FP8_E4M3 else key
-    vp = val.view(torch.uint8) if code == _lib.SVHIP_FP8_E4M3 else val
+    kp = key.view(torch.uint8) if fp8 else key
+    vp = val.view(torch.uint8) if fp8 else val
     _lib.check(lib.svhip_xattn_fwd(
         _lib.ptr(query), _lib.ptr(kp), _lib.ptr(vp), _lib.ptr(out), code, _lib.ptr(lengths), _lib.ptr(cu_seqlens),
         _lib.ptr(k_scale), _lib.ptr(v_scale), B, H, Q, D, kcap, query.stride(0), query.stride(1), query.stride(2),

@@ -25,11 +25,15 @@ class CachedContext:
     """Per-layer K [B,H,Kcap,D] and V (stored transposed, [B,H,D,Kcap]) with per-window lengths.
 
     Valid keys of window b are [0, L_b); the tail is zeroed on write. kv_dtype 'bf16' or 'fp8' (OCP e4m3fn with
-    per-(window, head) scales)."""
+    per-(window, head) scales); an fp8 cache is attended with the softmax weights in `p_dtype` ('e4m3': the fp8
+    matrix cores, or 'bf16': the reference's in-kernel dequantisation; see `attention`)."""
 
-    def __init__(self, layers, batch, heads, head_dim, kv_cap, device, kv_dtype='bf16'):
+    def __init__(self, layers, batch, heads, head_dim, kv_cap, device, kv_dtype='bf16', p_dtype='e4m3'):
         if kv_dtype not in ('bf16', 'fp8'):
             raise ValueError("kv_dtype must be 'bf16' or 'fp8'")
+        if p_dtype not in ('e4m3', 'bf16'):
+            raise ValueError("p_dtype must be 'e4m3' or 'bf16'")
+        self.p_dtype = p_dtype
         self.layers, self.batch, self.heads, self.head_dim = layers, batch, heads, head_dim
         self.kv_cap = kv_cap + (-kv_cap) % KEY_BLOCK
         self.kv_dtype = kv_dtype
@@ -112,7 +116,8 @@ class CachedContext:
         ks = self.k_scale[layer]
         vs = self.v_scale[layer]
         return attention(query, self.k[layer][:n], vt, lengths=self.lengths[:n], out=out,
-                         k_scale=None if ks is None else ks[:n], v_scale=None if vs is None else vs[:n])
+                         k_scale=None if ks is None else ks[:n], v_scale=None if vs is None else vs[:n],
+                         p_dtype=self.p_dtype)
 
 
 class EaseSelect:

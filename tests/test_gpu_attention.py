@@ -155,14 +155,15 @@ def test_768_wide_model_shape_direct_vt(dev):
     check(out.cpu()[:, sel_h, ::9], ref, BF16_ATOL, BF16_RTOL)
 
 
+@pytest.mark.parametrize('p_dtype', ['e4m3', 'bf16'])
 @pytest.mark.parametrize('D', [64, 96, 128])
-def test_fp8_e4m3_cached_kv(dev, D):
+def test_fp8_e4m3_cached_kv(dev, D, p_dtype):
     from streamvoxel_amd.stream.attention import attention, quantize_e4m3
     if not hasattr(torch, 'float8_e4m3fn'):
         pytest.skip('torch without float8_e4m3fn')
     B, H, Q, kcap = 3, 4, 256, 1100
     lengths = [1100, 517, 64]
-    _case(f'xattn fp8 e4m3 K/V D={D}')
+    _case(f'xattn fp8 e4m3 K/V D={D} P={p_dtype}')
     q, k, v = make_qkv(B, H, Q, kcap, D, seed=5)
     kc, ks = quantize_e4m3(k.float())
     vc, vs = quantize_e4m3(v.float())
@@ -170,12 +171,13 @@ def test_fp8_e4m3_cached_kv(dev, D):
     vd = A.dequant_e4m3(vc.view(torch.uint8), vs[:, :, None, None])
     ref = A.cross_attention(q, kd, vd, lengths)
     out = attention(q.to(dev), kc.to(dev), vc.to(dev), lengths=torch.tensor(lengths, dtype=torch.int32, device=dev),
-                    k_scale=ks.to(dev), v_scale=vs.to(dev))
+                    k_scale=ks.to(dev), v_scale=vs.to(dev), p_dtype=p_dtype)
     vt = vc.view(torch.uint8).transpose(2, 3).contiguous().to(dev).transpose(2, 3).view(torch.float8_e4m3fn)
     out_t = attention(q.to(dev), kc.to(dev), vt, lengths=torch.tensor(lengths, dtype=torch.int32, device=dev),
-                      k_scale=ks.to(dev), v_scale=vs.to(dev))
+                      k_scale=ks.to(dev), v_scale=vs.to(dev), p_dtype=p_dtype)
     torch.cuda.synchronize()
-    check(out, ref, FP8_ATOL)
+    # V here is small (std 1/sqrt(D)): the bar is also held relative to the output's scale
+    check(out, ref, FP8_ATOL, FP8_ATOL)
     assert torch.equal(out, out_t)
     # and against the unquantised inputs, the contract's looser bound
     check(out, A.cross_attention(q, k, v, lengths), FP8_ATOL)
@@ -276,6 +278,112 @@ def test_score_scale_jumps_between_key_halves(dev, transposed, D):
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
     check(out, ref, BF16_ATOL, BF16_RTOL)
+
+
+@pytest.mark.parametrize('p_dtype', ['e4m3', 'bf16'])
+@pytest.mark.parametrize('transposed,D', [(True, 64), (False, 64), (True, 48), (True, 96)])
+def test_e4m3_score_jumps_between_key_halves(dev, transposed, D, p_dtype):
+    """The score jumps above with an e4m3 cache: the running max rises inside a block's second half after the first
+    half's P is already packed for the fp8 second product (which must then take half 0 down by the rise), and
+    holds through much lower halves; with the ones row (D=48) and without."""
+    from streamvoxel_amd.stream.attention import attention, quantize_e4m3
+    B, H, Q, kcap = 3, 2, 96, 640
+    lengths = [640, 333, 47]
+    _case(f'xattn e4m3 score jumps transposed={transposed} D={D} lengths={lengths}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=31)
+    factors = torch.tensor([1.0, 30.0, 0.01, 90.0, 2.0, 0.3, 60.0, 0.001])
+    half = torch.arange(kcap) // 32
+    kc, ks = quantize_e4m3(k.float() * factors[half % 8][None, None, :, None])
+    vc, vs = quantize_e4m3(v.float())
+    kd = A.dequant_e4m3(kc.view(torch.uint8), ks[:, :, None, None])
+    vd = A.dequant_e4m3(vc.view(torch.uint8), vs[:, :, None, None])
+    ref = A.cross_attention(q, kd, vd, lengths)
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    if transposed:
+        vv = vc.view(torch.uint8).transpose(2, 3).contiguous().to(dev).transpose(2, 3).view(torch.float8_e4m3fn)
+    else:
+        vv = vc.to(dev)
+    out = attention(q.to(dev), kc.to(dev), vv, lengths=lt, k_scale=ks.to(dev), v_scale=vs.to(dev), p_dtype=p_dtype)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    check(out, ref, FP8_ATOL)
+
+
+@pytest.mark.parametrize('kv', ['bf16', 'e4m3', 'e4m3-pbf16'])
+@pytest.mark.parametrize('L', [64, 100, 128])
+def test_single_hot_key_returns_its_value_row(dev, kv, L):
+    """Window b has one key (b mod L) whose score dwarfs the others and V rows that name their key (V[k, d] = 1 iff
+    d = k mod 64): the output of every window must be exactly its hot key's row, so any mismatch between the order
+    of the scores and the order of the V^T columns in the second product shows up as the wrong row."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, D = L, 1, 4, 64
+    _case(f'xattn single hot key kv={kv} L={L}')
+    hot = torch.arange(B) % L
+    q = torch.zeros(B, H, Q, D)
+    q[..., 0] = 1.0
+    k = torch.zeros(B, H, L, D)
+    k[torch.arange(B), 0, hot, 0] = 448.0
+    v = torch.zeros(B, H, L, D)
+    keys = torch.arange(L)
+    v[:, 0, keys, keys % D] = 1.0
+    lt = torch.full((B,), L, dtype=torch.int32, device=dev)
+    qd = q.to(torch.bfloat16).to(dev)
+    vt = v.transpose(2, 3).contiguous().transpose(2, 3)
+    if kv == 'bf16':
+        out = attention(qd, k.to(torch.bfloat16).to(dev), vt.to(torch.bfloat16).to(dev), lengths=lt)
+    else:
+        ones = torch.ones(B, H, device=dev)
+        vt8 = vt.to(torch.float8_e4m3fn).view(torch.uint8).to(dev).view(torch.float8_e4m3fn)
+        out = attention(qd, k.to(torch.float8_e4m3fn).to(dev), vt8, lengths=lt, k_scale=ones, v_scale=ones,
+                        p_dtype='bf16' if kv == 'e4m3-pbf16' else 'e4m3')
+    torch.cuda.synchronize()
+    got = out.float().cpu()[:, 0, 0].argmax(-1)
+    expect = hot % D
+    # A window whose hot key is k >= 64 holds the same row as window k - 64: the key is told apart by its window.
+    bad = (got != expect).nonzero().flatten().tolist()
+    print(f'[gpu-case] hot-key mismatches (window: got, expected): '
+          f'{[(b, int(got[b]), int(expect[b])) for b in bad[:16]]}', flush=True)
+    worst = (out.float().cpu()[:, 0] - torch.nn.functional.one_hot(expect, D).float()[:, None]).abs().amax((1, 2))
+    print(f'[gpu-case] hot-key windows off by more than 1e-3: {(worst > 1e-3).nonzero().flatten().tolist()[:32]}',
+          flush=True)
+    assert not bad
+    want = torch.nn.functional.one_hot(expect, D).float()[:, None].expand(B, Q, D)
+    assert (out.float().cpu()[:, 0] - want).abs().max().item() <= 1e-3
+
+
+# The e4m3 second product rounds every softmax weight to e4m3 (relative 2^-4); the row sum is taken over the
+# rounded weights, so a single dominant key cancels and the error grows with the weight shared by a few keys:
+# within the fp8 bar up to logit standard deviation 2, and below 1e-1 at 4, measured. bf16 P holds the fp8 bar
+# throughout.
+SHARP_E4M3_BOUND = {1.0: FP8_ATOL, 2.0: FP8_ATOL, 4.0: 1e-1}
+
+
+@pytest.mark.parametrize('p_dtype', ['e4m3', 'bf16'])
+@pytest.mark.parametrize('D', [64, 48])
+def test_e4m3_sharp_softmax_rows(dev, D, p_dtype):
+    """Logit standard deviations 1, 2 and 4 over an e4m3 cache, against float64 on the dequantised cache."""
+    from streamvoxel_amd.stream.attention import attention, quantize_e4m3
+    B, H, Q, kcap = 2, 2, 256, 2048
+    lengths = [2048, 1500]
+    g = torch.Generator().manual_seed(37)
+    for std in (1.0, 2.0, 4.0):
+        _case(f'xattn e4m3 sharp rows D={D} P={p_dtype} logit std={std}')
+        q = torch.randn(B, H, Q, D, generator=g).to(torch.bfloat16)
+        k = torch.randn(B, H, kcap, D, generator=g) * std
+        v = torch.randn(B, H, kcap, D, generator=g)
+        kc, ks = quantize_e4m3(k)
+        vc, vs = quantize_e4m3(v)
+        kd = A.dequant_e4m3(kc.view(torch.uint8), ks[:, :, None, None])
+        vd = A.dequant_e4m3(vc.view(torch.uint8), vs[:, :, None, None])
+        ref = A.cross_attention(q, kd, vd, lengths)
+        vt = vc.view(torch.uint8).transpose(2, 3).contiguous().to(dev).transpose(2, 3).view(torch.float8_e4m3fn)
+        out = attention(q.to(dev), kc.to(dev), vt, lengths=torch.tensor(lengths, dtype=torch.int32, device=dev),
+                        k_scale=ks.to(dev), v_scale=vs.to(dev), p_dtype=p_dtype)
+        torch.cuda.synchronize()
+        err = (out.double().cpu() - ref).abs().max().item()
+        print(f'[gpu-case] e4m3 D={D} P={p_dtype} logit std={std}: |kernel - f64| {err:.2e}', flush=True)
+        bound = SHARP_E4M3_BOUND[std] if p_dtype == 'e4m3' else FP8_ATOL
+        assert err <= bound, (std, err)
 
 
 @pytest.mark.parametrize('B,H', [(300, 1), (256, 3)])

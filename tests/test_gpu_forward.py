@@ -158,20 +158,23 @@ def test_step_forward_graph_replays_equal_eager(dev):
         assert torch.equal(replayed, eager), r
 
 
-def test_step_forward_over_an_e4m3_context(dev):
+@pytest.mark.parametrize('p_dtype', ['bf16', 'e4m3'])
+def test_step_forward_over_an_e4m3_context(dev, p_dtype):
     """The same small step over a cached context stored as e4m3 codes with per-(window, head) scales (written by
     svhip_kv_write from the bf16 keys and values): against the float64 step on the dequantised keys and values,
-    within the e4m3 bar of the attention (5e-2 of max |reference|, max-abs) and 1e-2 of mean |reference|."""
+    within the e4m3 bar of the attention (5e-2 of max |reference|, max-abs) and, with bf16 softmax weights, 1e-2
+    of mean |reference| (2e-2 with the weights rounded to e4m3 for the fp8 matrix cores: a 2^-4 relative rounding
+    that the blocks carry to the class head)."""
     from oracle import attention as A
     from streamvoxel_amd.stream.forward import StepForward
     from streamvoxel_amd.stream.step import CachedContext
     if not hasattr(torch, 'float8_e4m3fn'):
         pytest.skip('torch without float8_e4m3fn')
-    _case('step forward e4m3 context')
+    _case(f'step forward e4m3 context P={p_dtype}')
     model = _small_model(dev)
     n, H, D, kcap = 2, 4, 24, 192
     lengths = [150, 37]
-    ctx = CachedContext(2, n, H, D, kcap, dev, kv_dtype='fp8')
+    ctx = CachedContext(2, n, H, D, kcap, dev, kv_dtype='fp8', p_dtype=p_dtype)
     g = torch.Generator().manual_seed(31)
     keys, values = [], []
     for j in range(2):
@@ -195,4 +198,5 @@ def test_step_forward_over_an_e4m3_context(dev):
                          voxel_shape=(32, 8, 8))
     err = (out.patches.float().cpu().double() - ref).abs()
     assert float(err.max()) <= 5e-2 * float(ref.abs().max()), (float(err.max()), float(ref.abs().max()))
-    assert float(err.mean()) <= 1e-2 * float(ref.abs().mean()), (float(err.mean()), float(ref.abs().mean()))
+    mean_bar = 1e-2 if p_dtype == 'bf16' else 2e-2
+    assert float(err.mean()) <= mean_bar * float(ref.abs().mean()), (float(err.mean()), float(ref.abs().mean()))
