@@ -265,7 +265,8 @@ __device__ __forceinline__ typename Raw<FP8>::type raw_select(bool keep, const t
 // row instead: a load under a per-lane condition makes the compiler merge its result with the other arm's value
 // right away, which waits for the load and exposes its latency in the prefetch. stage_store then puts zeros (and
 // the ones row) where head_dim ends. The partial block masks its loads (keys >= L read nothing).
-template <bool FP8, bool VT, int DT, bool TAIL, bool ONES = false>
+// VREG false: V^T is staged another way (direct loads) and left alone here.
+template <bool FP8, bool VT, int DT, bool TAIL, bool ONES = false, bool VREG = true>
 __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnParams& p,
                                            const typename Elem<FP8>::T* K, const typename Elem<FP8>::T* V, int L,
                                            int kv0, int dchunks, bool vt_vec) {
@@ -284,7 +285,7 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnPa
       if constexpr (!VT) st.v[r] = load8_vec<FP8>(V + (ok ? static_cast<int64_t>(kg) * p.sv_k + dc * 8 : 0));
     }
   }
-  if constexpr (VT) {
+  if constexpr (VT && VREG) {
 #pragma unroll
     for (int r = 0; r < DT; ++r) {
       const int c = threadIdx.x + kThreads * r;
@@ -306,7 +307,7 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnPa
 // Registers -> LDS (K rows under sigma in their sub-tile; V as V^T [d][key]; both swizzled), with zeros past
 // head_dim and, with ONES, the ones row D. PV8: K rows under pv8_row, V^T kept in e4m3 in its own tile (keys in
 // natural order).
-template <bool FP8, bool VT, int DT, bool ONES, bool PV8 = false>
+template <bool FP8, bool VT, int DT, bool ONES, bool PV8 = false, bool VREG = true>
 __device__ __forceinline__ void stage_store(const Stage<FP8, VT, DT>& st, uint16_t* sK, uint16_t* sV, int dchunks,
                                             int D) {
   static_assert(!PV8 || FP8, "the e4m3 second product takes e4m3 V");
@@ -346,7 +347,7 @@ __device__ __forceinline__ void stage_store(const Stage<FP8, VT, DT>& st, uint16
       }
     }
   }
-  if constexpr (VT) {
+  if constexpr (VT && VREG) {
 #pragma unroll
     for (int r = 0; r < DT; ++r) {
       const int c = threadIdx.x + kThreads * r;
@@ -451,6 +452,40 @@ __device__ __forceinline__ void stage_direct(const DirectLanes<DT>& dl, uint32_t
   }
 }
 
+// PV8 with e4m3 V^T rows whose 16-byte runs start aligned: full blocks of V^T go straight to LDS too. One
+// 1024-byte buffer_load_dwordx4 ... lds fills 16 rows of 64 bytes (lane l: row 16 j + l / 4 at physical chunk
+// l % 4, so logical chunk (l % 4) ^ the row's swizzle); instruction j of the 2 DT goes to wave j % 4. Rows >= D are
+// never loaded (they hold zeros, or the ones row, written once).
+template <int DT>
+struct DirectV8 {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off[(2 * DT + 3) / 4];  // per instruction of the wave (some waves one fewer)
+  bool ok[(2 * DT + 3) / 4];
+};
+
+template <int DT>
+__device__ __forceinline__ DirectV8<DT> direct_v8(const XattnParams& p, const uint8_t* V, int nfull, int w) {
+  DirectV8<DT> dv;
+  const int lane = threadIdx.x & 63;
+  const uint32_t bytes = static_cast<uint32_t>((p.D - 1) * p.sv_d + static_cast<int64_t>(nfull) * kKB);
+  dv.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(V), 0, bytes, kRsrcFlags);
+#pragma unroll
+  for (int t = 0; t < (2 * DT + 3) / 4; ++t) {
+    const int R = 16 * (w + 4 * t) + (lane >> 2);
+    const int c = swz8(R, lane & 3);  // swz8 is an involution in c
+    dv.off[t] = static_cast<uint32_t>(R * p.sv_d + 16 * c);
+    dv.ok[t] = R < p.D;
+  }
+  return dv;
+}
+
+// Instruction j of the direct e4m3 V^T loads (see DirectV8): 1024 bytes into rows 16 j .. 16 j + 15 of the tile.
+__device__ __forceinline__ void direct_v8_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t off, uint32_t soff, uint16_t* sV,
+                                               int j) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(reinterpret_cast<uint8_t*>(sV) + 1024 * j), 16, off, soff,
+                                           0, 0);
+}
+
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // STAGING: kRegister (registers for every block), kDirect (direct loads for full blocks, any head_dim),
@@ -464,13 +499,15 @@ enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2, kRegisterFull = 3 };
 // bf16 direct-staged ones fit by themselves.
 // KMASK: a key mask (p.kv_mask) on top of the window length; every block then masks its keys.
 // PV8: e4m3 K/V take the second product on the fp8 matrix cores (see the comment at the top).
-template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false, bool PV8 = false>
+// VD8: with PV8, V^T takes direct loads for full blocks (e4m3 rows of 16-byte aligned runs).
+template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false, bool PV8 = false, bool VD8 = false>
 __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDirect || STAGING == kDirectFull)) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
   constexpr bool DIRECT = STAGING == kDirect || STAGING == kDirectFull;
   constexpr bool FULLK = STAGING == kDirectFull || STAGING == kRegisterFull;  // head_dim 32 DT
   static_assert(!KMASK || !DIRECT, "the key-mask path stages through registers");
   static_assert(!ONES || !FULLK, "a full-width head has no padding row");
   static_assert(!PV8 || (FP8 && !DIRECT && !KMASK), "the e4m3 second product stages e4m3 K/V through registers");
+  static_assert(!VD8 || (PV8 && VT), "direct e4m3 V^T loads serve the e4m3 second product");
   constexpr int kSubTiles = Width<DT>::kSubTiles;
   // V^T tile: 32 DT rows of 64 keys, bf16 (kRow elements a row) or e4m3 (kRow8 bytes a row).
   constexpr int kVTile = PV8 ? 32 * DT * kRow8 / 2 : 32 * DT * kRow;
@@ -592,6 +629,18 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
     }
   }
 
+  [[maybe_unused]] DirectV8<DT> dv;
+  if constexpr (VD8) {
+    dv = direct_v8<DT>(p, reinterpret_cast<const uint8_t*>(V), nfull, w);
+    // V^T rows D .. 32 DT - 1 of both tiles, which direct loads never write: zeros (row D ones with ONES).
+    for (int i = threadIdx.x; i < (32 * DT - Dv) * 4; i += kThreads) {
+      const int R = Dv + (i >> 2), c = i & 3;
+      const uint32_t x = (ONES && R == Dv) ? 0x38383838u : 0u;  // e4m3 1.0
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(sV0) + R * kRow8 + c * 16) = make_uint4(x, x, x, x);
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(sV1) + R * kRow8 + c * 16) = make_uint4(x, x, x, x);
+    }
+  }
+
   // Operand reads: lane (col, hh) takes logical chunk 2 s + hh of rows col and 32 + col of a tile; the two rows
   // share the swizzle, so four byte offsets serve K and V^T of both buffers.
   uint32_t rd[4];
@@ -625,11 +674,18 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
       stage_direct<DT, STAGING == kDirectFull>(dl, static_cast<uint32_t>(kv0 * p.sk_k * 2), static_cast<uint32_t>(kv0 * 2),
                                          w, sK, sV);
     } else {
-      stage_load<FP8, VT, DT, false, ONES>(st, p, K, V, L, blk * kKB, dchunks, vt_vec);
+      stage_load<FP8, VT, DT, false, ONES, !VD8>(st, p, K, V, L, blk * kKB, dchunks, vt_vec);
+      if constexpr (VD8) {
+#pragma unroll
+        for (int t = 0; t < (2 * DT + 3) / 4; ++t) {
+          const int j = w + 4 * t;
+          if (j < 2 * DT && dv.ok[t]) direct_v8_load(dv.rsrc, dv.off[t], static_cast<uint32_t>(blk * kKB), sV, j);
+        }
+      }
     }
   };
   auto stage_commit = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
-    if constexpr (!DIRECT) stage_store<FP8, VT, DT, ONES, PV8>(st, sK, sV, dchunks, Dv);
+    if constexpr (!DIRECT) stage_store<FP8, VT, DT, ONES, PV8, !VD8>(st, sK, sV, dchunks, Dv);
   };
   // The partial block, synchronously through registers.
   auto stage_tail = [&](uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
@@ -1004,7 +1060,9 @@ void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool p
     return;
   }
   if (fp8 && pv8) {
-    if (vt) {
+    if (vt && direct) {
+      xattn_fwd_kernel<true, true, RS, DT, ONES, false, true, true><<<g, kThreads, 0, s>>>(p);
+    } else if (vt) {
       xattn_fwd_kernel<true, true, RS, DT, ONES, false, true><<<g, kThreads, 0, s>>>(p);
     } else {
       xattn_fwd_kernel<true, false, RS, DT, ONES, false, true><<<g, kThreads, 0, s>>>(p);
@@ -1110,9 +1168,12 @@ static int xattn_impl(const void* q, const void* k, const void* v, void* o, int 
   SVHIP_REQUIRE(grid < (1ll << 31), "%s: grid too large", name);
   // Direct-to-LDS staging: bf16 K and V^T of the padded layout whose rows (and every 8-key run of V^T) start on
   // 16-byte boundaries, whose byte offsets from a (window, head) base fit 32 bits.
-  const bool direct = !fp8 && vt && !cu_seqlens && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_d % 8 == 0 &&
-                      sv_h % 8 == 0 && sv_b % 8 == 0 && (kv_cap * sk_k + D) * 2 < (1ll << 32) &&
-                      (D * sv_d + kv_cap) * 2 < (1ll << 32);
+  // e4m3 with the fp8 second product: V^T alone takes direct loads, rows of 16-byte aligned 16-key runs.
+  const bool direct =
+      fp8 ? (pv8 && vt && !cu_seqlens && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_d % 16 == 0 &&
+             sv_h % 16 == 0 && sv_b % 16 == 0 && D * sv_d + kv_cap < (1ll << 32))
+          : (vt && !cu_seqlens && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_d % 8 == 0 && sv_h % 8 == 0 &&
+             sv_b % 8 == 0 && (kv_cap * sk_k + D) * 2 < (1ll << 32) && (D * sv_d + kv_cap) * 2 < (1ll << 32));
   hipStream_t s = as_stream(stream);
   const unsigned g = static_cast<unsigned>(grid);
   if (D <= 64) {
