@@ -72,6 +72,7 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kQTile = 128;   // queries per workgroup
 constexpr int kKB = 64;       // keys per block
@@ -84,11 +85,9 @@ constexpr float kSumHigh = 1048576.0f;  // 2^20: a half's row sum above it makes
 constexpr float kMaxHigh = 20.0f;       // the same bound on a single score above the running max (log2 units)
 constexpr float kFltMax = 3.40282347e38f;
 // e4m3 second product: P is formed 2^4 above the running max and packed only while it stays below 448, the
-// largest e4m3 value: a half's lane sum of its e4m3 P of 448 or more (or, with the ones row, a score more than
-// 4.8 above the running max, 2^8.8 < 448) raises the max first.
+// largest e4m3 value: a score more than 4.8 above the running max (2^(4 + 4.8) = 445.7) raises the max first.
 constexpr float kPv8Lift = 4.0f;
-constexpr float kPv8SumHigh = 448.0f;
-constexpr float kPv8MaxHigh = 4.8f;  // 2^(4 + 4.8) = 445.7 <= 448
+constexpr float kPv8MaxHigh = 4.8f;
 // Windows are ranked by length inside every workgroup (each thread compares its candidates against all windows);
 // beyond this many windows that quadratic cost is not worth the balance and the grid keeps the window order.
 constexpr int kMaxRankWindows = 256;
@@ -654,10 +653,21 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
   // 16-wide k-steps of the score product that head_dim reaches (2 DT at head_dim 32 DT).
   const int ksteps = FULLK ? 2 * DT : __builtin_amdgcn_readfirstlane(static_cast<int>((p.D + 15) / 16));
 
-  // PV8: the E8M0 scale 127 (1.0) of the V^T operand, in a register (a constant scale operand would be encoded
-  // as a float inline constant).
+  // PV8 at head_dim 32 DT: the row sums of the packed P (rowsum) from v_mfma_f32_16x16x128_f8f6f4 with a ones
+  // pattern as A (ones16). Read as a 16x16x128 B operand, lane l of the packed P is column l % 16, k group l / 16:
+  // groups 0 and 2 hold query l % 16's 64 keys, groups 1 and 3 query 16 + l % 16's. A row 0 of ones over groups 0
+  // and 2 (lanes 0 and 32) and row 4 over groups 1 and 3 (lanes 20 and 52) put query c's sum in entry 0 of lane c
+  // (the C rows of lane l are 4 (l / 16) + i): lane-local, so a raise rescales it like O.
+  [[maybe_unused]] f32x4_t rowsum = {0.f, 0.f, 0.f, 0.f};
+  // PV8: the E8M0 scale 127 (1.0) of the A operands, in a register (a constant scale operand would be encoded as a
+  // float inline constant).
   [[maybe_unused]] int unit_scale = 0;
   if constexpr (PV8) asm volatile("v_mov_b32 %0, 0x7f" : "=v"(unit_scale));
+  [[maybe_unused]] i32x8_t ones16;
+  if constexpr (PV8 && !ONES) {
+    const int x = (lane == 0 || lane == 32 || lane == 20 || lane == 52) ? 0x38383838 : 0;  // e4m3 1.0
+    ones16 = i32x8_t{x, x, x, x, x, x, x, x};
+  }
   f32x16_t o[DT];  // O^T tiles: d in [32 j, 32 j + 32)
 #pragma unroll
   for (int j = 0; j < DT; ++j) o[j] = f32x16_t{0};
@@ -712,16 +722,15 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
   // SIMD resident. MASKED: the partial block (keys >= L masked out).
   // PV8, the softmax of half t of a block, packed as it is formed: P = exp2(fma(S, sl2, 4 - m)), the running max
   // lifted by 2^4 so that P of scores from 2^-10 of the max upwards keeps a normal e4m3 value, straight into the
-  // e4m3 B operand (v_cvt_pk_fp8_f32, round to nearest even). The same lazy max as above with an e4m3 bound: a half
-  // whose lane sum (or, with the ones row, whose largest score) shows a P above 448 takes the slow path, so every
-  // packed P is at most 448 and in range. The running max is kept an integer: a raise in half 1 then rescales
-  // half 0, already packed, by an exact power of two through its E8M0 scale (byte block 0, bytes 0..15 of lanes c
-  // and c + 32, takes the scale of lane c): `drop` counts the halvings.
+  // e4m3 B operand (v_cvt_pk_fp8_f32, round to nearest even). The lazy max with an e4m3 bound: a half whose largest
+  // score passes m by more than 4.8 (P above 2^8.8 < 448) takes the slow path first, so every packed P is in range.
+  // The row sum never comes from the VALU: the ones row D of V^T, or (head_dim 32 DT) a 16x16x128 product of the
+  // packed P with a ones pattern (rowsum). The running max is kept an integer, so that a raise in half 1 takes
+  // half 0, already packed, down by an exact power of two through the second product's E8M0 scales: `drop` counts
+  // the halvings (see the second product); the row sum takes the same difference in fp32.
   auto half_pv8 = [&](int t, f32x16_t& s, uint32_t(&pf)[8], int& drop) __attribute__((always_inline)) {
-    float lb = 0.f;
     auto exps8 = [&]() __attribute__((always_inline)) {
       const float nm = kPv8Lift - m;
-      float pair[8];
 #pragma unroll
       for (int j = 0; j < 16; j += 4) {
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, nm));
@@ -731,24 +740,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
         int w = __builtin_amdgcn_cvt_pk_fp8_f32(p0, p1, 0, false);
         w = __builtin_amdgcn_cvt_pk_fp8_f32(p2, p3, w, true);
         pf[4 * t + j / 4] = static_cast<uint32_t>(w);
-        if constexpr (!ONES) {
-          // The row sum of the e4m3 P the matrix cores multiply (decoded exactly), so that a dominant key's
-          // rounding cancels in O / l; an e4m3 NaN (P past the range) makes the sum NaN, which the trigger catches.
-          const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
-          const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
-          pair[j / 2] = lo[0] + lo[1];
-          pair[j / 2 + 1] = hi[0] + hi[1];
-        }
       }
-      if constexpr (!ONES) {
-        lb = ((pair[0] + pair[1]) + (pair[2] + pair[3])) + ((pair[4] + pair[5]) + (pair[6] + pair[7]));
-      }
-    };
-    auto hmax = [&]() __attribute__((always_inline)) {
-      float mx = __builtin_amdgcn_fmed3f(s[0], s[1], kFltMax);
-#pragma unroll
-      for (int i = 2; i < 16; i += 2) mx = max3(mx, s[i], s[i + 1]);
-      return mx;
     };
     auto raise8 = [&](float mx) __attribute__((always_inline)) {
       first = false;
@@ -762,7 +754,22 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
         drop += rise < 256.f ? static_cast<int>(rise) : 256;
       }
       m = mn;
-      l *= alpha;
+      rowsum[0] *= alpha;
+      if constexpr (!ONES) {
+        if (t == 1) {
+          // The row-sum product takes half 0 unscaled (its E8M0 scale blocks mix queries c and c + 16): take the
+          // difference off here, the pair's half-0 sum decoded from the packed bytes.
+          float h0 = 0.f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(pf[q]), false);
+            const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(pf[q]), true);
+            h0 += (lo[0] + lo[1]) + (hi[0] + hi[1]);
+          }
+          const auto hs = __builtin_amdgcn_permlane32_swap(__float_as_int(h0), __float_as_int(h0), false, false);
+          rowsum[0] -= (__int_as_float(hs[0]) + __int_as_float(hs[1])) * (1.f - alpha);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
 #pragma unroll
@@ -770,15 +777,11 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
       }
       exps8();
     };
-    if constexpr (ONES) {
-      const float mx = hmax();
-      exps8();
-      if (first || __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, sl2, -m) > kPv8MaxHigh) != 0ull) raise8(mx);
-    } else {
-      exps8();
-      if (first || __builtin_amdgcn_ballot_w64(!(lb < kPv8SumHigh)) != 0ull) raise8(hmax());
-      l += lb;
-    }
+    float mx = __builtin_amdgcn_fmed3f(s[0], s[1], kFltMax);
+#pragma unroll
+    for (int i = 2; i < 16; i += 2) mx = max3(mx, s[i], s[i + 1]);
+    exps8();
+    if (first || __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, sl2, -m) > kPv8MaxHigh) != 0ull) raise8(mx);
   };
 
   auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vt, int kv0) __attribute__((always_inline)) {
@@ -912,7 +915,11 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
     }
     if constexpr (PV8) {
       // O^T += V^T . P^T over the block's 64 keys on the fp8 matrix cores; A: V^T rows 32 j + col, keys
-      // 32 hh + 0..31 (scale 1: E8M0 127); B: the packed P, half 0 scaled by 2^-drop.
+      // 32 hh + 0..31 (E8M0 scale 127: 1); B: the packed P, half 0 scaled by 2^-drop. The 32x32x64 form takes the
+      // scale of bytes 16 b .. 16 b + 15 of column c's two lanes from lane c + 32 b (measured), so lane half 0
+      // carries half 0's scale and every block belongs to one query. (The 16x16x128 row sum cannot: there block
+      // (l / 32) + 2 (j / 16) of column l % 16 takes the scale of lane l % 16 + 16 block, mixing queries c and
+      // c + 16; it runs unscaled, corrected in the raise.)
       const int sb = hh ? 127 : (drop < 127 ? 127 - drop : 0);
       const i32x8_t bp = {static_cast<int>(pf[0]), static_cast<int>(pf[1]), static_cast<int>(pf[2]),
                           static_cast<int>(pf[3]), static_cast<int>(pf[4]), static_cast<int>(pf[5]),
@@ -925,6 +932,9 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
                            static_cast<int>(lo.w), static_cast<int>(hi.x), static_cast<int>(hi.y),
                            static_cast<int>(hi.z), static_cast<int>(hi.w)};
         o[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bp, o[j], 0, 0, 0, unit_scale, 0, sb);
+      }
+      if constexpr (!ONES) {
+        rowsum = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones16, bp, rowsum, 0, 0, 0, 0, 0, 0);
       }
     }
   };
@@ -939,12 +949,12 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
   auto settle = [&]() __attribute__((always_inline)) {
 #define SVHIP_WAIT64 "s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
     if constexpr (PV8 && DT == 2) {
-      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]));
+      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(rowsum));
     } else if constexpr (PV8 && DT == 3) {
-      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]));
+      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(rowsum));
     } else if constexpr (PV8) {
       static_assert(DT == 4, "head widths are 2, 3 or 4 tiles");
-      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]));
+      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(rowsum));
     }
 #undef SVHIP_WAIT64
   };
@@ -1015,6 +1025,11 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
       }
     }
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    lsum = __int_as_float(sw[0]);
+  } else if constexpr (PV8) {
+    // Query c's sum is entry 0 of lane c (lane half 0).
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(rowsum[0]), __float_as_int(rowsum[0]), false,
+                                                     false);
     lsum = __int_as_float(sw[0]);
   } else {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(lsum), __float_as_int(lsum), false, false);
