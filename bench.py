@@ -33,6 +33,7 @@ SHAPE, CLASSES, BLOCK, STEPS_PER_WINDOW = (256, 16, 16), 256, 4, 26
 VOXELS = SHAPE[0] * SHAPE[1] * SHAPE[2]
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP8_TFLOPS = 5000.0
 LAST_EPS = 1e-4
 
 
@@ -52,7 +53,8 @@ def parse():
     p.add_argument('--no-forward', action='store_true', help='skip the whole-step forward component')
     p.add_argument('--forward-only', action='store_true',
                    help='time only the whole-step forward (shipped shape) and print its line')
-    p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'select', 'select_planes'],
+    p.add_argument('--no-c5', action='store_true', help='skip the 64-slot e4m3 stress component')
+    p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'select', 'select_planes', 'c5_xattn', 'c5'],
                    help='build only that kernel\'s inputs (the step\'s layer-0 attention or its first solid '
                         'selection), time 20 back-to-back launches and print one line: the run to profile')
     return p.parse_args()
@@ -420,6 +422,68 @@ def sampling_tail_component(w, dev, s=12):
                 philox_kernel_us=t_kernel * 1e6, philox_with_d2h_us=t_philox * 1e6)
 
 
+C5_SLOTS, C5_HEADS, C5_WIDTH = 64, 16, 1024
+
+
+def c5_context(dev, seed, kv_dtype, p_dtype='e4m3'):
+    """The 64-slot quantised-context stress: one cross-attention layer's cache for 64 windows, 16 x 64 heads
+    (hidden 1024), L_b = 1552 + 1024 k_b keys with k_b ~ U{0..8}, K/V projected from seeded context tokens and
+    written by svhip_kv_write (e4m3 with per-(window, head) amax/448 scales, or bf16); 1024 bf16 queries per
+    window in the projection's [B,Q,H,D] layout."""
+    import torch
+    from streamvoxel_amd import synth
+    from streamvoxel_amd.stream.step import CachedContext
+    g = torch.Generator(device=dev).manual_seed(seed)
+    lengths = synth.kv_lengths(C5_SLOTS, seed)
+    ctx = CachedContext(1, C5_SLOTS, C5_HEADS, HEAD_DIM, synth.MAX_KEYS, dev, kv_dtype, p_dtype=p_dtype)
+    w = torch.randn(C5_WIDTH, 2 * C5_WIDTH, device=dev, generator=g) / math.sqrt(C5_WIDTH)
+    for b, L in enumerate(lengths):
+        kv = (torch.randn(L, C5_WIDTH, device=dev, generator=g) @ w).reshape(L, 2, C5_HEADS, HEAD_DIM)
+        kv = kv.permute(1, 2, 0, 3)
+        ctx.write(0, b, kv[0].to(torch.bfloat16), kv[1].to(torch.bfloat16))
+    q = (torch.randn(C5_SLOTS, QUERIES, C5_HEADS, HEAD_DIM, device=dev, generator=g) / 8).to(torch.bfloat16)
+    return ctx, q, lengths
+
+
+def c5_component(dev, seed):
+    """The 64-slot quantised-context stress, timed: the cross-attention layer over the e4m3 cache (P . V on the fp8
+    matrix cores), the same with bf16 softmax weights, the same keys as a bf16 cache, and the EASE selection over
+    [64 x 65536, 256] fp32 logits (4.3 GB). HIP events around graphs of back-to-back launches."""
+    import torch
+    from streamvoxel_amd import synth
+    from streamvoxel_amd.stream.step import EaseSelect
+    out = {}
+    for name, kv_dtype, p_dtype in (('e4m3', 'fp8', 'e4m3'), ('e4m3_bf16p', 'fp8', 'bf16'), ('bf16', 'bf16', 'e4m3')):
+        ctx, q, lengths = c5_context(dev, seed, kv_dtype, p_dtype)
+        o = torch.empty_like(q)
+        t = time_graph(lambda: ctx.attend(0, q.transpose(1, 2), out=o.transpose(1, 2)), 5)
+        flops = 4 * C5_HEADS * HEAD_DIM * QUERIES * sum(lengths)
+        out[f'xattn_{name}_us'] = t * 1e6
+        out[f'xattn_{name}_TFLOPs'] = flops / t / 1e12
+        out['flops_per_layer'] = flops
+        out['kv_lengths_sum'] = sum(lengths)
+        del ctx, q, o
+    out['xattn_e4m3_frac_fp8_peak'] = out['xattn_e4m3_TFLOPs'] / PEAK_FP8_TFLOPS
+    out['xattn_e4m3_frac_bf16_peak'] = out['xattn_e4m3_TFLOPs'] / PEAK_BF16_TFLOPS
+    out['xattn_bf16_frac_bf16_peak'] = out['xattn_bf16_TFLOPs'] / PEAK_BF16_TFLOPS
+    torch.cuda.empty_cache()
+    g = torch.Generator(device=dev).manual_seed(seed + 5)
+    sel = EaseSelect(C5_SLOTS, SHAPE, CLASSES, BLOCK, dev, air_ids=(0,))
+    logits = torch.empty(C5_SLOTS * VOXELS, CLASSES, device=dev)
+    synth.bimodal_logits_(logits, 0.7, generator=g)
+    k = VOXELS // (STEPS_PER_WINDOW - 1)
+    for b in range(C5_SLOTS):
+        sel.bind_window(b, torch.randperm(VOXELS // BLOCK ** 3, generator=torch.Generator().manual_seed(b)))
+        sel.set_step(b, k, 0, k / VOXELS)
+    t = time_graph(lambda: sel.run(logits), 5)
+    nbytes = C5_SLOTS * VOXELS * (CLASSES * 4 + 8 + 1 + 1)
+    out.update(select_us=t * 1e6, select_GBps=nbytes / t / 1e9, select_frac_hbm=nbytes / t / 1e9 / PEAK_HBM_GBS,
+               select_bytes=nbytes, select_bad_flag=bool(sel.bad.any()))
+    del sel, logits
+    torch.cuda.empty_cache()
+    return out
+
+
 def kernel_only(dev, args):
     """One kernel of the step alone, on the step's own inputs: the cross-attention layer (8 windows, 12 x 64 heads,
     1024 queries, the step's key lengths; bf16 or e4m3 cache) or the first solid selection (8 windows, fp32 logits
@@ -428,6 +492,14 @@ def kernel_only(dev, args):
     import torch
     from streamvoxel_amd import synth
     from streamvoxel_amd.stream.step import CachedContext, EaseSelect
+    if args.kernel == 'c5':
+        return dict(kernel='c5', **c5_component(dev, args.seed))
+    if args.kernel == 'c5_xattn':            # the 64-slot e4m3 layer alone (for the profilers)
+        ctx, q, lengths = c5_context(dev, args.seed, 'fp8')
+        o = torch.empty_like(q)
+        t = time_graph(lambda: ctx.attend(0, q.transpose(1, 2), out=o.transpose(1, 2)), 5)
+        flops = 4 * C5_HEADS * HEAD_DIM * QUERIES * sum(lengths)
+        return dict(kernel=args.kernel, us_per_launch=t * 1e6, TFLOPs=flops / t / 1e12, flops_per_launch=flops)
     g = torch.Generator(device=dev).manual_seed(args.seed)
     lengths = synth.kv_lengths(SLOTS, args.seed)
     if args.kernel.startswith('xattn'):
@@ -539,6 +611,12 @@ def main():
     log(f'sampling tail (8 windows, solid step {tail["solid_step"]}): multinomial eager '
         f'{tail["multinomial_eager_us"]:.1f} us, counter-based kernel {tail["philox_kernel_us"]:.1f} us '
         f'({tail["philox_with_d2h_us"]:.1f} us with its D2H copy)')
+    c5 = None
+    if not args.no_c5:
+        c5 = c5_component(dev, args.seed)
+        log(f'64-slot e4m3 stress (16x64 heads): layer {c5["xattn_e4m3_us"]:.0f} us = {c5["xattn_e4m3_TFLOPs"]:.0f} '
+            f'TFLOP/s (bf16 P {c5["xattn_e4m3_bf16p_us"]:.0f} us, bf16 cache {c5["xattn_bf16_us"]:.0f} us); select '
+            f'over 4.3 GB {c5["select_us"]:.0f} us = {c5["select_GBps"]:.0f} GB/s')
     eng = None
     if not args.no_forward:
         eng = shipped_engine_component(dev)
@@ -589,7 +667,8 @@ def main():
                         shipped_step_forward_plus_select_ms=(None if eng is None else
                                                              eng['forward_ms'] + t_select304 * 1e3),
                         reference_fast_forward_rtx4090d_ms=44.0,
-                        sampling_tail=tail),
+                        sampling_tail=tail,
+                        c5_64slot_e4m3=c5),
         measured_peaks=peaks,
         cpu_baseline=cpu,
     )
