@@ -11,17 +11,22 @@
 // easy as 1, 2, 3", SC 2011): ten rounds of two 64 x 64 -> 128-bit products with the published multipliers, the
 // key bumped by the published Weyl constants between rounds. u is an fp32 number in (0, 1).
 //
-// One wave per 64 voxels: the lanes read their voxels' chosen flags, write -1 (not chosen) to `values`, and the
-// wave then walks its chosen voxels one at a time. For a chosen row each lane holds ceil(C / 64) consecutive
-// classes; the wave takes the row max, the exponentials exp(x - max) and their per-lane sums, an inclusive scan of
-// the sums over the lanes gives the CDF at each lane's last class, the first lane whose prefix passes u * total
-// holds the class and walks its own classes. Rows whose max is not finite (NaN, all -inf) set `err`.
+// One workgroup per 1024 voxels of a window: every thread reads the chosen flags of 4 voxels and writes -1 (not
+// chosen) to `values`; the chosen voxels are compacted into a list in LDS (ballots and prefix counts, in voxel
+// order) and only they are hashed (the 64-bit products of Philox are the kernel's costliest arithmetic). The four
+// waves then take the listed rows G at a time each, one group of 64 / G lanes per row, so that the rows' loads and
+// reductions overlap (a row's chain of load, max, scan and pick is latency-bound). For a chosen row each lane of
+// its group holds ceil(C / lanes) consecutive classes; the group takes the row max, the exponentials
+// exp(x - max) and their per-lane sums, an inclusive scan of the sums over the group gives the CDF at each lane's
+// last class, the first lane whose prefix passes u * total holds the class, walks its own classes and writes the
+// draw. Rows whose max is not finite (NaN, all -inf) set `err`.
 #include "common.hpp"
 #include "stats.hpp"
 
 namespace svhip {
 
 constexpr int kSampleThreads = 256;
+constexpr int kSampleVoxels = 1024;  // voxels per workgroup, 4 per thread
 constexpr int kSampleMaxClasses = 1024;
 constexpr int kSampleMaxPerLane = kSampleMaxClasses / 64;
 constexpr uint64_t kPhiloxM0 = 0xD2E7470EE14C6C93ull;
@@ -69,74 +74,142 @@ __device__ __forceinline__ float load_logit(const void* x, int dtype, int64_t of
   return static_cast<const float*>(x)[off];
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-
-// PL: classes per lane held in registers (4, 8 or 16: up to 256, 512 or 1024 classes), so that short rows keep
-// more waves resident.
-template <int PL>
+// LPR lanes per row (16 or 32: four or two rows per wave at a time, or 64), PL classes per lane held in registers
+// (LPR * PL >= C; a launch has about two waves per SIMD, so registers do not bound its residency). VEC: rows are
+// contiguous (class stride 1) and 16-byte aligned, PL classes a multiple of 16 bytes: a lane whose classes all lie
+// inside the row reads them with 16-byte loads.
+template <int LPR, int PL, bool VEC>
 __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArgs a) {
-  const int lane = threadIdx.x & 63;
+  constexpr int G = 64 / LPR;              // rows per wave at a time
+  constexpr int kPerPass = 4 * G;          // rows per pass of the workgroup
+  __shared__ uint16_t s_list[kSampleVoxels];  // chosen voxels (offsets in the workgroup's range), voxel order
+  __shared__ float s_u[kSampleVoxels];        // their draws
+  __shared__ int s_count[4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int grp = lane / LPR, sub = lane % LPR;
   const int64_t b = blockIdx.y;
-  const int64_t base = (static_cast<int64_t>(blockIdx.x) * (kSampleThreads / 64) + (threadIdx.x >> 6)) * 64;
-  if (base >= a.N) return;  // wave-uniform
-  const int64_t v = base + lane;
-  const bool in = v < a.N;
-  const bool ch = in && a.chosen[b * a.N + v] != 0;
-  uint64_t todo = __ballot(ch);
-  const int cpl = static_cast<int>((a.C + 63) / 64);
-  const int c0 = lane * cpl;
-  const uint64_t seed = static_cast<uint64_t>(a.seed[b]);
-  const uint64_t step = static_cast<uint64_t>(a.step[b]);
+  const int64_t wg0 = static_cast<int64_t>(blockIdx.x) * kSampleVoxels;
+  // Flags of voxels wg0 + 4 tid + k.
+  bool f[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t v = wg0 + 4 * tid + k;
+    f[k] = v < a.N && a.chosen[b * a.N + v] != 0;
+    if (v < a.N && !f[k]) a.values[b * a.N + v] = -1;
+  }
+  // Rank of each chosen voxel: chosen voxels of lower lanes (all k), then this lane's earlier k.
+  int below = 0, own = 0;
+  int rank[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint64_t m = __ballot(f[k]);
+    below += __builtin_popcountll(m & ((1ull << lane) - 1));
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    rank[k] = below + own;
+    own += f[k] ? 1 : 0;
+  }
+  if (lane == 63) s_count[w] = below + own;
+  __syncthreads();
+  int wave_off = 0, total = 0;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    wave_off += x < w ? s_count[x] : 0;
+    total += s_count[x];
+  }
+  if (total == 0) return;  // workgroup-uniform
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (f[k]) s_list[wave_off + rank[k]] = static_cast<uint16_t>(4 * tid + k);
+  }
+  __syncthreads();
+  // The listed voxels' draws: u = (floor(w0 / 2^41) + 1/2) / 2^23.
+  const uint64_t seed = static_cast<uint64_t>(a.seed[b]), step = static_cast<uint64_t>(a.step[b]);
+  for (int t = tid; t < total; t += kSampleThreads) {
+    const uint64_t w0 = philox_w0(static_cast<uint64_t>(wg0 + s_list[t]), step, seed, kSampleStream);
+    s_u[t] = (static_cast<float>(w0 >> 41) + 0.5f) * (1.0f / 8388608.0f);
+  }
+  __syncthreads();
+  const int c0 = sub * PL;
   const char* xb = static_cast<const char*>(a.x) + b * a.sb * (a.dtype == SVHIP_BF16 ? 2 : 4);
-  int mine = -1;  // the class of this lane's voxel
-  while (todo) {
-    const int i = __builtin_ctzll(todo);
-    todo &= todo - 1;
-    const int64_t vox = base + i;
+  for (int r0 = 0; r0 < total; r0 += kPerPass) {
+    if (r0 + w * G >= total) break;  // wave-uniform: this wave has no row left
+    const int r = r0 + w * G + grp;
+    const bool active = r < total;
+    const int64_t vox = wg0 + (active ? s_list[r] : s_list[r0 + w * G]);
+    const float u = active ? s_u[r] : 0.f;
     const int64_t row = a.rows(vox) * a.sn;
     float e[PL];
     float m = -INFINITY;
+    if (VEC && active && c0 + PL <= a.C) {
+      if (a.dtype == SVHIP_BF16) {
+        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(static_cast<const void*>(xb)) +
+                                                          row + c0);
 #pragma unroll
-    for (int j = 0; j < PL; ++j) {
-      const int c = c0 + j;
-      e[j] = (j < cpl && c < a.C) ? load_logit(xb, a.dtype, row + c * a.sc) : -INFINITY;
-      m = fmaxf(m, e[j]);
+        for (int q = 0; q < PL / 8; ++q) {
+          const uint4 x = src[q];
+          const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            e[8 * q + 2 * t] = __uint_as_float(xs[t] << 16);
+            e[8 * q + 2 * t + 1] = __uint_as_float(xs[t] & 0xffff0000u);
+          }
+        }
+      } else {
+        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(static_cast<const void*>(xb)) +
+                                                            row + c0);
+#pragma unroll
+        for (int q = 0; q < PL / 4; ++q) {
+          const float4 x = src[q];
+          e[4 * q] = x.x;
+          e[4 * q + 1] = x.y;
+          e[4 * q + 2] = x.z;
+          e[4 * q + 3] = x.w;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < PL; ++j) m = fmaxf(m, e[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < PL; ++j) {
+        const int c = c0 + j;
+        e[j] = (active && c < a.C) ? load_logit(xb, a.dtype, row + c * a.sc) : -INFINITY;
+        m = fmaxf(m, e[j]);
+      }
     }
-    // A NaN logit makes fmaxf skip it; it is caught by the sum below.
-    const float mx = wave_max(m);
+    // The row max over the group (a NaN logit makes fmaxf skip it; it is caught by the sum below).
+#pragma unroll
+    for (int o = LPR / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < PL; ++j) {
-      e[j] = fast_exp(e[j] - mx);
+      e[j] = fast_exp(e[j] - m);
       s += e[j];
     }
-    // Inclusive scan of the lane sums (class order) and the exclusive prefix of this lane.
+    // Inclusive scan of the lane sums over the group (class order) and the exclusive prefix of this lane.
     float incl = s;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
+    for (int o = 1; o < LPR; o <<= 1) {
       const float t = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += t;
+      if (sub >= o) incl += t;
     }
     float excl = __shfl_up(incl, 1, 64);
-    if (lane == 0) excl = 0.f;
-    const float total = __shfl(incl, 63, 64);
-    const uint64_t w0 = philox_w0(static_cast<uint64_t>(vox), step, seed, kSampleStream);
-    const float u = (static_cast<float>(w0 >> 41) + 0.5f) * (1.0f / 8388608.0f);
-    int cls;
-    if (!(mx > -INFINITY && mx < INFINITY) || !(total > 0.f && total < INFINITY)) {
+    if (sub == 0) excl = 0.f;
+    const float tot = __shfl(incl, grp * LPR + LPR - 1, 64);
+    const bool ok = m > -INFINITY && m < INFINITY && tot > 0.f && tot < INFINITY;
+    const float target = u * tot;
+    const uint64_t gmask = (LPR == 64) ? ~0ull : (((1ull << LPR) - 1) << (grp * LPR));
+    const uint64_t past = __ballot(incl > target) & gmask;
+    // Rounding can leave u * total at the very top: the last lane with mass then holds the class.
+    const uint64_t mass = __ballot(s > 0.f) & gmask;
+    const int owner = past ? __builtin_ctzll(past) : (mass ? 63 - __builtin_clzll(mass) : grp * LPR);
+    if (active && !ok && sub == 0) {
       // No class is drawn (the reference's multinomial raises here): the voxel keeps its token and reads -1.
-      if (lane == 0) atomicOr(a.err, 1);
-      cls = -1;
-    } else {
-      const float target = u * total;
-      const uint64_t past = __ballot(incl > target);
-      // Rounding can leave u * total at the very top: the last lane with mass then holds the class.
-      const uint64_t mass = __ballot(s > 0.f);
-      const int owner = past ? __builtin_ctzll(past) : 63 - __builtin_clzll(mass);
+      atomicOr(a.err, 1);
+      a.values[b * a.N + vox] = -1;
+    }
+    if (active && ok && lane == owner) {
       int found = -1, last = -1;
       float run = excl;
 #pragma unroll
@@ -146,13 +219,9 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
         if (found < 0 && run > target && e[j] > 0.f) found = c0 + j;
       }
       if (found < 0) found = last;
-      cls = __shfl(found, owner, 64);
+      a.values[b * a.N + vox] = static_cast<int16_t>(found);
+      if (a.tokens) a.tokens[b * a.N + vox] = found;
     }
-    if (lane == i) mine = cls;
-  }
-  if (in) {
-    a.values[b * a.N + v] = static_cast<int16_t>(ch ? mine : -1);
-    if (ch && mine >= 0 && a.tokens) a.tokens[b * a.N + v] = mine;
   }
 }
 
@@ -194,16 +263,35 @@ extern "C" int svhip_sample_chosen(const void* logits, int dtype, int64_t classe
   a.step = step;
   a.err = err;
   a.N = N;
-  const int64_t waves = cdiv(N, 64);
-  const dim3 grid(static_cast<unsigned>(cdiv(waves, kSampleThreads / 64)), static_cast<unsigned>(batch));
-  const int64_t per_lane = cdiv(classes, 64);
-  if (per_lane <= 4) {
-    sample_chosen_kernel<4><<<grid, kSampleThreads, 0, as_stream(stream)>>>(a);
-  } else if (per_lane <= 8) {
-    sample_chosen_kernel<8><<<grid, kSampleThreads, 0, as_stream(stream)>>>(a);
+  const dim3 grid(static_cast<unsigned>(cdiv(N, kSampleVoxels)), static_cast<unsigned>(batch));
+  hipStream_t st = as_stream(stream);
+  const int64_t esize = dtype == SVHIP_BF16 ? 2 : 4;
+  // 16-byte loads of contiguous rows: class stride 1, 16-byte aligned base and row and window strides (a lane's
+  // PL classes start at a multiple of 16 bytes for every PL below).
+  const bool vec = stride_c == 1 && reinterpret_cast<uintptr_t>(logits) % 16 == 0 && (stride_n * esize) % 16 == 0 &&
+                   (stride_b * esize) % 16 == 0;
+#define SVHIP_SAMPLE(LPR, PL)                                                 \
+  do {                                                                        \
+    if (vec) {                                                                \
+      sample_chosen_kernel<LPR, PL, true><<<grid, kSampleThreads, 0, st>>>(a);  \
+    } else {                                                                  \
+      sample_chosen_kernel<LPR, PL, false><<<grid, kSampleThreads, 0, st>>>(a); \
+    }                                                                         \
+  } while (0)
+  if (classes <= 64) {
+    SVHIP_SAMPLE(16, 4);
+  } else if (classes <= 128) {
+    SVHIP_SAMPLE(16, 8);
+  } else if (classes <= 256) {
+    SVHIP_SAMPLE(16, 16);
+  } else if (classes <= 384) {
+    SVHIP_SAMPLE(16, 24);
+  } else if (classes <= 512) {
+    SVHIP_SAMPLE(32, 16);
   } else {
-    sample_chosen_kernel<kSampleMaxPerLane><<<grid, kSampleThreads, 0, as_stream(stream)>>>(a);
+    SVHIP_SAMPLE(64, kSampleMaxPerLane);
   }
+#undef SVHIP_SAMPLE
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;
 }
