@@ -34,37 +34,43 @@ ORDER_SEED_OFFSET = 9173
 
 class ForwardBudget:
     """Forward counting of one window (stream/slot.py:12-47): the marking forward, then one forward per solid quota.
+
+    Kept as two counters, the window's forward total and the forwards taken so far; the phase follows from them:
+    'idle' before `arm` and once every forward is taken, 'marking' before the first forward, 'solid' in between.
     `arm(total)` sets the whole-window count including the marking forward; `forward()` returns True on the forward
-    that finishes the window."""
+    that finishes the window (an idle budget takes no forward and returns False)."""
 
     def __init__(self):
-        self.phase = 'idle'
-        self.solid = 0
-        self.left = 0
+        self.total = 0
         self.nfe = 0
 
     def arm(self, total):
         total = int(total)
         if total < 1:
             raise ValueError('A window needs at least the marking forward')
-        self.phase = 'marking'
-        self.solid = total - 1
-        self.left = 0
-        self.nfe = 0
+        self.total, self.nfe = total, 0
+
+    @property
+    def phase(self):
+        if self.nfe >= self.total:
+            return 'idle'
+        return 'marking' if self.nfe == 0 else 'solid'
+
+    @property
+    def solid(self):
+        """Solid forwards of the armed window."""
+        return max(self.total - 1, 0)
+
+    @property
+    def left(self):
+        """Solid forwards still to take (0 before the marking forward and once idle)."""
+        return self.total - self.nfe if self.phase == 'solid' else 0
 
     def forward(self):
         if self.phase == 'idle':
             return False
         self.nfe += 1
-        if self.phase == 'marking':
-            self.phase = 'solid'
-            self.left = self.solid
-        else:
-            self.left -= 1
-        if self.left == 0:
-            self.phase = 'idle'
-            return True
-        return False
+        return self.nfe == self.total
 
 
 def _class_major(logits, classes, total):
@@ -369,67 +375,71 @@ class LowEntropyLastSlot:
 FastLowEntropyLastSlot = LowEntropyLastSlot
 
 
-class SelectGraphs:
-    """One captured `select` per (bucket, slot) over an engine's static outputs and token rows
-    (fast_ops.py:584-623). `engine` provides `device`, `graphs` (non-empty once captured), `outputs`
-    ({bucket size: logits [size, C, Y, Z, X] or PatchLogits}) and `tokens` ([slots, Y, Z, X] int64). `lookup(logits)` returns the
-    bucket whose output tensor `logits` is, or None (eager logits then select eagerly)."""
+class _NothingSelected:
+    """Context in which every slot's quota is 0, so that a captured or warm-up `select` commits and draws nothing
+    (a slot with the 'philox' sampler would otherwise draw into the engine's token rows); the quotas come back
+    afterwards and the static outputs are cleared. `prepare()` sets the quota before every real step."""
 
-    def __init__(self, engine, slots):
-        self.engine, self.slots = engine, slots
-        self.graphs = {}
-        if not getattr(engine, 'graphs', None):
-            return
-        device = engine.device
-        # Warm-up and capture select nothing (k = 0): a slot with the 'philox' sampler would otherwise draw into the
-        # engine's token rows. prepare() sets k before every step.
-        saved_k = [slot.k.clone() for slot in slots]
-        for slot in slots:
+    def __init__(self, slots):
+        self.slots = slots
+
+    def __enter__(self):
+        self.saved = [slot.k.clone() for slot in self.slots]
+        for slot in self.slots:
             slot.k.zero_()
-        current = torch.cuda.current_stream(device)
-        warm = torch.cuda.Stream(device=device)
-        warm.wait_stream(current)
-        with torch.cuda.stream(warm), torch.inference_mode():
-            for size, out in engine.outputs.items():
-                for i in range(size):
-                    slots[i].select(out[i], engine.tokens[i])
-        current.wait_stream(warm)
-        torch.cuda.synchronize(device)
-        stream = torch.cuda.Stream(device=device)
-        pool = torch.cuda.graph_pool_handle()
-        with torch.inference_mode():
-            for size, out in sorted(engine.outputs.items()):
-                for i in range(size):
-                    graph = torch.cuda.CUDAGraph()
-                    with torch.cuda.graph(graph, pool=pool, stream=stream, capture_error_mode='thread_local'):
-                        slots[i].select(out[i], engine.tokens[i])
-                    self.graphs[size, i] = graph
-        for slot, k in zip(slots, saved_k):
+
+    def __exit__(self, *exc):
+        for slot, k in zip(self.slots, self.saved):
             slot.chosen.zero_()
             slot.bad.zero_()
             slot.k.copy_(k)
+        return False
+
+
+class SelectGraphs:
+    """One captured `select` per (bucket, slot) over an engine's static outputs and token rows
+    (fast_ops.py:584-623). `engine` provides `device`, `graphs` (non-empty once captured), `outputs`
+    ({bucket size: logits [size, C, Y, Z, X] or PatchLogits}) and `tokens` ([slots, Y, Z, X] int64). The graphs are
+    made by the engine's own `StepGraphs` (warm-up on a side stream, one pool, the buckets in ascending order); if
+    a capture fails the dictionary stays empty and every step selects eagerly. `lookup(logits)` returns the bucket
+    whose output tensor `logits` is, or None (eager logits then select eagerly)."""
+
+    def __init__(self, engine, slots):
+        from streamvoxel_amd.stream.engine import StepGraphs
+        self.engine, self.slots = engine, slots
+        self.graphs = {}
+        self._buckets = {}
+        if not getattr(engine, 'graphs', None):
+            return
+        outputs = engine.outputs
+        self._buckets = {(out.data_ptr(), len(out)): size for size, out in outputs.items()}
+        keys = [(size, i) for size in sorted(outputs) for i in range(size)]
+
+        def body(key):
+            size, i = key
+            slots[i].select(outputs[size][i], engine.tokens[i])
+
+        with _NothingSelected(slots), torch.inference_mode():
+            captured = StepGraphs(engine.device, body, keys, warmup=1)
+            torch.cuda.synchronize(engine.device)
+        self.graphs = captured.graphs
 
     def lookup(self, logits):
-        for size, out in self.engine.outputs.items():
-            if logits.data_ptr() == out.data_ptr() and len(logits) == len(out):
-                return size
-        return None
+        return self._buckets.get((logits.data_ptr(), len(logits)))
 
 
 def consume_batch(slots, logits, tokens, count, graphs=None):
     """`[slot.consume(logits[i], tokens[i]) for i < count]` with every staged solid step enqueued before the first
-    host wait (fast_ops.py:626-642). Returns {index: (finished, commit)} for the non-idle slots."""
-    size = graphs.lookup(logits) if graphs is not None else None
-    staged, results = {}, {}
-    for index in range(count):
-        slot = slots[index]
-        if slot.idle:
-            continue
-        if slot.stageable():
-            graph = graphs.graphs.get((size, index)) if size is not None else None
-            staged[index] = slot.stage(logits[index], tokens[index], graph)
-        else:
-            results[index] = slot.consume(logits[index], tokens[index])
-    for index, item in staged.items():
-        results[index] = slots[index].collect(item)
-    return dict(sorted(results.items()))
+    host wait (fast_ops.py:626-642): the device work of all the batch's solid steps is queued first (each slot's
+    captured select when `logits` is a bucket's output), then the host collects the slots in order. Marking and
+    finishing forwards go through `consume`. Returns {index: (finished, commit)} for the non-idle slots."""
+    bucket = graphs.lookup(logits) if graphs is not None else None
+    active = [(i, slots[i]) for i in range(count) if not slots[i].idle]
+    queued = [(i, slot) for i, slot in active if slot.stageable()]
+    handles = {}
+    for i, slot in queued:
+        graph = graphs.graphs.get((bucket, i)) if bucket is not None else None
+        handles[i] = slot.stage(logits[i], tokens[i], graph)
+    results = {i: slot.consume(logits[i], tokens[i]) for i, slot in active if i not in handles}
+    results.update({i: slot.collect(handles[i]) for i, slot in queued})
+    return {i: results[i] for i in sorted(results)}
