@@ -195,6 +195,18 @@ def time_events(fn, reps, warm=3):
     return start.elapsed_time(end) / reps / 1e3   # seconds per call
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None where it is not readable."""
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def time_graph(fn, reps, replays=5):
     """Seconds per call of `fn` from HIP events around replays of one graph of `reps` back-to-back calls (no host
     gaps between the launches), recorded on the stream the graph launches on."""
@@ -295,7 +307,8 @@ def cpu_baseline(w, budget_s):
                         f'queries, {kcap} padded keys) + {len(sel_times)} x fp32 entropy + block-quota select of one '
                         f'[256,16,16] window (C={CLASSES}); step extrapolated x{SLOTS * LAYERS} / x{SLOTS}'),
                 seconds_per_step=t_step, attn_s_per_window_layer=t_attn, select_s_per_window=t_sel,
-                cpu_count=os.cpu_count(), wall_s=time.perf_counter() - began)
+                cpu_count=os.cpu_count(), torch_threads=torch.get_num_threads(), cpu_model=cpu_model(),
+                wall_s=time.perf_counter() - began)
 
 
 def shipped_engine_component(dev, lengths_seed=7):

@@ -89,6 +89,32 @@ def test_class_major_and_patch_layouts_match_oracle(dev, classes, dtype):
         print(f'[gpu-case] C={classes} {dtype} window {b}: {same:.5f} of the draws equal the oracle class', flush=True)
 
 
+@pytest.mark.parametrize('shape,share', [((5, 7, 9), 1.0), ((8, 8, 24), 0.6)])
+@pytest.mark.parametrize('classes,dtype', [(256, torch.float32), (304, torch.bfloat16), (1000, torch.float32)])
+def test_ragged_windows_and_dense_choices_match_oracle(dev, shape, share, classes, dtype):
+    """Windows whose voxel count is not a multiple of the kernel's 1024-voxel workgroup (315: one partial group,
+    1536: one full and one partial), up to every voxel chosen, from voxel rows (a class-major view with unit class
+    stride, the 16-byte row loads where they apply)."""
+    from streamvoxel_amd.stream.sampler import sample_chosen
+    n = 2
+    N = shape[0] * shape[1] * shape[2]
+    _case(f'sample_chosen ragged C={classes} dtype={dtype} shape={shape} share={share}')
+    g = torch.Generator().manual_seed(N + classes)
+    rows = (torch.randn(n, N, classes, generator=g) * 2.0).to(dtype)          # voxel rows [n, N, C]
+    chosen = torch.rand(n, *shape, generator=g) < share
+    cm = rows.to(dev).transpose(1, 2).reshape(n, classes, *shape)              # view, class stride 1
+    assert cm.stride(1) == 1
+    values, _, steps, err = _buffers(n, shape, dev, step=3)
+    seeds = [5, 77]
+    sample_chosen(cm, chosen.to(dev), torch.tensor(seeds, dtype=torch.int64, device=dev), steps, values, err)
+    torch.cuda.synchronize()
+    assert int(err) == 0
+    v = values.cpu()
+    for b in range(n):
+        _check_draws(v[b].reshape(-1).numpy(), rows[b].double().numpy(), chosen[b].reshape(-1).numpy(), seeds[b], 3,
+                     f'ragged C={classes} window={b}')
+
+
 def test_equal_logits_draw_floor_u_times_classes(dev):
     """Equal logits: the CDF is (c + 1) / C, so the class is floor(u C) (up to the fp32 rounding of u * total at
     the boundaries)."""
