@@ -76,8 +76,8 @@ __device__ __forceinline__ float load_logit(const void* x, int dtype, int64_t of
 
 // LPR lanes per row (16 or 32: four or two rows per wave at a time, or 64), PL classes per lane held in registers
 // (LPR * PL >= C; a launch has about two waves per SIMD, so registers do not bound its residency). VEC: rows are
-// contiguous (class stride 1) and 16-byte aligned, PL classes a multiple of 16 bytes: a lane whose classes all lie
-// inside the row reads them with 16-byte loads.
+// contiguous (class stride 1) and 16-byte aligned: a lane whose classes all lie inside the row and fill whole
+// 16-byte loads reads them so.
 template <int LPR, int PL, bool VEC>
 __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArgs a) {
   constexpr int G = 64 / LPR;              // rows per wave at a time
@@ -142,7 +142,9 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
     const int64_t row = a.rows(vox) * a.sn;
     float e[PL];
     float m = -INFINITY;
-    if (VEC && active && c0 + PL <= a.C) {
+    // (the lane's classes must fill whole 16-byte loads: PL % 8 == 0 for bf16, PL % 4 == 0 for fp32)
+    const bool whole = a.dtype == SVHIP_BF16 ? PL % 8 == 0 : PL % 4 == 0;
+    if (VEC && whole && active && c0 + PL <= a.C) {
       if (a.dtype == SVHIP_BF16) {
         const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(static_cast<const void*>(xb)) +
                                                           row + c0);
