@@ -918,15 +918,18 @@ static int launch_ease_stats(const T* x, int64_t batch, int64_t C, int64_t n, in
                 name, Vec16<T>::kElems, 128 * Vec16<T>::kElems);
   const unsigned grid = static_cast<unsigned>(plan.grid + side);
   if (plan.layout == kVoxelMajor) {
+    // The row plan takes 8 lanes per voxel only with an odd vector count (row_plan), so only those are built.
 #define SVHIP_EVM(NVV)                                                                                        \
   case NVV:                                                                                                   \
-    if (plan.lpv == 8) {                                                                                      \
-      ease_stats_kernel<T, kVoxelMajor, NVV, 8><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side, \
-                                                                      rows);                                  \
-    } else {                                                                                                  \
-      ease_stats_kernel<T, kVoxelMajor, NVV, 16><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap,      \
-                                                                       side, rows);                           \
+    if constexpr (NVV % 2 == 1) {                                                                             \
+      if (plan.lpv == 8) {                                                                                    \
+        ease_stats_kernel<T, kVoxelMajor, NVV, 8><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap,     \
+                                                                        side, rows);                          \
+        return SVHIP_OK;                                                                                      \
+      }                                                                                                       \
     }                                                                                                         \
+    ease_stats_kernel<T, kVoxelMajor, NVV, 16><<<grid, 256, 0, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side,  \
+                                                                     rows);                                   \
     return SVHIP_OK;
     switch (plan.nv) {
       SVHIP_EVM(1)
@@ -948,11 +951,13 @@ static int launch_ease_stats(const T* x, int64_t batch, int64_t C, int64_t n, in
     const int nv = plan.nv;
 #define SVHIP_ECANON(LAY, LPVV, CM)                                                                          \
   ease_stats_kernel<T, LAY, 0, LPVV, CM><<<grid, 256, lds, s>>>(x, batch, n, C, sb, sc, sn, ks, ap, side, rows, nv)
-#define SVHIP_ECANON_C(LAY, LPVV)           \
-  if (C <= 256) {                           \
-    SVHIP_ECANON(LAY, LPVV, 256);           \
-  } else {                                  \
-    SVHIP_ECANON(LAY, LPVV, kCanonMaxC);    \
+    // Above 256 classes 8 lanes per voxel occur only for bf16 rows (fp32 rows then have more than 8 vectors per
+    // lane of 8), so the fp32 form of that case is not built.
+#define SVHIP_ECANON_C(LAY, LPVV)                                 \
+  if (C <= 256) {                                                 \
+    SVHIP_ECANON(LAY, LPVV, 256);                                 \
+  } else if constexpr (LPVV == 16 || sizeof(T) == 2) {            \
+    SVHIP_ECANON(LAY, LPVV, kCanonMaxC);                          \
   }
     if (plan.layout == kCanonVec) {
       if (plan.lpv == 8) {

@@ -101,6 +101,8 @@ __host__ __device__ inline bool row_plan(int64_t C, RowPlan* rp) {
   if (C < E || C % E != 0) return false;
   const int64_t vecs = C / E;
   if (cdiv(vecs, 16) > 8) return false;
+  // 8 lanes leave fewer vector slots idle than 16 exactly when ceil(vecs / 8) is odd (for an even count both leave
+  // the same): 8 lanes therefore always come with an odd vector count per lane, and the launchers build only those.
   const bool eight = cdiv(vecs, 8) <= 8 && cdiv(vecs, 8) * 8 - vecs < cdiv(vecs, 16) * 16 - vecs;
   rp->lpv = eight ? 8 : 16;
   rp->nv = static_cast<int>(cdiv(vecs, rp->lpv));

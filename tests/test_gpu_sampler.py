@@ -51,7 +51,7 @@ def _check_draws(got, rows64, chosen, seed, step, where):
     return same
 
 
-@pytest.mark.parametrize('classes', [5, 256, 304, 1000])
+@pytest.mark.parametrize('classes', [5, 100, 256, 304, 500, 1000])
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
 def test_class_major_and_patch_layouts_match_oracle(dev, classes, dtype):
     from streamvoxel_amd.stream.patches import PatchLogits
@@ -90,8 +90,9 @@ def test_class_major_and_patch_layouts_match_oracle(dev, classes, dtype):
 
 
 @pytest.mark.parametrize('shape,share', [((5, 7, 9), 1.0), ((8, 8, 24), 0.6)])
-@pytest.mark.parametrize('classes,dtype', [(64, torch.bfloat16), (64, torch.float32), (256, torch.float32),
-                                           (304, torch.bfloat16), (1000, torch.float32)])
+@pytest.mark.parametrize('classes,dtype', [(64, torch.bfloat16), (64, torch.float32), (100, torch.float32),
+                                           (256, torch.float32), (304, torch.bfloat16), (512, torch.bfloat16),
+                                           (1000, torch.float32)])
 def test_ragged_windows_and_dense_choices_match_oracle(dev, shape, share, classes, dtype):
     """Windows whose voxel count is not a multiple of the kernel's 1024-voxel workgroup (315: one partial group,
     1536: one full and one partial), up to every voxel chosen, from voxel rows (a class-major view with unit class
