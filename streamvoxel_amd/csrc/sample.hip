@@ -11,22 +11,22 @@
 // easy as 1, 2, 3", SC 2011): ten rounds of two 64 x 64 -> 128-bit products with the published multipliers, the
 // key bumped by the published Weyl constants between rounds. u is an fp32 number in (0, 1).
 //
-// One workgroup per 1024 voxels of a window: every thread reads the chosen flags of 4 voxels and writes -1 (not
+// One workgroup per 512 voxels of a window: every thread reads the chosen flags of 2 voxels and writes -1 (not
 // chosen) to `values`; the chosen voxels are compacted into a list in LDS (ballots and prefix counts, in voxel
-// order) and only they are hashed (the 64-bit products of Philox are the kernel's costliest arithmetic). The four
-// waves then take the listed rows G at a time each, one group of 64 / G lanes per row, so that the rows' loads and
-// reductions overlap (a row's chain of load, max, scan and pick is latency-bound). For a chosen row each lane of
-// its group holds ceil(C / lanes) consecutive classes; the group takes the row max, the exponentials
-// exp(x - max) and their per-lane sums, an inclusive scan of the sums over the group gives the CDF at each lane's
-// last class, the first lane whose prefix passes u * total holds the class, walks its own classes and writes the
-// draw. Rows whose max is not finite (NaN, all -inf) set `err`.
+// order) and only they are hashed (the 64-bit products of Philox are the kernel's costliest arithmetic), while the
+// first rows' loads are in flight. The four waves take the listed rows G at a time each, one group of 64 / G lanes
+// per row, so that the rows' loads and reductions overlap (a row's chain of load, max, scan and pick is
+// latency-bound). For a chosen row each lane of its group holds ceil(C / lanes) consecutive classes; the group
+// takes the row max, the exponentials exp(x - max) and their per-lane sums, an inclusive scan of the sums over
+// the group gives the CDF at each lane's last class, the first lane whose prefix passes u * total holds the class,
+// walks its own classes and writes the draw. Rows whose max is not finite (NaN, all -inf) set `err`.
 #include "common.hpp"
 #include "stats.hpp"
 
 namespace svhip {
 
 constexpr int kSampleThreads = 256;
-constexpr int kSampleVoxels = 1024;  // voxels per workgroup, 4 per thread
+constexpr int kSampleVoxels = 512;  // voxels per workgroup, 2 per thread
 constexpr int kSampleMaxClasses = 1024;
 constexpr int kSampleMaxPerLane = kSampleMaxClasses / 64;
 constexpr uint64_t kPhiloxM0 = 0xD2E7470EE14C6C93ull;
@@ -82,6 +82,7 @@ template <int LPR, int PL, bool VEC>
 __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArgs a) {
   constexpr int G = 64 / LPR;              // rows per wave at a time
   constexpr int kPerPass = 4 * G;          // rows per pass of the workgroup
+  constexpr int kPerThread = kSampleVoxels / kSampleThreads;
   __shared__ uint16_t s_list[kSampleVoxels];  // chosen voxels (offsets in the workgroup's range), voxel order
   __shared__ float s_u[kSampleVoxels];        // their draws
   __shared__ int s_count[4];
@@ -89,24 +90,24 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
   const int grp = lane / LPR, sub = lane % LPR;
   const int64_t b = blockIdx.y;
   const int64_t wg0 = static_cast<int64_t>(blockIdx.x) * kSampleVoxels;
-  // Flags of voxels wg0 + 4 tid + k.
-  bool f[4];
+  // Flags of voxels wg0 + kPerThread tid + k.
+  bool f[kPerThread];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int64_t v = wg0 + 4 * tid + k;
+  for (int k = 0; k < kPerThread; ++k) {
+    const int64_t v = wg0 + kPerThread * tid + k;
     f[k] = v < a.N && a.chosen[b * a.N + v] != 0;
     if (v < a.N && !f[k]) a.values[b * a.N + v] = -1;
   }
   // Rank of each chosen voxel: chosen voxels of lower lanes (all k), then this lane's earlier k.
   int below = 0, own = 0;
-  int rank[4];
+  int rank[kPerThread];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < kPerThread; ++k) {
     const uint64_t m = __ballot(f[k]);
     below += __builtin_popcountll(m & ((1ull << lane) - 1));
   }
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < kPerThread; ++k) {
     rank[k] = below + own;
     own += f[k] ? 1 : 0;
   }
@@ -120,28 +121,22 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
   }
   if (total == 0) return;  // workgroup-uniform
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    if (f[k]) s_list[wave_off + rank[k]] = static_cast<uint16_t>(4 * tid + k);
+  for (int k = 0; k < kPerThread; ++k) {
+    if (f[k]) s_list[wave_off + rank[k]] = static_cast<uint16_t>(kPerThread * tid + k);
   }
   __syncthreads();
-  // The listed voxels' draws: u = (floor(w0 / 2^41) + 1/2) / 2^23.
-  const uint64_t seed = static_cast<uint64_t>(a.seed[b]), step = static_cast<uint64_t>(a.step[b]);
-  for (int t = tid; t < total; t += kSampleThreads) {
-    const uint64_t w0 = philox_w0(static_cast<uint64_t>(wg0 + s_list[t]), step, seed, kSampleStream);
-    s_u[t] = (static_cast<float>(w0 >> 41) + 0.5f) * (1.0f / 8388608.0f);
-  }
-  __syncthreads();
+
   const int c0 = sub * PL;
   const char* xb = static_cast<const char*>(a.x) + b * a.sb * (a.dtype == SVHIP_BF16 ? 2 : 4);
-  for (int r0 = 0; r0 < total; r0 += kPerPass) {
-    if (r0 + w * G >= total) break;  // wave-uniform: this wave has no row left
+  float e[PL];
+  float m = -INFINITY;
+  // The row of the pass starting at list entry r0 into e (and its max into m); lanes without a row read nothing.
+  auto load_row = [&](int r0) __attribute__((always_inline)) {
     const int r = r0 + w * G + grp;
     const bool active = r < total;
-    const int64_t vox = wg0 + (active ? s_list[r] : s_list[r0 + w * G]);
-    const float u = active ? s_u[r] : 0.f;
+    const int64_t vox = wg0 + s_list[active ? r : r0 + w * G];
     const int64_t row = a.rows(vox) * a.sn;
-    float e[PL];
-    float m = -INFINITY;
+    m = -INFINITY;
     // (the lane's classes must fill whole 16-byte loads: PL % 8 == 0 for bf16, PL % 4 == 0 for fp32)
     const bool whole = a.dtype == SVHIP_BF16 ? PL % 8 == 0 : PL % 4 == 0;
     if (VEC && whole && active && c0 + PL <= a.C) {
@@ -170,16 +165,22 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
           e[4 * q + 3] = x.w;
         }
       }
-#pragma unroll
-      for (int j = 0; j < PL; ++j) m = fmaxf(m, e[j]);
     } else {
 #pragma unroll
       for (int j = 0; j < PL; ++j) {
         const int c = c0 + j;
         e[j] = (active && c < a.C) ? load_logit(xb, a.dtype, row + c * a.sc) : -INFINITY;
-        m = fmaxf(m, e[j]);
       }
     }
+  };
+  // The rest of the pass: the categorical draw of the row each group holds.
+  auto finish_row = [&](int r0) __attribute__((always_inline)) {
+    const int r = r0 + w * G + grp;
+    const bool active = r < total;
+    const int64_t vox = wg0 + s_list[active ? r : r0 + w * G];
+    const float u = active ? s_u[r] : 0.f;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) m = fmaxf(m, e[j]);
     // The row max over the group (a NaN logit makes fmaxf skip it; it is caught by the sum below).
 #pragma unroll
     for (int o = LPR / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
@@ -224,6 +225,24 @@ __global__ __launch_bounds__(kSampleThreads) void sample_chosen_kernel(SampleArg
       a.values[b * a.N + vox] = static_cast<int16_t>(found);
       if (a.tokens) a.tokens[b * a.N + vox] = found;
     }
+  };
+
+  // The first pass's rows are in flight while the listed voxels' draws are hashed:
+  // u = (floor(w0 / 2^41) + 1/2) / 2^23.
+  const bool first_pass = w * G < total;  // wave-uniform
+  if (first_pass) load_row(0);
+  const uint64_t seed = static_cast<uint64_t>(a.seed[b]), step = static_cast<uint64_t>(a.step[b]);
+  for (int t = tid; t < total; t += kSampleThreads) {
+    const uint64_t w0 = philox_w0(static_cast<uint64_t>(wg0 + s_list[t]), step, seed, kSampleStream);
+    s_u[t] = (static_cast<float>(w0 >> 41) + 0.5f) * (1.0f / 8388608.0f);
+  }
+  __syncthreads();
+  if (!first_pass) return;  // wave-uniform: no barrier follows
+  finish_row(0);
+  for (int r0 = kPerPass; r0 < total; r0 += kPerPass) {
+    if (r0 + w * G >= total) break;  // wave-uniform: this wave has no row left
+    load_row(r0);
+    finish_row(r0);
   }
 }
 
