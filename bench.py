@@ -147,39 +147,44 @@ class Workload:
         for layer in range(LAYERS):
             self.ctx.attend(layer, self.q[step][layer], out=self.o[layer].transpose(1, 2))
 
-    def marking_step(self):
-        self.sel.tokens.fill_(CLASSES)
-        self.sel.last.zero_()
-        self.attention_layers(0)
-        self.sel.mark(self.mark_logits, LAST_EPS)
-
-    def solid_step(self, s):
+    def selection(self, step):
+        """Everything of a step but the attention layers: step 0 marks, step 1 + s is solid step s."""
+        if step == 0:
+            self.sel.tokens.fill_(CLASSES)
+            self.sel.last.zero_()
+            self.sel.mark(self.mark_logits, LAST_EPS)
+            return
+        s = step - 1
         self.sel.k.copy_(self.k_tab[s])
         self.sel.committed.copy_(self.com_tab[s])
         self.sel.frac.copy_(self.frac_tab[s])
-        self.attention_layers(s + 1)
         self.sel.run(self.logits[s])
         self.bad_seen |= self.sel.bad
         self.sel.tokens.masked_fill_(self.sel.chosen.view(SLOTS, VOXELS), 1)
         if s == STEPS_PER_WINDOW - 2:
             self.sel.tokens.masked_fill_(self.sel.last, 0)     # finish: deferred voxels become air
 
-    def capture(self):
-        """One HIP graph per step of the window (the marking step, then the 25 solid steps), captured by the
-        engine's `StepGraphs`; returns the callables that replay them."""
+    def step(self, step):
+        self.attention_layers(step)
+        self.selection(step)
+
+    def _graphs(self, body):
         from streamvoxel_amd.stream.engine import StepGraphs
-
-        def body(step):
-            if step == 0:
-                self.marking_step()
-            else:
-                self.solid_step(step - 1)
-
         graphs = StepGraphs(self.dev, body, range(STEPS_PER_WINDOW), warmup=1)
         if not graphs.ok:
             raise RuntimeError('the step graphs could not be captured')
         self.bad_seen.zero_()
         return [graphs.graphs[step].replay for step in range(STEPS_PER_WINDOW)]
+
+    def capture(self):
+        """One HIP graph per step of the window (the marking step, then the 25 solid steps), captured by the
+        engine's `StepGraphs`; returns the callables that replay them."""
+        return self._graphs(self.step)
+
+    def capture_split(self):
+        """The same steps as two graphs each, the attention layers and the rest, so that HIP events between them
+        time the layers inside the step sequence; returns (layers, rest) lists of replay callables."""
+        return self._graphs(self.attention_layers), self._graphs(self.selection)
 
 
 def time_events(fn, reps, warm=3):
@@ -580,8 +585,25 @@ def main():
     log(f'{ms_per_step:.3f} ms/step, bad={bad}')
     value = SLOTS * VOXELS / (STEPS_PER_WINDOW * ms_per_step / 1e3)
 
+    # The attention kernel's average launch inside the step sequence: the same steps replayed as (layers, rest)
+    # graph pairs, HIP events around every layers graph on the stream the graphs launch on (12 launches each; the
+    # gaps between them count too).
+    layer_graphs, rest_graphs = w.capture_split()
+    for i in range(args.warmup):
+        layer_graphs[i % n_graphs]()
+        rest_graphs[i % n_graphs]()
+    torch.cuda.synchronize()
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i in range(args.steps):
+        marks[i][0].record()
+        layer_graphs[i % n_graphs]()
+        marks[i][1].record()
+        rest_graphs[i % n_graphs]()
+    torch.cuda.synchronize()
+    t_layer = sum(a.elapsed_time(b) for a, b in marks) / (args.steps * LAYERS) / 1e3
+    del layer_graphs, rest_graphs
     # Component timings: HIP events around graphs of back-to-back launches on the launching stream.
-    t_layer = time_graph(lambda: w.ctx.attend(0, w.q[1][0], out=w.o[0].transpose(1, 2)), 20)
+    t_layer_alone = time_graph(lambda: w.ctx.attend(0, w.q[1][0], out=w.o[0].transpose(1, 2)), 20)
     w.sel.k.copy_(w.k_tab[0])
     w.sel.committed.copy_(w.com_tab[0])
     w.sel.frac.copy_(w.frac_tab[0])
@@ -662,6 +684,7 @@ def main():
                       unit='TFLOP/s', frac=xattn_tflops / PEAK_BF16_TFLOPS,
                       traffic=profiled_traffic('xattn_fwd_kernel'),
                       flops_per_launch=w.flops_per_layer, avg_launch_us=t_layer * 1e6,
+                      layer0_back_to_back_us=t_layer_alone * 1e6,
                       e4m3_cache_us=t_layer_e4m3 * 1e6, e4m3_cache_TFLOPs=w.flops_per_layer / t_layer_e4m3 / 1e12),
         roofline_select=dict(kernel='svhip_ease_select (entropy + apportion + in-block + fix)', bound='hbm',
                              achieved=select_gbs, peak=PEAK_HBM_GBS, unit='GB/s', frac=select_gbs / PEAK_HBM_GBS,
