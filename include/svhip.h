@@ -195,6 +195,20 @@ int svhip_xattn_fwd_masked(const void* q, const void* k, const void* v, void* o,
                            int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream);
 
 /*
+ * Cross attention in fp32 arithmetic: fp32 q/k/v/o with the layouts and strides of svhip_xattn_fwd (elements, not
+ * bytes; rows 16-byte aligned; V as rows or as V^T), padded with kv_len or packed with cu_seqlens; head_dim 16, 32,
+ * 48 or 64. Every product, sum and exponential is fp32 (the VALU; no rounding of the operands), at the fp32 FMA
+ * rate. A window with no key gives zeros.
+ * Replaces: the masked SDPA of SlotCrossAttention.forward (streamvoxel/stream/engine.py:28-47) as the reference runs
+ * it on fp32 tensors (its CPU path, the single-column configuration).
+ */
+int svhip_xattn_fwd_f32(const float* q, const float* k, const float* v, float* o, const int32_t* kv_len,
+                        const int32_t* cu_seqlens, int64_t B, int64_t H, int64_t Q, int64_t D, int64_t kv_cap,
+                        int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b, int64_t sk_h, int64_t sk_k,
+                        int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d, int64_t so_b, int64_t so_h,
+                        int64_t so_q, float scale, void* stream);
+
+/*
  * AxialRoPE of bf16 activations: x [B,H,N,D] (element (b,h,n,d) at b*sx_b + h*sx_h + n*sx_n + d) -> out (same
  * shape, own strides; out may equal x). D, a multiple of 6, splits into three axes of D/3; in axis t the pair
  * (x[2i], x[2i+1]) (i < D/6 within the axis) turns by phase = positions[b,n,t] * freq[i] (fp32, positions element

@@ -14,7 +14,8 @@ CSRC = os.path.join(HERE, 'csrc')
 LIB = os.path.join(HERE, 'libsvhip.so')
 ARCH = os.environ.get('SVHIP_ARCH', 'gfx950')
 
-SOURCES = ['api.hip', 'entropy.hip', 'select.hip', 'xattn.hip', 'producer.hip', 'norm.hip', 'embed.hip', 'sample.hip']
+SOURCES = ['api.hip', 'entropy.hip', 'select.hip', 'xattn.hip', 'xattn_f32.hip', 'producer.hip', 'norm.hip', 'embed.hip',
+           'sample.hip']
 
 FLAGS = [
     '-O3', '-std=c++17', '-fPIC', '-shared', f'--offload-arch={ARCH}',

@@ -38,10 +38,16 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
     `p_dtype` 'e4m3' (default) takes P . V on the fp8 matrix cores with the softmax weights rounded to e4m3, 'bf16'
     keeps them in bf16 (the reference's in-kernel dequantisation, slower).
     `out` (optional) [B,H,Q,D] bf16 with head_dim contiguous, e.g. a [B,Q,H,D] buffer's transpose(1, 2) view.
+    fp32 query, key and val (head_dim 16, 32, 48 or 64, rows 16-byte aligned, lengths or cu_seqlens) take fp32
+    arithmetic throughout and return fp32 (`svhip_xattn_fwd_f32`, the reference's fp32 SDPA; no key mask).
     Returns out."""
     _lib.require_gpu(query, key, val, lengths, cu_seqlens, k_scale, v_scale, out)
+    if query.dtype == torch.float32:
+        if key_mask is not None or k_scale is not None or v_scale is not None:
+            raise TypeError('fp32 attention takes neither a key mask nor fp8 scales')
+        return _attention_f32(query, key, val, lengths, cu_seqlens, scale, out)
     if query.dtype != torch.bfloat16:
-        raise TypeError('query must be bfloat16')
+        raise TypeError('query must be bfloat16 (or float32 with float32 K/V)')
     B, H, Q, D = query.shape
     if lengths is not None and cu_seqlens is not None:
         raise ValueError('pass at most one of lengths / cu_seqlens')
@@ -105,6 +111,46 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
         _lib.ptr(query), _lib.ptr(kp), _lib.ptr(vp), _lib.ptr(out), code, _lib.ptr(lengths), _lib.ptr(cu_seqlens),
         _lib.ptr(k_scale), _lib.ptr(v_scale), B, H, Q, D, kcap, query.stride(0), query.stride(1), query.stride(2),
         *sk, *sv, out.stride(0), out.stride(1), out.stride(2), scale, _lib.stream_of(query)), 'svhip_xattn_fwd')
+    return out
+
+
+def _attention_f32(query, key, val, lengths, cu_seqlens, scale, out):
+    """fp32 Q/K/V -> fp32 O with fp32 arithmetic throughout (svhip_xattn_fwd_f32): the reference's fp32 SDPA."""
+    if key.dtype != torch.float32 or val.dtype != torch.float32:
+        raise TypeError('fp32 query takes fp32 key and val')
+    B, H, Q, D = query.shape
+    if (lengths is None) == (cu_seqlens is None):
+        raise ValueError('pass exactly one of lengths / cu_seqlens')
+    if query.stride(-1) != 1 or key.stride(-1) != 1:
+        raise ValueError('query and key need a contiguous head_dim')
+    if out is None:
+        out = torch.empty((B, H, Q, D), dtype=torch.float32, device=query.device)
+    if out.shape != (B, H, Q, D) or out.dtype != torch.float32 or out.stride(-1) != 1:
+        raise ValueError('out must be fp32 [B,H,Q,D] with a contiguous head_dim')
+    if cu_seqlens is not None:
+        if key.dim() != 3 or val.dim() != 3:
+            raise ValueError('packed K/V are [H, sum L, D]')
+        if cu_seqlens.dtype != torch.int32 or cu_seqlens.numel() != B + 1:
+            raise ValueError('cu_seqlens must be int32 [B+1]')
+        kcap = key.shape[1]
+        sk = (0, key.stride(0), key.stride(1))
+        sv = (0, val.stride(0), val.stride(1), val.stride(2))
+    else:
+        if key.dim() != 4 or key.shape[:2] != (B, H) or val.shape != key.shape:
+            raise ValueError('padded K/V are [B,H,Kcap,D] like the query')
+        if lengths.dtype != torch.int32 or lengths.numel() != B:
+            raise ValueError('lengths must be int32 [B]')
+        kcap = key.shape[2]
+        sk = (key.stride(0), key.stride(1), key.stride(2))
+        sv = (val.stride(0), val.stride(1), val.stride(2), val.stride(3))
+    if key.shape[-1] != D or val.shape[-1] != D:
+        raise ValueError('head_dim mismatch')
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    lib = _lib.load()
+    _lib.check(lib.svhip_xattn_fwd_f32(
+        _lib.ptr(query), _lib.ptr(key), _lib.ptr(val), _lib.ptr(out), _lib.ptr(lengths), _lib.ptr(cu_seqlens),
+        B, H, Q, D, kcap, query.stride(0), query.stride(1), query.stride(2), *sk, *sv,
+        out.stride(0), out.stride(1), out.stride(2), scale, _lib.stream_of(query)), 'svhip_xattn_fwd_f32')
     return out
 
 

@@ -164,3 +164,22 @@ def test_sampling_tail_refuses_host_tensors():
         sample_chosen(torch.zeros(8, *shape), torch.zeros(shape, dtype=torch.bool), torch.zeros(1, dtype=torch.int64),
                       torch.zeros(1, dtype=torch.int64), torch.zeros(shape, dtype=torch.int16),
                       torch.zeros(1, dtype=torch.int32))
+
+
+def test_argument_errors_of_the_fp32_attention(lib):
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails its host checks first
+    lengths = ctypes.c_void_p(0x2000)
+
+    def f32(D, scale=0.125, kv_len=lengths, cu=None, q=fake, sk_k=64, sv=(64 * 64, 64 * 64, 64, 1)):
+        sizes = [1, 1, 128, D, 64]
+        strides = [128 * 64, 128 * 64, 64, 64 * 64, 64 * 64, sk_k, *sv, 128 * 64, 128 * 64, 64]
+        return lib.svhip_xattn_fwd_f32(q, fake, fake, fake, kv_len, cu, *sizes, *strides, scale, None)
+
+    assert f32(96) == -1 and b'head_dim' in lib.svhip_last_error()
+    assert f32(40) == -1 and b'head_dim' in lib.svhip_last_error()
+    assert f32(64, scale=0.0) == -1 and b'scale' in lib.svhip_last_error()
+    assert f32(64, kv_len=None) == -1 and b'kv_len or cu_seqlens' in lib.svhip_last_error()
+    assert f32(64, cu=lengths) == -1 and b'exclusive' in lib.svhip_last_error()
+    assert f32(64, q=None) == -1 and b'null' in lib.svhip_last_error()
+    assert f32(64, sk_k=66) == -1 and b'16-byte' in lib.svhip_last_error()
+    assert f32(64, sv=(64 * 64, 64 * 64, 2, 3)) == -1 and b'unit stride' in lib.svhip_last_error()

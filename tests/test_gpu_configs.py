@@ -59,15 +59,20 @@ def _fresh_select(dev, logits, batch, k, seed):
 def test_single_column_fp32_attention_and_fresh_select(dev):
     from streamvoxel_amd import synth
     from streamvoxel_amd.stream.attention import attention
-    _case('single column: attention 12x64, Q 1024, 9744 keys, fp32 inputs')
+    _case('single column: attention 12x64, Q 1024, 9744 keys, fp32 inputs and fp32 arithmetic')
     g = torch.Generator().manual_seed(2024)
     q = torch.randn(1, 12, 1024, 64, generator=g) / 8
     k = torch.randn(1, 12, 9744, 64, generator=g) / 8
     v = torch.randn(1, 12, 9744, 64, generator=g) / 8
     lt = torch.tensor([9744], dtype=torch.int32, device=dev)
+    ref = A.cross_attention(q, k, v, [9744])
+    out32 = attention(q.to(dev), k.to(dev), v.to(dev), lengths=lt)       # the configuration's fp32
+    torch.cuda.synchronize()
+    assert out32.dtype == torch.float32
+    _check(out32, ref, 2e-5, 1e-4)
+    # The same column through the bf16 kernel (operands rounded to bf16) holds the bf16 bar.
     out = attention(q.to(dev).bfloat16(), k.to(dev).bfloat16(), v.to(dev).bfloat16(), lengths=lt)
     torch.cuda.synchronize()
-    ref = A.cross_attention(q, k, v, [9744])
     _check(out, ref, 2e-2, 1e-2)
 
     _case('single column: fresh EASE select, k = 2621, 4^3 blocks')
