@@ -584,6 +584,71 @@ __global__ __launch_bounds__(kWG) void fix_kernel(int64_t n, int64_t nb, const i
     return;
   }
   const int64_t d = have > kk ? have - kk : kk - have;
+  if (bnd != nullptr && d <= kBoundary && nb <= kWG) {
+    // One block per thread. Its first d candidates (trim: the last d chosen, top-up: the first d unchosen
+    // selectable; the sentinel where a rank does not exist) are distinct (key << 32 | flat) values in rank order,
+    // so with r = trim ? c : ~c (0 for the sentinel) each thread's list is sorted descending and the d voxels to
+    // flip are the d largest r of all lists. Their chosen state needs no read: the in-block pass chose exactly the
+    // ranks below the quota and only this pass flips them. Phase 1: every wave takes its own d largest by d
+    // wave-wide maxima over its lanes' list heads (no workgroup barrier), into LDS; phase 2: wave 0 merges the
+    // waves' sorted lists the same way and flips the winners.
+    const bool trim = have > kk;
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int64_t j = threadIdx.x;
+    auto rank_of = [&](uint64_t c) __attribute__((always_inline)) { return c == ~0ull ? 0ull : (trim ? c : ~c); };
+    auto wave_max = [&](uint64_t v) __attribute__((always_inline)) {
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const uint64_t o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+      }
+      return v;
+    };
+    uint64_t cand[kBoundary];
+#pragma unroll
+    for (int t = 0; t < kBoundary; ++t) {
+      cand[t] = (j < nb && t < d)
+                    ? rank_of(bnd[(b * nb + j) * 2 * kBoundary + (trim ? kBoundary - 1 - t : kBoundary + t)])
+                    : 0ull;
+    }
+    uint64_t* wtop = reinterpret_cast<uint64_t*>(sh.hist);  // [wave][kBoundary]; the histogram is unused here
+    int head = 0;
+    for (int64_t r = 0; r < d; ++r) {
+      uint64_t cur = 0ull;
+#pragma unroll
+      for (int t = 0; t < kBoundary; ++t) cur = (t == head) ? cand[t] : cur;
+      const uint64_t best = wave_max(cur);
+      if (best != 0ull && cur == best) ++head;  // one lane holds it
+      if (lane == 0) wtop[w * kBoundary + r] = best;
+    }
+    __syncthreads();
+    if (w == 0) {
+      // Lane l: list l % kWaves, positions 4 (l / kWaves) .. + 3 (sorted descending within the lane).
+      static_assert(kWaves * 4 == 64, "phase 2 holds four entries of every wave's list per lane");
+      const int list = lane % kWaves, p0 = 4 * (lane / kWaves);
+      uint64_t c4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c4[i] = p0 + i < d ? wtop[list * kBoundary + p0 + i] : 0ull;
+      int h2 = 0;
+      int64_t done = 0;
+      for (int64_t r = 0; r < d; ++r) {
+        uint64_t cur = 0ull;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cur = (i == h2) ? c4[i] : cur;
+        const uint64_t best = wave_max(cur);
+        if (best == 0ull) break;  // no candidate left (uniform)
+        if (cur == best) {
+          ++h2;
+          const uint64_t c = trim ? best : ~best;
+          ch[static_cast<uint32_t>(c)] = trim ? 0 : 1;
+        }
+        ++done;
+      }
+      if (lane == 0) bad[b] = (done != d) ? 1 : 0;
+    }
+    return;
+  }
   if (bnd != nullptr && d <= kBoundary) {
     // The d voxels to drop (trim: the last d chosen in (key, index) order) or to add (top-up: the first d
     // unchosen selectable ones) are among the boundary candidates: such a voxel has fewer than d voxels of its own
