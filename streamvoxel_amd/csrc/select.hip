@@ -506,10 +506,33 @@ __global__ __launch_bounds__(256) void inblock_wave_kernel(KeySrc src, Geometry 
   if (quota < 0) quota = 0;
   if (quota > legal) quota = legal;
   int rank = 0;
+  if constexpr (B3 == 64) {
+    // One block per wave. Only selectable voxels' ranks are used, and every other voxel holds the sentinel, above
+    // every selectable key: rank = voxels with a smaller key, plus equal keys at lower in-block indices. Each lane's
+    // key is broadcast by readlane (a constant lane, no LDS). The tie pass runs only when there is a tie: without
+    // one the smaller-key counts of the legal selectable voxels are 0 .. legal - 1, whose sum is
+    // legal (legal - 1) / 2.
 #pragma unroll
-  for (int t = 0; t < B3; ++t) {
-    const uint32_t other = __shfl(key, group0 + t, 64);
-    rank += (other < key || (other == key && t < i)) ? 1 : 0;
+    for (int t = 0; t < 64; ++t) {
+      const uint32_t other = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), t));
+      rank += other < key ? 1 : 0;
+    }
+    int64_t sum = masked ? rank : 0;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (sum != legal * (legal - 1) / 2) {
+#pragma unroll
+      for (int t = 0; t < 64; ++t) {
+        const uint32_t other = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), t));
+        rank += (other == key && t < i) ? 1 : 0;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < B3; ++t) {
+      const uint32_t other = __shfl(key, group0 + t, 64);
+      rank += (other < key || (other == key && t < i)) ? 1 : 0;
+    }
   }
   const bool sel = masked && rank < quota;
   chosen[b * n + flat] = sel ? 1 : 0;
