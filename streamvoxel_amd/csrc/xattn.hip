@@ -17,15 +17,17 @@
 // Because O^T's columns are queries too, the per-query rescale and the final 1/l are lane-local.
 //
 // The softmax is VALU-bound at head_dim 64 (one exp per score against 2 x 64 MACs), so per score it costs one
-// FMA, one exp, half a bf16 pack and one fp32 add (the row sum; v_dot2c_f32_bf16 over the packed P would need half
-// the instructions but does not co-execute with the matrix cores), and no max:
+// FMA, one exp and half a bf16 pack on the VALU, and no max and no add: the row sum comes from the matrix cores
+// (two v_mfma_f32_16x16x32_bf16 per 32-key half over the packed P with a ones pattern, a sixteenth of the half's
+// matrix-core time, in place of 15 fp32 adds per lane; v_dot2c_f32_bf16 would not co-execute with the matrix
+// cores):
 //   * Q enters the score product as given (bf16) and the fp32 scores are scaled by sl2 = scale * log2(e) (and the
 //     e4m3 K scale) inside the exponent's FMA, P = exp2(fma(S, sl2, -m)) with m the running max in log2 units, so
 //     the only roundings of the query are the caller's.
-//   * P is formed against the running max m as it stands. The half's row sum tells whether m still bounds the
-//     half's scores: only a sum above 2^20 (and always the window's first half) makes the wave take the half's
-//     max (16 three-input maxes and the partner's over v_permlane32_swap), raise m, rescale O and l and redo P
-//     shifted by the rise. P may thus reach 2^20, harmless in fp32 sums and bf16 P; O and l always share m, so
+//   * P is formed against the running max m as it stands. The half's row sum (read back from the matrix cores
+//     before the second product is issued) tells whether m still bounds the half's scores: only a sum above 2^20
+//     (and always the window's first half) makes the wave take the half's max (16 three-input maxes and the
+//     partner's over v_permlane32_swap), raise m, rescale O and l and redo P and its sum shifted by the rise. P may thus reach 2^20, harmless in fp32 sums and bf16 P; O and l always share m, so
 //     O / l does not depend on where m sits.
 //   * With direct staging and head_dim below 32 DT (the shipped 48) V^T row D, a padding row, holds ones: the
 //     second product then accumulates the row sum of the bf16 P in O^T row D, and the VALU drops the adds. The
@@ -507,6 +509,8 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
   static_assert(!ONES || !FULLK, "a full-width head has no padding row");
   static_assert(!PV8 || (FP8 && !DIRECT && !KMASK), "the e4m3 second product stages e4m3 K/V through registers");
   static_assert(!VD8 || (PV8 && VT), "direct e4m3 V^T loads serve the e4m3 second product");
+  // bf16 P with no padding row for the row sum: the matrix cores form it from the packed P (see onesb).
+  constexpr bool MSUM = !ONES && !PV8;
   constexpr int kSubTiles = Width<DT>::kSubTiles;
   // V^T tile: 32 DT rows of 64 keys, bf16 (kRow elements a row) or e4m3 (kRow8 bytes a row).
   constexpr int kVTile = PV8 ? 32 * DT * kRow8 / 2 : 32 * DT * kRow;
@@ -668,11 +672,20 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
     const int x = (lane == 0 || lane == 32 || lane == 20 || lane == 52) ? 0x38383838 : 0;  // e4m3 1.0
     ones16 = i32x8_t{x, x, x, x, x, x, x, x};
   }
+  // bf16 P at head_dim 32 DT (MSUM): the half's row sums from two v_mfma_f32_16x16x32_bf16 over the packed P with
+  // the same ones pattern in bf16 (a 16x16x32 B operand reads lane l of P as column l % 16, k group l / 16, as
+  // above), so query c's sum is entry 0 of lane c and the VALU adds no P.
+  [[maybe_unused]] bf16x8_t onesb;
+  if constexpr (MSUM) {
+    const bool one = lane == 0 || lane == 32 || lane == 20 || lane == 52;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) onesb[i] = one ? static_cast<__bf16>(1.0f) : static_cast<__bf16>(0.0f);
+  }
   f32x16_t o[DT];  // O^T tiles: d in [32 j, 32 j + 32)
 #pragma unroll
   for (int j = 0; j < DT; ++j) o[j] = f32x16_t{0};
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
-  float l = 0.f;                // row-sum partial of this lane's keys
+  float l = 0.f;                // MSUM: query c's row sum in lane c (lanes 32-63 hold 0)
   bool first = true;            // uniform: the window's first half always takes the max
 
   // Full block `blk` into (sK, sV): issued now, complete at the next vmem wait (direct) or at `stage_commit`
@@ -834,12 +847,11 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
       // P^T = exp2(sl2 S^T - m) against the running max m as it stands, as B operands: k-step ks (keys
       // 32 t + 16 ks + 8 hh + 0..7) = entries 8 ks + 0..7. On the window's first half m is -inf and the fast pass
       // gives inf or NaN, which the slow path always taken there replaces.
-      // The row sum is taken over the fp32 P (unless the matrix cores form it).
+      // The row sum is taken over the packed (bf16-rounded) P that the second product reads, so a dominant key's
+      // rounding cancels in O / l.
       bf16x8_t pb[2];
-      float lb;
       auto exps = [&]() __attribute__((always_inline)) {
         const float nm = -m;
-        float pair[8];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -847,14 +859,17 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
             f32x2_t two = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j], sl2, nm)),
                            __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j + 1], sl2, nm))};
             const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
-            pair[4 * ks + j / 2] = two[0] + two[1];
             pb[ks][j] = c[0];
             pb[ks][j + 1] = c[1];
           }
         }
-        // Row sum over the fp32 P as a tree of fp32 adds (v_dot2c_f32_bf16, the packed alternative, does not
-        // co-execute with the matrix cores on gfx950).
-        lb = ((pair[0] + pair[1]) + (pair[2] + pair[3])) + ((pair[4] + pair[5]) + (pair[6] + pair[7]));
+      };
+      // Without the ones row (MSUM): the half's row sums over the packed P from the matrix cores (query c's in
+      // lane c, 0 in lanes 32-63); the VALU adds no P.
+      [[maybe_unused]] auto half_sum = [&]() __attribute__((always_inline)) {
+        f32x4_t h = __builtin_amdgcn_mfma_f32_16x16x32_bf16(onesb, pb[0], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        h = __builtin_amdgcn_mfma_f32_16x16x32_bf16(onesb, pb[1], h, 0, 0, 0);
+        return h[0];
       };
       // The slow path: the half's max (raw scores; the chain opens with a compiler-visible v_med3_f32, med3(a, b,
       // FLT_MAX) = max(a, b) for scores below +inf, before which the compiler inserts the wait states a VALU read
@@ -894,13 +909,17 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
         const float mx = half_max();
         exps();
         if (first || __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, sl2, -m) > kMaxHigh) != 0ull) raise(mx);
-      } else {
+      } else if constexpr (MSUM) {
         // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN) some
         // score passed m by about 20 (log2 units). Only then (and on the window's first half, where m is -inf)
         // is the slow path taken.
         exps();
-        if (first || __builtin_amdgcn_ballot_w64(!(lb <= kSumHigh)) != 0ull) raise(half_max());
-        l += lb;
+        float hs = half_sum();
+        if (first || __builtin_amdgcn_ballot_w64(!(hs <= kSumHigh)) != 0ull) {
+          raise(half_max());
+          hs = half_sum();
+        }
+        l += hs;
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
@@ -1032,8 +1051,10 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDir
                                                      false);
     lsum = __int_as_float(sw[0]);
   } else {
+    static_assert(MSUM, "the row sum comes from the ones row, the fp8 ones pattern or the bf16 one");
+    // Query c's sum is l of lane c (lane half 0; half 1 holds 0).
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(lsum), __float_as_int(lsum), false, false);
-    lsum = __int_as_float(sw[0]) + __int_as_float(sw[1]);
+    lsum = __int_as_float(sw[0]);
   }
   // A query with no attended key (only possible with a key mask) has l = 0 and O = 0: it gets zeros.
   const float inv = (KMASK && !(lsum > 0.f)) ? 0.f : vscale / lsum;
