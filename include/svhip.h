@@ -157,7 +157,9 @@ int svhip_ease_select_patches(const void* logits, int dtype, int64_t classes, in
  * Cross attention over per-window, variable-length cached keys:
  *   O[b,h,q,:] = sum_{j < L_b} softmax_j(scale * Q[b,h,q,:] . K[b,h,j,:]) V[b,h,j,:]
  * with L_b = min(kv_len[b], kv_cap) (device int32 [B]) or, for the packed layout, cu_seqlens[b+1] - cu_seqlens[b] with key j of
- * window b at row cu_seqlens[b] + j. A window with L_b = 0 gets zeros.
+ * window b at row cu_seqlens[b] + j. A window with L_b = 0 gets zeros. cu_seqlens stays on the device and is
+ * read as given (no host check, which would need a synchronisation): it must be non-decreasing with every row
+ * inside the packed K/V, as for the reference's packed attention.
  * Q, O: bf16, element (b,h,q,d) at b*s?_b + h*s?_h + q*s?_q + d. K: element (b,h,j,d) at
  * b*sk_b + h*sk_h + row*sk_k + d; V: at b*sv_b + h*sv_h + row*sv_k + d*sv_d, where either sv_d == 1 (rows of
  * head_dim, the reference layout) or sv_k == 1 (V stored transposed, keys contiguous: the fast staging path);
