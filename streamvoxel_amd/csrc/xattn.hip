@@ -502,7 +502,7 @@ enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2, kRegisterFull = 3 };
 // PV8: e4m3 K/V take the second product on the fp8 matrix cores (see the comment at the top).
 // VD8: with PV8, V^T takes direct loads for full blocks (e4m3 rows of 16-byte aligned runs).
 template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false, bool PV8 = false, bool VD8 = false>
-__global__ __launch_bounds__(kThreads, (DT == 2 && VT && (FP8 || STAGING == kDirect || STAGING == kDirectFull)) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
+__global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
   constexpr bool DIRECT = STAGING == kDirect || STAGING == kDirectFull;
   constexpr bool FULLK = STAGING == kDirectFull || STAGING == kRegisterFull;  // head_dim 32 DT
   static_assert(!KMASK || !DIRECT, "the key-mask path stages through registers");
