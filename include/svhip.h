@@ -23,8 +23,8 @@
 extern "C" {
 #endif
 
-/* SVHIP_FP8_E4M3_PBF16: e4m3 K/V whose attention keeps P in bf16 (see svhip_xattn_fwd). */
-enum svhip_dtype { SVHIP_F32 = 0, SVHIP_BF16 = 1, SVHIP_FP8_E4M3 = 3, SVHIP_FP8_E4M3_PBF16 = 4 };
+/* SVHIP_FP8_E4M3_PFP8: e4m3 K/V whose attention rounds P to e4m3 for the fp8 matrix cores (see svhip_xattn_fwd). */
+enum svhip_dtype { SVHIP_F32 = 0, SVHIP_BF16 = 1, SVHIP_FP8_E4M3 = 3, SVHIP_FP8_E4M3_PFP8 = 5 };
 
 enum svhip_status { SVHIP_OK = 0, SVHIP_EINVAL = -1, SVHIP_ELAUNCH = -2, SVHIP_EWORKSPACE = -3 };
 
@@ -165,10 +165,12 @@ int svhip_ease_select_patches(const void* logits, int dtype, int64_t classes, in
  * head_dim, the reference layout) or sv_k == 1 (V stored transposed, keys contiguous: the fast staging path);
  * row = j, or cu_seqlens[b] + j in the packed layout (sk_b / sv_b are then ignored). kv_dtype SVHIP_BF16, or
  * e4m3 (OCP e4m3fn bytes) with per-(window, head) fp32 dequantisation scales k_scale/v_scale [B,H]:
- * SVHIP_FP8_E4M3 takes P . V on the fp8 matrix cores with P rounded to e4m3 (relative rounding 2^-4 on every
- * softmax weight, the row sum taken over the rounded weights), SVHIP_FP8_E4M3_PBF16 keeps P in bf16 on the bf16
- * matrix cores (the reference's in-kernel dequantisation). Q . K^T is a bf16 product of the exactly decoded keys
- * in both. head_dim: a multiple of 8 up to 128 (zero-padded inside the kernel to 64, 96 or 128: the 384-wide
+ * SVHIP_FP8_E4M3 decodes K and V exactly to bf16 in the kernel and keeps P in bf16 (the reference's in-kernel
+ * dequantisation with fp32 accumulation: within 5e-2 of fp32 attention over the unquantised K/V);
+ * SVHIP_FP8_E4M3_PFP8, an opt-in outside that bar, takes P . V on the fp8 matrix cores with P rounded to e4m3 (a
+ * relative rounding of 2^-4 on every softmax weight, the row sum taken over the rounded weights; up to about 8e-2
+ * on rows whose logits have a standard deviation of 4). Q . K^T is a bf16 product of the exactly decoded keys in
+ * both. head_dim: a multiple of 8 up to 128 (zero-padded inside the kernel to 64, 96 or 128: the 384-wide
  * model's 48, the 768-wide model's 96). fp32 accumulation.
  * scale: the softmax scale, > 0 (the reference uses 1/sqrt(head_dim)).
  * Replaces: flex_attention over PackedKeys' block mask in cross_flex (streamvoxel/stream/fast_ops.py:104-108,

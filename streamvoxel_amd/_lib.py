@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, 'libsvhip.so')
 
-SVHIP_F32, SVHIP_BF16, SVHIP_FP8_E4M3, SVHIP_FP8_E4M3_PBF16 = 0, 1, 3, 4
+SVHIP_F32, SVHIP_BF16, SVHIP_FP8_E4M3, SVHIP_FP8_E4M3_PFP8 = 0, 1, 3, 5
 SVHIP_LEL_LAYER, SVHIP_LEL_BAND, SVHIP_LEL_COLUMN = 0, 1, 2
 
 _c_i64, _c_i32, _c_p, _c_sz, _c_f, _c_d = (ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t,
@@ -119,3 +119,20 @@ def dtype_code(dtype):
     if dtype == torch.bfloat16:
         return SVHIP_BF16
     raise TypeError(f'unsupported logits dtype {dtype} (float32 or bfloat16)')
+
+
+def byte_span(t):
+    """[first, last) device byte addresses a tensor's elements occupy (its strides taken into account)."""
+    if t.numel() == 0:
+        return (t.data_ptr(), t.data_ptr())
+    extent = sum((n - 1) * abs(s) for n, s in zip(t.shape, t.stride())) + 1
+    low = t.data_ptr() + sum((n - 1) * s for n, s in zip(t.shape, t.stride()) if s < 0) * t.element_size()
+    return (low, low + extent * t.element_size())
+
+
+def overlaps(a, b):
+    """True when the elements of two tensors may share memory (their byte spans intersect)."""
+    if a is None or b is None:
+        return False
+    (a0, a1), (b0, b1) = byte_span(a), byte_span(b)
+    return a0 < b1 and b0 < a1

@@ -18,6 +18,6 @@ void clear_error() { g_error[0] = '\0'; }
 
 }  // namespace svhip
 
-extern "C" int svhip_version(void) { return 100; }
+extern "C" int svhip_version(void) { return 200; }
 
 extern "C" const char* svhip_last_error(void) { return svhip::g_error; }

@@ -34,14 +34,14 @@
 //     trigger becomes the half's own max (8 three-input maxes): a score more than 20 above m.
 //   * key masking runs only in the last, partial block; padding keys are staged as zeros.
 //
-// e4m3 K/V (PV8, the default for an e4m3 cache): the second product runs on the fp8 matrix cores,
+// e4m3 K/V with PV8 (SVHIP_FP8_E4M3_PFP8): the second product runs on the fp8 matrix cores,
 // v_mfma_f32_32x32x64_f8f6f4 over a whole 64-key block per output tile (half the bf16 product's matrix-core time).
 // V^T stays e4m3 in LDS (its per-head scale applied at the end); P is formed 2^4 above the running max and rounded
 // to e4m3 as it is packed, a lane's 32 weights being exactly the B operand's 32 k slots (K rows are placed by
 // pv8_row for that); the row sum is taken over the rounded weights (decoded, or from the ones row), so a dominant
 // key's rounding cancels in O / l. The score product stays bf16 over the exactly decoded keys. The price is a 2^-4
-// relative rounding of every softmax weight; SVHIP_FP8_E4M3_PBF16 keeps P in bf16 (PV8 off) for the reference's
-// numerics.
+// relative rounding of every softmax weight, so PV8 is an opt-in (SVHIP_FP8_E4M3_PFP8); SVHIP_FP8_E4M3, the e4m3
+// cache's default, keeps P in bf16 (PV8 off): the reference's in-kernel dequantisation.
 //
 // Staging. An LDS tile holds 64 rows of 128 bytes, the eight 16-byte chunks of row r XOR-swizzled by (r / 2) % 8
 // so that the 16-byte operand reads are bank-conflict-free; a K row is one key's head_dim, a V^T row one
@@ -687,6 +687,10 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
   float m = -INFINITY;          // stored running max (log2 units), shared by O and l
   float l = 0.f;                // MSUM: query c's row sum in lane c (lanes 32-63 hold 0)
   bool first = true;            // uniform: the window's first half always takes the max
+  // KMASK: the lane's query has seen no attended key yet (m is then a placeholder 0, O and l are 0); every half
+  // takes the max while any lane of the wave is in that state, so the first half with an attended key sets m to
+  // that key's score however far below 0 it lies.
+  [[maybe_unused]] bool placeholder = false;
 
   // Full block `blk` into (sK, sV): issued now, complete at the next vmem wait (direct) or at `stage_commit`
   // (registers, prefetched into `st`).
@@ -733,6 +737,25 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
   // One key block from (Ks, Vt), as two 32-key halves that each run the whole online-softmax step (scores,
   // running max, exponentials, second product): a half's scores take 16 registers, which keeps four waves per
   // SIMD resident. MASKED: the partial block (keys >= L masked out).
+  // PV8: the fp8 products write O^T over 16 passes, the final rows last, and this toolchain (ROCm 7.2 hipcc)
+  // places too few wait states between them and the first VALU reads of O (the rows written last were read stale
+  // on the GPU, in windows whose last block is the partial one). Every VALU read of O waits here explicitly first:
+  // after the window's last block, and before the rescale of a raise (between blocks the next block's score
+  // products and exponentials usually come first, but that distance is the compiler's choice). 64 wait states; the
+  // asm takes O as an operand so that no read of it moves above the wait.
+  auto settle = [&]() __attribute__((always_inline)) {
+#define SVHIP_WAIT64 "s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+    if constexpr (PV8 && DT == 2) {
+      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(rowsum));
+    } else if constexpr (PV8 && DT == 3) {
+      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(rowsum));
+    } else if constexpr (PV8) {
+      static_assert(DT == 4, "head widths are 2, 3 or 4 tiles");
+      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(rowsum));
+    }
+#undef SVHIP_WAIT64
+  };
+
   // PV8, the softmax of half t of a block, packed as it is formed: P = exp2(fma(S, sl2, 4 - m)), the running max
   // lifted by 2^4 so that P of scores from 2^-10 of the max upwards keeps a normal e4m3 value, straight into the
   // e4m3 B operand (v_cvt_pk_fp8_f32, round to nearest even). The lazy max with an e4m3 bound: a half whose largest
@@ -756,6 +779,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
       }
     };
     auto raise8 = [&](float mx) __attribute__((always_inline)) {
+      settle();
       first = false;
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
       const float mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
@@ -883,11 +907,17 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
         const float mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
         const float cand = mr * sl2;
-        float mn = cand > m ? cand : m;
+        float mn = (cand > m || (KMASK && placeholder)) ? cand : m;
         // Only with a key mask can a query have seen no attended key yet (every score -inf): its running max is
-        // then set to 0, with O and l still 0, so that later scores are taken against a finite bias.
-        if (KMASK) mn = mn == -INFINITY ? 0.f : mn;
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first half
+        // then set to 0, with O and l still 0, so that later scores are taken against a finite bias, and the lane is
+        // marked so that its first attended key replaces that bias (alpha 0: O and l hold nothing to rescale).
+        bool was_placeholder = false;
+        if (KMASK) {
+          was_placeholder = placeholder;
+          placeholder = mn == -INFINITY;
+          mn = placeholder ? 0.f : mn;
+        }
+        const float alpha = was_placeholder ? 0.f : __builtin_amdgcn_exp2f(m - mn);  // 0 on the first half
         m = mn;
         l *= alpha;
 #pragma unroll
@@ -908,14 +938,17 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
         // below 2^kMaxHigh); the row sum accumulates in O^T row D.
         const float mx = half_max();
         exps();
-        if (first || __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, sl2, -m) > kMaxHigh) != 0ull) raise(mx);
+        if (first || __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, sl2, -m) > kMaxHigh || (KMASK && placeholder)) !=
+                         0ull) {
+          raise(mx);
+        }
       } else if constexpr (MSUM) {
         // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN) some
         // score passed m by about 20 (log2 units). Only then (and on the window's first half, where m is -inf)
         // is the slow path taken.
         exps();
         float hs = half_sum();
-        if (first || __builtin_amdgcn_ballot_w64(!(hs <= kSumHigh)) != 0ull) {
+        if (first || __builtin_amdgcn_ballot_w64(!(hs <= kSumHigh) || (KMASK && placeholder)) != 0ull) {
           raise(half_max());
           hs = half_sum();
         }
@@ -959,24 +992,6 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
   };
   using Full = std::false_type;
   using Partial = std::true_type;
-  // After the window's last block: the fp8 products write O^T over 16 passes, the final rows last, and this
-  // toolchain places too few wait states between them and the first VALU reads of O (the rows written last were
-  // read stale on the GPU, in windows whose last block is the partial one). The reads wait here explicitly, right
-  // after the products and before any copy of O: 64 wait states, once per window. The asm takes O as an operand
-  // so that no read of it moves above the wait. (Between blocks the next block's score products and exponentials
-  // come first, far more than the wait a 16-pass product needs.)
-  auto settle = [&]() __attribute__((always_inline)) {
-#define SVHIP_WAIT64 "s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-    if constexpr (PV8 && DT == 2) {
-      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(rowsum));
-    } else if constexpr (PV8 && DT == 3) {
-      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(rowsum));
-    } else if constexpr (PV8) {
-      static_assert(DT == 4, "head widths are 2, 3 or 4 tiles");
-      asm volatile(SVHIP_WAIT64 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(rowsum));
-    }
-#undef SVHIP_WAIT64
-  };
 
   // Full block blk from (Ks, Vt) while full block blk + 1 is staged into (nK, nV).
   auto full_step = [&](int blk, const uint16_t* Ks, const uint16_t* Vt, uint16_t* nK, uint16_t* nV) __attribute__((always_inline)) {
@@ -1142,10 +1157,10 @@ static int xattn_impl(const void* q, const void* k, const void* v, void* o, int 
   SVHIP_REQUIRE(D >= 8 && D <= kMaxD && D % 8 == 0, "%s: head_dim %lld unsupported (multiple of 8, <= %d)", name,
                 (long long)D, kMaxD);
   SVHIP_REQUIRE(scale > 0.f && scale < 3.0e38f, "%s: softmax scale must be positive and finite", name);
-  SVHIP_REQUIRE(kv_dtype == SVHIP_BF16 || kv_dtype == SVHIP_FP8_E4M3 || kv_dtype == SVHIP_FP8_E4M3_PBF16,
+  SVHIP_REQUIRE(kv_dtype == SVHIP_BF16 || kv_dtype == SVHIP_FP8_E4M3 || kv_dtype == SVHIP_FP8_E4M3_PFP8,
                 "%s: kv dtype %d unsupported", name, kv_dtype);
   const bool fp8 = kv_dtype != SVHIP_BF16;
-  const bool pv8 = kv_dtype == SVHIP_FP8_E4M3;
+  const bool pv8 = kv_dtype == SVHIP_FP8_E4M3_PFP8;
   SVHIP_REQUIRE(!fp8 || (k_scale && v_scale), "%s: fp8 K/V need k_scale and v_scale", name);
   SVHIP_REQUIRE(!kv_mask || !fp8, "%s: the key mask takes bf16 K/V", name);
   SVHIP_REQUIRE(sv_k == 1 || sv_d == 1, "%s: V needs a unit stride along keys or head_dim", name);

@@ -19,26 +19,30 @@ def _bytes(mask):
     return mask.contiguous().view(torch.uint8)
 
 
-_TOP_OUT = {}
+def _check_out(out, shape, device, *inputs):
+    """`out` must be a contiguous bool tensor of `shape` on `device` that shares no memory with an input (the
+    kernels read their inputs while they write the output)."""
+    if out.dtype != torch.bool or tuple(out.shape) != tuple(shape) or out.device != device:
+        raise ValueError(f'out must be a bool tensor of shape {tuple(shape)} on {device}')
+    if not out.is_contiguous():
+        raise ValueError('out must be contiguous')
+    if any(_lib.overlaps(out, t) for t in inputs):
+        raise ValueError('out shares memory with an input; pass a separate buffer')
 
 
-def _top_out(shape, device):
-    key = (torch.device(device), tuple(shape))
-    out = _TOP_OUT.get(key)
-    if out is None:
-        out = _TOP_OUT[key] = torch.empty(shape, dtype=torch.bool, device=device)
-    return out
-
-
-def top_mask(scores, eligible, count):
+def top_mask(scores, eligible, count, out=None):
     """The `count` largest scores among `eligible`, ties to the lower flat index
-    (streamvoxel/sampling/block_quota.py:4-12). `count` is a host int or a 0-dim device int64 tensor. The result
-    lives in a buffer of this module that the next call of the same shape on the device overwrites (clone it to
-    keep it); calls with contiguous fp32 scores and a device int64 count allocate nothing."""
-    _lib.require_gpu(scores, eligible)
+    (streamvoxel/sampling/block_quota.py:4-12). `count` is a host int or a 0-dim device int64 tensor (no host
+    read). Returns a new bool tensor, as the reference does; `out` (a bool tensor of eligible's shape that shares no
+    memory with the inputs) takes the result instead, and then a call with contiguous fp32 scores, a contiguous
+    mask and a device int64 count allocates nothing."""
+    _lib.require_gpu(scores, eligible, out)
     s = scores.contiguous().float().reshape(-1)
     e = _bytes(eligible).reshape(-1)
-    out = _top_out(eligible.shape, scores.device)
+    if out is None:
+        out = torch.empty(eligible.shape, dtype=torch.bool, device=scores.device)
+    else:
+        _check_out(out, eligible.shape, scores.device, s, e)
     lib = _lib.load()
     if torch.is_tensor(count):
         cnt = count.to(device=scores.device, dtype=torch.int64).reshape(1)
@@ -81,15 +85,19 @@ def quota_select_into(score, mask, k, b, pos, frac, n_total, committed, chosen, 
         _lib.ptr(workspace.buffer), workspace.buffer.numel(), _lib.stream_of(score)), 'svhip_quota_select')
 
 
-class _SelectBuffers:
-    """Per (device, window shape, block size): the workspace, the outputs and the per-call scalars of the one-window
-    functions below, so that repeated calls allocate nothing (the reference keeps the same buffers static,
-    fast_ops.py:501-510)."""
+class SelectBuffers:
+    """Caller-owned device buffers of the one-window selection functions below: the workspace, the per-call
+    scalars (k, frac, committed), the `bad` flag and the block positions, for windows of `shape` with block size
+    `b`. Passed as `buffers=` together with `out=`, a call allocates nothing (the reference keeps such buffers on its
+    slot, fast_ops.py:501-510). The object is the caller's: calls that share one must not run concurrently on
+    different streams."""
 
     def __init__(self, shape, b, device):
+        shape = tuple(int(s) for s in shape)
+        b = int(b)
         nb = (shape[0] // b) * (shape[1] // b) * (shape[2] // b)
+        self.shape, self.b, self.device = shape, b, torch.device(device)
         self.ws = QuotaWorkspace(1, shape, b, device)
-        self.chosen = torch.empty((1, *shape), dtype=torch.bool, device=device)
         self.bad = torch.empty(1, dtype=torch.bool, device=device)
         self.k = torch.empty(1, dtype=torch.int64, device=device)
         self.committed = torch.empty(1, dtype=torch.int64, device=device)
@@ -97,16 +105,17 @@ class _SelectBuffers:
         self.pos = torch.empty(nb, dtype=torch.int64, device=device)
         self.arange = torch.arange(nb, dtype=torch.int64, device=device)
 
+    def fits(self, shape, b, device):
+        return self.shape == tuple(shape) and self.b == int(b) and self.device == torch.device(device)
 
-_BUFFERS = {}
 
-
-def _buffers(shape, b, device):
-    key = (torch.device(device), tuple(shape), int(b))
-    buf = _BUFFERS.get(key)
-    if buf is None:
-        buf = _BUFFERS[key] = _SelectBuffers(tuple(shape), int(b), device)
-    return buf
+def _select_buffers(buffers, shape, b, device):
+    if buffers is None:
+        return SelectBuffers(shape, b, device)
+    if not buffers.fits(shape, b, device):
+        raise ValueError(f'buffers are for {buffers.shape} windows, block {buffers.b} on {buffers.device}; the call '
+                         f'has {tuple(shape)}, block {b} on {device}')
+    return buffers
 
 
 def _set_scalar(dst, v):
@@ -119,30 +128,35 @@ def _set_scalar(dst, v):
     return dst
 
 
-def quota_select(score, mask, k, b, pos, frac, n_total, committed):
+def quota_select(score, mask, k, b, pos, frac, n_total, committed, out=None, buffers=None):
     """One window, like `quota_select_nosync` (streamvoxel/stream/fast_ops.py:442-473): k, frac and committed are
     host numbers or 0-dim device tensors (committed None: derived on the device as sum(n_total) - sum(mask)); pos
-    is the inverse block order. The returned mask lives in a buffer of
-    this module that the next call for the same (device, window shape, block size) overwrites, as the reference's
-    static `chosen` is (clone it to keep it); with fp32 contiguous scores, int64 pos / n_total and a contiguous
-    mask, a call allocates nothing."""
-    _lib.require_gpu(score, mask)
+    is the inverse block order. Returns a new bool mask, as the reference does. `out` (bool, the window's shape,
+    no memory shared with an input) takes the result instead, and `buffers` (a `SelectBuffers` of this geometry)
+    holds the workspace and scalars; with both, fp32 contiguous scores, int64 pos / n_total and a contiguous mask,
+    a call allocates nothing."""
+    _lib.require_gpu(score, mask, out)
     device = score.device
     shape = tuple(score.shape)
-    buf = _buffers(shape, b, device)
-    quota_select_into(score.contiguous().float().reshape(1, *shape), mask.contiguous().reshape(1, *shape),
-                      _set_scalar(buf.k, k), b, pos.to(device=device, dtype=torch.int64).reshape(1, -1),
+    buf = _select_buffers(buffers, shape, b, device)
+    s = score.contiguous().float().reshape(1, *shape)
+    m = mask.contiguous().reshape(1, *shape)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.bool, device=device)
+    else:
+        _check_out(out, shape, device, s, m)
+    quota_select_into(s, m, _set_scalar(buf.k, k), b, pos.to(device=device, dtype=torch.int64).reshape(1, -1),
                       _set_scalar(buf.frac, frac), n_total.to(device=device, dtype=torch.int64).reshape(1, -1),
-                      None if committed is None else _set_scalar(buf.committed, committed), buf.chosen, buf.bad,
-                      buf.ws)
-    return buf.chosen[0]
+                      None if committed is None else _set_scalar(buf.committed, committed), out.view(1, *shape),
+                      buf.bad, buf.ws)
+    return out
 
 
-def block_quota_select(score, mask, k, b, order, frac, n_total):
+def block_quota_select(score, mask, k, b, order, frac, n_total, out=None, buffers=None):
     """Exactly k voxels of `mask`, balanced over b^3 blocks (streamvoxel/sampling/block_quota.py:20-38). `order` is
-    the seeded block order; the committed count is derived on the device as sum(n_total) - sum(mask). The result
-    is the reused buffer of `quota_select`."""
+    the seeded block order; the committed count is derived on the device as sum(n_total) - sum(mask). Returns a
+    new bool mask (or fills `out`; `buffers` as for `quota_select`)."""
     _lib.require_gpu(score, mask, order, n_total)
-    buf = _buffers(tuple(score.shape), b, score.device)
+    buf = _select_buffers(buffers, tuple(score.shape), b, score.device)
     pos = buf.pos.scatter_(0, order.to(torch.int64), buf.arange)
-    return quota_select(score, mask, k, b, pos, frac, n_total, None)
+    return quota_select(score, mask, k, b, pos, frac, n_total, None, out=out, buffers=buf)

@@ -142,6 +142,21 @@ class StepGraphs:
         return self.outputs[key]
 
 
+PATCHIFY = ('gather', 'conv')
+ATTENTION = ('flex', 'sdpa')
+KV_DTYPES = ('bf16', 'fp8')
+
+
+def check_engine_options(patchify, attention, compile, kv_dtype='bf16'):
+    """The engine's options, validated as the reference does (fast_ops.py:170-171): ValueError for unknown ones."""
+    if patchify not in PATCHIFY or attention not in ATTENTION:
+        raise ValueError('patchify must be gather|conv and attention flex|sdpa')
+    if compile not in (False, True, 'emulate'):
+        raise ValueError("compile must be False, True or 'emulate'")
+    if kv_dtype not in KV_DTYPES:
+        raise ValueError(f'kv_dtype must be one of {KV_DTYPES}')
+
+
 class SlotEngine:
     """`batch` window slots of the model `model` (the reference's StreamingControlNet / CompactStreamingControlNet,
     or a module with the same attributes: backbone, control, cross, zero, optional layer_map) for windows of
@@ -153,19 +168,15 @@ class SlotEngine:
     without one, `load_slot` takes an `Encoded` (or a (prefix, local, positions) tuple) itself.
     `kv_dtype` 'bf16' (the reference's cache) or 'fp8' (e4m3 with per-(window, head) scales). `concurrent` runs the
     control branch on its own stream inside the step. `patchify`, `attention` and `compile` are the reference's
-    option names: 'gather' is the only patchify (bit for bit the reference's gather patchify); 'flex' and 'sdpa'
-    both run the HIP attention kernel over the slots' key lengths (each is masked attention over the valid keys);
-    `compile` is accepted and changes nothing (the blocks run on HIP kernels that round where eager autocast
-    does)."""
+    option names (fast_ops.py:168-171): 'gather' and 'conv' both run the HIP gather patchify, bit for bit the
+    reference's embedding-bag form, which computes the one-hot Conv3d's sum (the reference's own test,
+    tests/stream/test_live_fast_ops.py:14-21, holds the two equal); 'flex' and 'sdpa' both run the HIP attention
+    kernel over the slots' key lengths (each is masked attention over the valid keys); `compile` is accepted and
+    changes nothing (the blocks run on HIP kernels that round where eager autocast does)."""
 
     def __init__(self, model, spec, device, batch, l1_cap, l2_cap, *, patchify='gather', attention='flex',
                  compile=False, capture=True, encoder=None, kv_dtype='bf16', concurrent=True):
-        if patchify != 'gather':
-            raise ValueError("patchify must be 'gather' (the HIP gather patchify; the one-hot conv is not built)")
-        if attention not in ('flex', 'sdpa'):
-            raise ValueError("attention must be 'flex' or 'sdpa'")
-        if compile not in (False, True, 'emulate'):
-            raise ValueError("compile must be False, True or 'emulate'")
+        check_engine_options(patchify, attention, compile, kv_dtype)
         self.device = torch.device(device)
         if self.device.type != 'cuda':
             raise RuntimeError('SlotEngine runs on a HIP device; there is no CPU path')

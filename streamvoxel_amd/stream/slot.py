@@ -30,6 +30,16 @@ from streamvoxel_amd.stream.patches import PatchLogits
 from streamvoxel_amd.stream.sampler import sample_chosen
 
 ORDER_SEED_OFFSET = 9173
+ENTROPY_NAMES = ('torch', 'triton', 'hip')
+SAMPLERS = ('multinomial', 'philox')
+
+
+def check_slot_options(entropy, sampler):
+    """The slot's options, validated as the reference does (fast_ops.py:494-495): ValueError for unknown names."""
+    if entropy not in ENTROPY_NAMES:
+        raise ValueError(f'entropy must be one of {ENTROPY_NAMES} (each runs the HIP entropy kernel)')
+    if sampler not in SAMPLERS:
+        raise ValueError(f'sampler must be one of {SAMPLERS}')
 
 
 class ForwardBudget:
@@ -87,19 +97,19 @@ def _class_major(logits, classes, total):
 
 class LowEntropyLastSlot:
     """One window of `shape` ([Y,Z,X]) inside a batched forward (stream/slot.py:50-176, with the solid steps of
-    `FastLowEntropyLastSlot`, fast_ops.py:481-581). `entropy` names the score kernel; only 'hip' exists here.
+    `FastLowEntropyLastSlot`, fast_ops.py:481-581). `entropy` takes the reference's names, 'torch' (its default)
+    and 'triton' (fast_ops.py:491-496), and 'hip': each runs the HIP entropy kernel, whose scores are within 2e-6
+    of float64 and so within tolerance of torch's, not bit for bit (the reference's own two are not bitwise equal
+    either, fast_ops.py:421-422).
     `keep_scores=True` also leaves each solid step's fp32 scores in `self.scores` (for checking).
     `sampler` draws the chosen voxels' classes: 'multinomial' (the reference's tail: `torch.multinomial` on the
     slot's generator, eager, k-sized) or 'philox' (`svhip_sample_chosen`: a counter-based draw per voxel keyed by
     the window's seed and the solid step, inside `select` and thus inside a captured step; the host reads back one
     int16 per voxel)."""
 
-    def __init__(self, shape, classes, air_ids, air_token, last_eps, block_size, device, entropy='hip',
+    def __init__(self, shape, classes, air_ids, air_token, last_eps, block_size, device, entropy='torch',
                  keep_scores=False, sampler='multinomial'):
-        if entropy != 'hip':
-            raise ValueError("entropy must be 'hip' (the HIP entropy kernel)")
-        if sampler not in ('multinomial', 'philox'):
-            raise ValueError("sampler must be 'multinomial' or 'philox'")
+        check_slot_options(entropy, sampler)
         self.sampler = sampler
         self.shape = tuple(int(s) for s in shape)
         if len(self.shape) != 3:

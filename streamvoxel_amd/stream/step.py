@@ -25,10 +25,11 @@ class CachedContext:
     """Per-layer K [B,H,Kcap,D] and V (stored transposed, [B,H,D,Kcap]) with per-window lengths.
 
     Valid keys of window b are [0, L_b); the tail is zeroed on write. kv_dtype 'bf16' or 'fp8' (OCP e4m3fn with
-    per-(window, head) scales); an fp8 cache is attended with the softmax weights in `p_dtype` ('e4m3': the fp8
-    matrix cores, or 'bf16': the reference's in-kernel dequantisation; see `attention`)."""
+    per-(window, head) scales); an fp8 cache is attended with the softmax weights in `p_dtype` ('bf16', the
+    default: the reference's in-kernel dequantisation, within 5e-2 of fp32 attention over the unquantised K/V; or
+    'e4m3': the fp8 matrix cores, an opt-in outside that bar; see `attention`)."""
 
-    def __init__(self, layers, batch, heads, head_dim, kv_cap, device, kv_dtype='bf16', p_dtype='e4m3'):
+    def __init__(self, layers, batch, heads, head_dim, kv_cap, device, kv_dtype='bf16', p_dtype='bf16'):
         if kv_dtype not in ('bf16', 'fp8'):
             raise ValueError("kv_dtype must be 'bf16' or 'fp8'")
         if p_dtype not in ('e4m3', 'bf16'):

@@ -39,7 +39,7 @@ def test_engine_options_and_device_checked_before_any_work():
     from streamvoxel_amd.stream.engine import SlotEngine
     spec = _Spec(16, 16)
     with pytest.raises(ValueError):
-        SlotEngine(None, spec, 'cuda', 2, 1, 1, patchify='conv')
+        SlotEngine(None, spec, 'cuda', 2, 1, 1, patchify='onehot')
     with pytest.raises(ValueError):
         SlotEngine(None, spec, 'cuda', 2, 1, 1, attention='math')
     with pytest.raises(ValueError):

@@ -351,17 +351,19 @@ def test_single_hot_key_returns_its_value_row(dev, kv, L):
     assert (out.float().cpu()[:, 0] - want).abs().max().item() <= 1e-3
 
 
-# The e4m3 second product rounds every softmax weight to e4m3 (relative 2^-4); the row sum is taken over the
-# rounded weights, so a single dominant key cancels and the error grows with the weight shared by a few keys:
-# within the fp8 bar up to logit standard deviation 2, and below 1e-1 at 4, measured. bf16 P holds the fp8 bar
-# throughout.
-SHARP_E4M3_BOUND = {1.0: FP8_ATOL, 2.0: FP8_ATOL, 4.0: 1e-1}
+# The default e4m3 form (bf16 softmax weights) holds the fp8 bar at every logit scale. The opt-in fp8 second
+# product (p_dtype='e4m3', SVHIP_FP8_E4M3_PFP8) rounds every softmax weight to e4m3 (relative 2^-4); the row sum is
+# taken over the rounded weights, so a single dominant key cancels and the error grows with the weight shared by a
+# few keys: within the bar up to logit standard deviation 2, 7.6e-2 measured at 4, which is why it is not the
+# default. Its documented accuracy there:
+PFP8_OPT_IN_STD4 = 1e-1
 
 
-@pytest.mark.parametrize('p_dtype', ['e4m3', 'bf16'])
+@pytest.mark.parametrize('p_dtype', ['bf16', 'e4m3'])
 @pytest.mark.parametrize('D', [64, 48])
 def test_e4m3_sharp_softmax_rows(dev, D, p_dtype):
-    """Logit standard deviations 1, 2 and 4 over an e4m3 cache, against float64 on the dequantised cache."""
+    """Logit standard deviations 1, 2 and 4 over an e4m3 cache, against float64 on the dequantised cache: the
+    default form within the fp8 bar throughout."""
     from streamvoxel_amd.stream.attention import attention, quantize_e4m3
     B, H, Q, kcap = 2, 2, 256, 2048
     lengths = [2048, 1500]
@@ -382,8 +384,8 @@ def test_e4m3_sharp_softmax_rows(dev, D, p_dtype):
         torch.cuda.synchronize()
         err = (out.double().cpu() - ref).abs().max().item()
         print(f'[gpu-case] e4m3 D={D} P={p_dtype} logit std={std}: |kernel - f64| {err:.2e}', flush=True)
-        bound = SHARP_E4M3_BOUND[std] if p_dtype == 'e4m3' else FP8_ATOL
-        assert err <= bound, (std, err)
+        opt_in_outside_bar = p_dtype == 'e4m3' and std > 2.0
+        assert err <= (PFP8_OPT_IN_STD4 if opt_in_outside_bar else FP8_ATOL), (std, err)
 
 
 @pytest.mark.parametrize('B,H', [(300, 1), (256, 3)])
@@ -444,6 +446,33 @@ def test_key_mask_any_pattern(dev, D, transposed):
         check(out, ref, BF16_ATOL, BF16_RTOL)
         assert torch.all(out[2] == 0)
 
+
+
+@pytest.mark.parametrize('D', [64, 48])
+def test_key_mask_first_attended_keys_far_below_zero(dev, D):
+    """A wave whose queries see no attended key in the first blocks, then only keys whose scores lie far below 0
+    (about -150 in natural units, -217 in log2 units, where exp2 of the score underflows against a running max of
+    0): the first attended key must set the running max, so that the output is the softmax over those keys and not
+    zeros. Row sums from the matrix cores (D = 64) and from the ones row (D = 48)."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, kcap = 2, 2, 96, 400
+    _case(f'xattn key mask, far negative scores after masked blocks D={D}')
+    g = torch.Generator().manual_seed(7 + D)
+    q = (4.0 * torch.ones(B, H, Q, D) + 0.05 * torch.randn(B, H, Q, D, generator=g)).to(torch.bfloat16)
+    # scale 1/sqrt(D): q . k = -4 D (4.7 + 0.2 n) / sqrt(D), about -150 at D = 64 with a spread of a few units
+    depth = (4.7 * 8 / math.sqrt(D) + 0.2 * torch.randn(B, H, kcap, 1, generator=g))
+    k = (-depth * torch.ones(B, H, kcap, D)).to(torch.bfloat16)
+    v = torch.randn(B, H, kcap, D, generator=g).to(torch.bfloat16)
+    mask = torch.rand(B, kcap, generator=g) < 0.6
+    mask[0, :150] = False                    # two whole blocks and more without an attended key
+    mask[1, :64] = False                     # exactly the first block
+    out = attention(q.to(dev), k.to(dev), v.to(dev), key_mask=mask.to(dev))
+    torch.cuda.synchronize()
+    ref = _masked_reference(q, k, v, mask)
+    scores = (q[0, 0, 0].double() @ k[0, 0, 150:160].double().t()) / math.sqrt(D)
+    assert float(scores.max()) < -100, scores
+    assert ref.abs().amax((2, 3)).min() > 0.1        # the reference is not zeros
+    check(out, ref, BF16_ATOL, BF16_RTOL)
 
 def test_key_mask_prefix_equals_lengths_and_packed(dev):
     """A prefix mask gives the bits of the length form; the packed cu_seqlens layout takes the mask per window."""

@@ -124,6 +124,59 @@ def test_engine_numerical_gate(dev):
     assert engine.packed.lengths.tolist()[:2] == [32 + 584, 12 + 200]
 
 
+
+@pytest.mark.parametrize('config', [dict(patchify='conv', attention='sdpa', compile=False),
+                                    dict(patchify='conv', attention='flex', compile=False),
+                                    dict(patchify='gather', attention='sdpa', compile=False),
+                                    dict(patchify='gather', attention='flex', compile=True)])
+def test_engine_reference_option_sets_give_the_default_forward(dev, config):
+    """The reference's FastSlotForward option sets (scripts/bench_ops.py:201-206) construct on the GPU and give the
+    default engine's forward bit for bit: 'conv' and 'gather' are one sum (the gather kernel), 'sdpa' and 'flex' one
+    masked attention over the valid keys (the attention kernel)."""
+    from streamvoxel_amd import synth
+    from streamvoxel_amd.stream.engine import SlotEngine
+    _case(f'engine small: options {config}')
+    model = _model(dev, **SMALL)
+    spec = synth.WindowSpec(height=64, tile=16, num_classes=40)
+    engines = [SlotEngine(model, spec, dev, 2, l1_cap=2, l2_cap=8, capture=False),
+               SlotEngine(model, spec, dev, 2, l1_cap=2, l2_cap=8, capture=False, **config)]
+    g = torch.Generator(device=dev).manual_seed(4)
+    tokens = torch.randint(0, spec.num_classes + 1, engines[0].tokens.shape, device=dev, generator=g)
+    outs = []
+    for engine in engines:
+        for i in range(2):
+            engine.load_slot(i, synth.condition(model, 10 * i, 150 + 60 * i, seed=20 + i, device=dev))
+        engine.wait_loads()
+        engine.tokens.copy_(tokens)
+        outs.append(engine.eager([0.8, 0.4]).class_major().clone())
+    assert engines[1].options['patchify'] == config['patchify']
+    assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize('entropy', ['torch', 'triton'])
+def test_slot_reference_entropy_names_select_like_hip(dev, entropy):
+    """FastLowEntropyLastSlot(..., entropy='torch' | 'triton') (fast_ops.py:491-496) runs the HIP entropy kernel: the
+    marking forward and two solid steps commit exactly what entropy='hip' commits on the same logits."""
+    from streamvoxel_amd import synth
+    from streamvoxel_amd.stream.slot import FastLowEntropyLastSlot
+    _case(f'slot entropy={entropy}')
+    shape, classes = (64, 16, 16), 40
+    N = 64 * 16 * 16
+    runs = []
+    for name in ('hip', entropy):
+        slot = FastLowEntropyLastSlot(shape, classes, (0,), 0, 1e-4, 4, dev, entropy=name)
+        slot.arm(77, 10, (0, 0))
+        tokens = torch.full(shape, classes, dtype=torch.int64, device=dev)
+        commits = []
+        for step in range(3):
+            logits = synth.bimodal_logits(N, classes, 0.7, seed=50 + step, device=dev).t().reshape(classes, *shape)
+            commits.append(slot.consume(logits, tokens)[1])
+        runs.append((commits, tokens.clone()))
+    (c_a, t_a), (c_b, t_b) = runs
+    assert torch.equal(t_a, t_b) and c_a[0] is None and c_b[0] is None
+    for x, y in zip(c_a[1:], c_b[1:]):
+        assert np.array_equal(x['positions'], y['positions']) and np.array_equal(x['values'], y['values'])
+
 def _drive(engine, slots, seeds, cap, staged):
     """The worker's loop (streamvoxel/stream/worker.py:378-397): arm every slot, then forward / consume until all
     windows finish. staged: graph replays + SelectGraphs + consume_batch; else eager forwards + per-slot consume."""

@@ -92,7 +92,7 @@ def test_selection_names(dev):
     assert torch.equal(entropy_torch(logits), s)
     eligible = torch.rand(shape, device=dev) < 0.7
     count = torch.tensor(1000, device=dev)
-    first = top_mask_nosync(s, eligible, count).clone()     # results live in reused buffers: keep a copy
+    first = top_mask_nosync(s, eligible, count)
     assert torch.equal(first, top_mask(s, eligible, 1000)) and int(first.sum()) == 1000
     nb = N // 64
     pos = torch.randperm(nb, generator=torch.Generator().manual_seed(1)).to(dev)
@@ -100,16 +100,16 @@ def test_selection_names(dev):
     mask = torch.ones(shape, dtype=torch.bool, device=dev)
     a = quota_select_nosync(s, mask, torch.tensor(700, device=dev), 4, pos, torch.tensor(700 / N, device=dev,
                                                                                           dtype=torch.float64),
-                            n_total, torch.tensor(0, device=dev)).clone()
+                            n_total, torch.tensor(0, device=dev))
     b = quota_select(s, mask, 700, 4, pos, 700 / N, n_total, 0)
     torch.cuda.synchronize()
     assert torch.equal(a, b) and int(a.sum()) == 700
 
 
-def test_one_window_selection_functions_allocate_nothing_when_repeated(dev):
-    """quota_select / block_quota_select / top_mask keep their workspace and outputs per (device, shape, block):
-    once warm, repeated eager calls make no allocation of the caching allocator."""
-    from streamvoxel_amd.sampling.block_quota import block_quota_select, quota_select, top_mask
+def test_one_window_selection_functions_allocate_nothing_with_caller_buffers(dev):
+    """quota_select / block_quota_select / top_mask with `out=` and `buffers=` (caller-owned SelectBuffers): once
+    warm, repeated eager calls make no allocation of the caching allocator, and give the default calls' results."""
+    from streamvoxel_amd.sampling.block_quota import SelectBuffers, block_quota_select, quota_select, top_mask
     shape = (64, 16, 16)
     N = 64 * 16 * 16
     nb = N // 64
@@ -125,15 +125,17 @@ def test_one_window_selection_functions_allocate_nothing_when_repeated(dev):
     com_dev = torch.tensor(N - int(mask.sum()), device=dev)
     count = torch.tensor(300, device=dev)
     frac_h, com_h = float(frac_dev), int(com_dev)
+    buffers = SelectBuffers(shape, 4, dev)
+    outs = [torch.empty(shape, dtype=torch.bool, device=dev) for _ in range(4)]
 
     def calls():
-        a = quota_select(s, mask, k_dev, 4, pos, frac_dev, n_total, com_dev)
-        b = quota_select(s, mask, 500, 4, pos, frac_h, n_total, com_h)
-        c = block_quota_select(s, mask, 500, 4, order, frac_h, n_total)
-        d = top_mask(s, mask, count)
+        a = quota_select(s, mask, k_dev, 4, pos, frac_dev, n_total, com_dev, out=outs[0], buffers=buffers)
+        b = quota_select(s, mask, 500, 4, pos, frac_h, n_total, com_h, out=outs[1], buffers=buffers)
+        c = block_quota_select(s, mask, 500, 4, order, frac_h, n_total, out=outs[2], buffers=buffers)
+        d = top_mask(s, mask, count, out=outs[3])
         return a, b, c, d
 
-    want = [t.clone() for t in calls()[:1]]
+    want = [quota_select(s, mask, 500, 4, pos, frac_h, n_total, com_h), top_mask(s, mask, 300)]
     calls()
     torch.cuda.synchronize()
     before = torch.cuda.memory_stats(dev)['allocation.all.allocated']
@@ -141,4 +143,54 @@ def test_one_window_selection_functions_allocate_nothing_when_repeated(dev):
         a, b, c, d = calls()
     torch.cuda.synchronize()
     assert torch.cuda.memory_stats(dev)['allocation.all.allocated'] == before
-    assert torch.equal(c, want[0]) and int(c.sum()) == 500 and int(d.sum()) == 300
+    assert all(t is o for t, o in zip((a, b, c, d), outs))
+    assert torch.equal(a, want[0]) and torch.equal(b, want[0]) and torch.equal(c, want[0])
+    assert torch.equal(d, want[1]) and int(c.sum()) == 500 and int(d.sum()) == 300
+
+
+def test_selection_results_are_fresh_and_chain_like_the_reference(dev):
+    """The reference's callers keep selection results and chain them: `top_mask(score, top_mask(draw, mask, c), k)`
+    (eval/samplers.py:27-28) and a held quota_select result across a second call. Every default call returns a
+    tensor of its own, so both equal the oracle bit for bit; an `out` that aliases an input is refused."""
+    import numpy as np
+    from oracle import sampling as S
+    from streamvoxel_amd.sampling.block_quota import SelectBuffers, block_quota_select, quota_select, top_mask
+    shape = (32, 16, 16)
+    N = 32 * 16 * 16
+    nb = N // 64
+    rng = np.random.default_rng(3)
+    score = (rng.integers(-40, 1, shape) / 8).astype(np.float32)
+    draw = rng.random(shape).astype(np.float32)
+    mask = rng.random(shape) < 0.75
+    sd, dd, md = (torch.from_numpy(a).to(dev) for a in (score, draw, mask))
+    c, k = 1500, 600
+    got = top_mask(sd, top_mask(dd, md, c), k)
+    want = S.top_mask(score, S.top_mask(draw, mask, c), k)
+    assert np.array_equal(got.cpu().numpy(), want)
+
+    order = rng.permutation(nb)
+    pos = S.order_to_pos(order)
+    n_total = np.full(nb, 64, np.int64)
+    committed = int(N - mask.sum())
+    results = []
+    for kk in (300, 900):
+        frac = (committed + kk) / N
+        results.append((kk, frac, quota_select(sd, md, kk, 4, torch.from_numpy(pos).to(dev), frac,
+                                               torch.from_numpy(n_total).to(dev), committed)))
+    held = [block_quota_select(sd, md, kk, 4, torch.from_numpy(order).to(dev), (committed + kk) / N,
+                               torch.from_numpy(n_total).to(dev)) for kk in (300, 900)]
+    for (kk, frac, res), blk in zip(results, held):
+        expect = S.quota_select_nosync(score, mask, kk, 4, pos, frac, n_total, committed)
+        assert np.array_equal(res.cpu().numpy(), expect), kk
+        assert np.array_equal(blk.cpu().numpy(), expect), kk
+    assert results[0][2].data_ptr() != results[1][2].data_ptr()
+
+    eligible = md.clone()
+    with pytest.raises(ValueError, match='shares memory'):
+        top_mask(sd, eligible, 10, out=eligible)
+    with pytest.raises(ValueError, match='shares memory'):
+        quota_select(sd, eligible, 10, 4, torch.from_numpy(pos).to(dev), 0.5, torch.from_numpy(n_total).to(dev),
+                     committed, out=eligible)
+    with pytest.raises(ValueError, match='buffers are for'):
+        quota_select(sd, md, 10, 4, torch.from_numpy(pos).to(dev), 0.5, torch.from_numpy(n_total).to(dev),
+                     committed, buffers=SelectBuffers((64, 16, 16), 4, dev))

@@ -89,14 +89,14 @@ def test_class_major_and_patch_layouts_match_oracle(dev, classes, dtype):
         print(f'[gpu-case] C={classes} {dtype} window {b}: {same:.5f} of the draws equal the oracle class', flush=True)
 
 
-@pytest.mark.parametrize('shape,share', [((5, 7, 9), 1.0), ((8, 8, 24), 0.6)])
+@pytest.mark.parametrize('shape,share', [((5, 7, 9), 1.0), ((10, 10, 10), 1.0), ((8, 8, 20), 0.6)])
 @pytest.mark.parametrize('classes,dtype', [(64, torch.bfloat16), (64, torch.float32), (100, torch.float32),
                                            (256, torch.float32), (304, torch.bfloat16), (512, torch.bfloat16),
                                            (1000, torch.float32)])
 def test_ragged_windows_and_dense_choices_match_oracle(dev, shape, share, classes, dtype):
-    """Windows whose voxel count is not a multiple of the kernel's 1024-voxel workgroup (315: one partial group,
-    1536: one full and one partial), up to every voxel chosen, from voxel rows (a class-major view with unit class
-    stride, the 16-byte row loads where they apply)."""
+    """Windows whose voxel count is not a multiple of the kernel's 512-voxel workgroup (315: one partial group;
+    1000: one full and one partial; 1280: two full and one partial), up to every voxel chosen, from voxel rows (a
+    class-major view with unit class stride, the 16-byte row loads where they apply)."""
     from streamvoxel_amd.stream.sampler import sample_chosen
     n = 2
     N = shape[0] * shape[1] * shape[2]
