@@ -32,6 +32,28 @@ def hipcc():
     return path
 
 
+TRACE_LIB = os.path.join(HERE, 'libsvhip_trace.so')
+
+
+def build_trace(verbose=False):
+    """The wave-timeline build of the library (cross attention compiled with -DSVHIP_XATTN_TRACE, every other
+    source the product's objects): libsvhip_trace.so, for streamvoxel_amd.xattn_trace only. Needs `build()` first."""
+    objdir = os.path.join(HERE, '_build')
+    obj = os.path.join(objdir, 'xattn_trace.o')
+    cmd = [hipcc(), *[f for f in FLAGS if f != '-shared'], '-DSVHIP_XATTN_TRACE', '-c', os.path.join(CSRC, 'xattn.hip'),
+           '-o', obj]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    if res.returncode != 0:
+        raise RuntimeError('hipcc failed (trace build):\n' + res.stdout.decode(errors='replace'))
+    objects = [os.path.join(objdir, src.replace('.hip', '.o')) for src in SOURCES if src != 'xattn.hip'] + [obj]
+    tmp = TRACE_LIB + '.tmp'
+    res = subprocess.run([hipcc(), *FLAGS, *objects, '-o', tmp], stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    if res.returncode != 0:
+        raise RuntimeError('link failed (trace build):\n' + res.stdout.decode(errors='replace'))
+    os.replace(tmp, TRACE_LIB)
+    return TRACE_LIB
+
+
 def build(verbose=False, jobs=4):
     """Compile each source to an object in parallel, then link the shared library. Returns the library path."""
     objdir = os.path.join(HERE, '_build')
@@ -67,3 +89,5 @@ def build(verbose=False, jobs=4):
 
 if __name__ == '__main__':
     print(build(verbose='-v' in sys.argv))
+    if '--trace' in sys.argv:
+        print(build_trace())

@@ -95,6 +95,76 @@ constexpr float kPv8MaxHigh = 4.8f;
 constexpr int kMaxRankWindows = 256;
 constexpr int kCusPerXcd = 32;  // MI355X: 8 XCDs x 32 CUs
 
+// Wave timelines (built only with -DSVHIP_XATTN_TRACE, into the separate trace library that
+// streamvoxel_amd/xattn_trace.py loads; the product library compiles every hook below to nothing). Per wave of the
+// bf16 direct-staged full-width kernel: the wave's HW_ID / XCC_ID registers, its (window, head, query tile, full
+// blocks), s_memtime at the wave's start and end, and for key blocks kTraceBlock0 .. + kTraceBlocks - 1 five stamps
+// per 32-key half (before the score product's operand reads; after the score product, read back by a
+// compiler-visible VALU op; after the exponentials and packs; after the row-sum readback; after the second product
+// is issued) and one after the block's barrier. The stamps are s_memtime (a per-CU counter: compare stamps of one
+// CU only); the asm takes the value a stamp must follow as an operand, so it cannot move above it.
+#ifdef SVHIP_XATTN_TRACE
+__device__ unsigned long long* g_trace = nullptr;
+constexpr int kTraceBlock0 = 4, kTraceBlocks = 8, kTraceWords = 4 + kTraceBlocks * 11;
+struct WaveTrace {
+  unsigned long long* slot = nullptr;
+  unsigned long long tt[11];
+  bool block_on = false;
+  static __device__ __forceinline__ unsigned long long stamp() {
+    unsigned long long t;
+    asm volatile("s_memtime %0" : "=s"(t));
+    return t;
+  }
+  static __device__ __forceinline__ unsigned long long stamp_after(float dep, float dep2 = 0.f) {
+    unsigned long long t;
+    asm volatile("s_memtime %0" : "=s"(t) : "v"(dep), "v"(dep2));
+    return t;
+  }
+  static __device__ __forceinline__ unsigned long long stamp_now(float dep) {
+    unsigned long long t;
+    asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t) : "v"(dep));
+    return t;
+  }
+  __device__ __forceinline__ void begin(bool on, int w, int lane, int64_t b, int64_t h, int qt, int nfull) {
+    if (!on || g_trace == nullptr) return;
+    slot = g_trace + (static_cast<long long>(blockIdx.x) * 4 + w) * kTraceWords;
+    if (lane == 0) {
+      unsigned int hw, xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      slot[0] = (static_cast<unsigned long long>(xcc) << 32) | hw;
+      slot[1] = (static_cast<unsigned long long>(b) << 40) | (static_cast<unsigned long long>(h) << 24) |
+                (static_cast<unsigned long long>(qt) << 16) | static_cast<unsigned long long>(nfull);
+      slot[2] = stamp_now(0.f);
+    }
+  }
+  __device__ __forceinline__ void block(int blk) {
+    block_on = slot != nullptr && blk >= kTraceBlock0 && blk < kTraceBlock0 + kTraceBlocks;
+  }
+  __device__ __forceinline__ void mark(int i) {
+    if (block_on) tt[i] = stamp();
+  }
+  __device__ __forceinline__ void mark_after(int i, float dep, float dep2 = 0.f) {
+    if (block_on) tt[i] = stamp_after(dep, dep2);
+  }
+  __device__ __forceinline__ void block_end(int blk, int lane) {
+    const int k = blk - kTraceBlock0;
+    if (slot == nullptr || k < 0 || k >= kTraceBlocks) return;
+    tt[10] = stamp();
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 11; ++i) slot[4 + 11 * k + i] = tt[i];
+    }
+  }
+  __device__ __forceinline__ void end(int lane, float dep) {
+    if (slot != nullptr && lane == 0) slot[3] = stamp_now(dep);
+  }
+};
+#define SVHIP_TRACE(...) __VA_ARGS__
+#else
+#define SVHIP_TRACE(...)
+#endif
+
 struct XattnParams {
   const void* q;
   const void* k;
@@ -821,8 +891,11 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
     if (first || __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, sl2, -m) > kPv8MaxHigh) != 0ull) raise8(mx);
   };
 
+  SVHIP_TRACE(WaveTrace trace;)
+  SVHIP_TRACE(trace.begin(!FP8 && !KMASK && STAGING == kDirectFull, w, lane, b, h, qt, nfull);)
   auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vt, int kv0) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked)::value;
+    SVHIP_TRACE(trace.block(MASKED ? -1 : kv0 / kKB);)
     const char* kp = reinterpret_cast<const char*>(Ks);
     const char* vp = reinterpret_cast<const char*>(Vt);
     const uint64_t bits = block_bits(kv0);
@@ -831,6 +904,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       // S^T of keys 32 t .. 32 t + 31 (LDS rows 32 t + col); k-steps past head_dim (zero in Q) are skipped.
+      SVHIP_TRACE(trace.mark(5 * t);)
       f32x16_t s;
       if constexpr (FULLK) {
         bf16x8_t a[2 * DT];
@@ -946,8 +1020,11 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
         // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN) some
         // score passed m by about 20 (log2 units). Only then (and on the window's first half, where m is -inf)
         // is the slow path taken.
+        SVHIP_TRACE(trace.mark_after(5 * t + 1, __builtin_amdgcn_fmed3f(s[15], s[14], kFltMax));)
         exps();
+        SVHIP_TRACE(trace.mark_after(5 * t + 2, __builtin_bit_cast(float, __builtin_bit_cast(uint4, pb[1]).w));)
         float hs = half_sum();
+        SVHIP_TRACE(trace.mark_after(5 * t + 3, __builtin_amdgcn_fmed3f(hs, hs, kFltMax));)
         if (first || __builtin_amdgcn_ballot_w64(!(hs <= kSumHigh) || (KMASK && placeholder)) != 0ull) {
           raise(half_max());
           hs = half_sum();
@@ -964,6 +1041,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
 #pragma unroll
         for (int j = 0; j < DT; ++j) o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], pb[ks], o[j], 0, 0, 0);
       }
+      SVHIP_TRACE(trace.mark_after(5 * t + 4, o[DT - 1][15], l);)
     }
     if constexpr (PV8) {
       // O^T += V^T . P^T over the block's 64 keys on the fp8 matrix cores; A: V^T rows 32 j + col, keys
@@ -1000,6 +1078,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
     stage_commit(nK, nV);
     wait_vmem();
     __syncthreads();
+    SVHIP_TRACE(trace.block_end(blk, lane);)
   };
 
   if (nfull > 0) {
@@ -1071,6 +1150,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(lsum), __float_as_int(lsum), false, false);
     lsum = __int_as_float(sw[0]);
   }
+  SVHIP_TRACE(trace.end(lane, lsum);)
   // A query with no attended key (only possible with a key mask) has l = 0 and O = 0: it gets zeros.
   const float inv = (KMASK && !(lsum > 0.f)) ? 0.f : vscale / lsum;
   if (q_ok) {
@@ -1241,6 +1321,13 @@ static int xattn_impl(const void* q, const void* k, const void* v, void* o, int 
 }  // namespace svhip
 
 using namespace svhip;
+
+#ifdef SVHIP_XATTN_TRACE
+// Trace build only: the device buffer the instrumented kernel writes (kTraceWords words per wave), or NULL to stop.
+extern "C" int svhip_xattn_trace_set(void* buffer) {
+  return hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &buffer, sizeof(buffer)) == hipSuccess ? 0 : -1;
+}
+#endif
 
 extern "C" int svhip_xattn_fwd(const void* q, const void* k, const void* v, void* o, int kv_dtype,
                                const int32_t* kv_len, const int32_t* cu_seqlens, const float* k_scale,

@@ -212,7 +212,9 @@ def test_sixty_four_slot_e4m3_stress(dev):
             err = (o[b:b + 1, [3, 12], ::16].double().cpu() - ref).abs().max().item()
             print(f'[gpu-case] 64-slot e4m3 {name} window {b}: |kernel - f64 over the original K/V| {err:.2e} '
                   f'(max |ref| {ref.abs().max().item():.2e})', flush=True)
-            _check(o[b:b + 1, [3, 12], ::16], ref, 5e-2, 1.0)
+            # 5e-2 absolute (the fp8 bar); the default form also within 5e-2 of the output's own scale (measured
+            # 2-2.5 %; the fp8 second product about twice that)
+            _check(o[b:b + 1, [3, 12], ::16], ref, 5e-2, 5e-2 if name == 'default' else 1.0)
     for b in raw:
         # Dequantised cache = what the kernel multiplies; float64 attention over it, 2 heads, every 16th query.
         L = lengths[b]
