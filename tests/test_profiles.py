@@ -1,5 +1,6 @@
 """The committed profiles carry what bench.py reads from them: the per-launch HBM traffic totals of the attention
-kernel and of the selection (rocprofv3 FETCH_SIZE / WRITE_SIZE), and every summary names the command that made it."""
+kernel and of the selection (rocprofv3 FETCH_SIZE / WRITE_SIZE), and every summary names the command that made it
+(rocprofv3, or a committed entry point: bench.py, python -m streamvoxel_amd....)."""
 import os
 import sys
 
@@ -25,4 +26,6 @@ def test_every_profile_names_its_command():
     for name in names:
         with open(os.path.join(d, name)) as f:
             text = f.read()
-        assert 'rocprofv3' in text, name
+        # a rocprofv3 summary, or a timing summary made by a committed entry point of this repository
+        assert any(cmd in text for cmd in ('rocprofv3', 'python -m streamvoxel_amd.', 'bench.py')), name
+        assert '```' in text, name
