@@ -74,11 +74,13 @@ __device__ __forceinline__ void load16(const T* p, float* dst) {
   unpack16<T>(*reinterpret_cast<const uint4*>(p), dst);
 }
 
-// One logit of the canonical order into a lane's sums (the same instructions in every pass).
+// One logit of the canonical order into a lane's sums (the same instructions in every pass), in log2 units:
+// t = (x - max) log2(e) (the difference exact, so the row's max gives t = 0 and a one-hot row entropy 0), p = 2^t,
+// s += p, w += p t (entropy) or w += p (air classes). finish_stat turns (s, w) into the statistic.
 template <int MODE>
 __device__ __forceinline__ void accumulate(float x, float m, int c, const uint32_t* air_bits, float& s, float& w) {
-  const float t = x - m;
-  const float p = fast_exp(t);
+  const float t = (x - m) * kLog2e;
+  const float p = __builtin_amdgcn_exp2f(t);
   s += p;
   if constexpr (MODE == kEntropy) {
     w = __builtin_fmaf(p, t, w);
@@ -115,10 +117,12 @@ constexpr int kCanonTile = 32;       // voxels per LDS tile
 
 __host__ inline size_t canon_lds_bytes(int64_t C) { return sizeof(float) * kCanonTile * (C + 1); }
 
+// sum p log p / sum p - log sum p with p = 2^t: (w / s - log2 s) ln 2 (entropy, w = sum p t in log2 units), or the
+// air classes' share w / s.
 template <int MODE>
 __device__ __forceinline__ float finish_stat(float s, float w) {
   if constexpr (MODE == kEntropy) {
-    return w / s - __builtin_amdgcn_logf(s) * kLn2;
+    return (w / s - __builtin_amdgcn_logf(s)) * kLn2;
   } else {
     return w / s;
   }
@@ -150,6 +154,10 @@ constexpr VoxelRows kYzxRows{-1, 0, 0};
 // Voxel-major pass: LPV (8 or 16) lanes own a voxel; workgroup `blk` of `nblk` takes voxels
 // blk * (256 / LPV) + (tid / LPV), stepping by nblk * (256 / LPV). Each lane loads NV 16-byte vectors of the row.
 // Requires 256-thread workgroups, C % (16 / sizeof(T)) == 0 and 16-byte aligned rows.
+// C / E vectors per row: the first `vfull` vectors of every lane are inside the row; a lane's later ones may lie
+// past it (only when C / E is not a multiple of LPV) and are loaded from vector 0, set to -inf for the max and
+// skipped by the sums (a divergent branch: no per-element selects). (window, voxel) advance by the stride without
+// a division.
 template <typename T, int NV, int MODE, typename Out, int LPV = 16>
 __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_t total, int64_t n, int64_t C,
                                                  int64_t sb, int64_t sn, const uint32_t* air_bits, Out& out,
@@ -158,24 +166,31 @@ __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_
   const int g = threadIdx.x & (LPV - 1);
   constexpr int64_t kRowsPerBlock = 256 / LPV;
   const int64_t stride = nblk * kRowsPerBlock;
-  for (int64_t voxel = blk * kRowsPerBlock + (threadIdx.x / LPV); voxel < total; voxel += stride) {
+  const int vecs = static_cast<int>(C / E);
+  const int vfull = vecs / LPV;
+  int64_t voxel = blk * kRowsPerBlock + (threadIdx.x / LPV);
+  int64_t b = voxel / n;
+  int64_t i = voxel - b * n;
+  const int64_t sdiv = stride / n, smod = stride - sdiv * n;
+  for (; voxel < total; voxel += stride) {
     const auto pre = out.prefetch(voxel);
-    const int64_t b = voxel / n;
-    const int64_t i = voxel - b * n;
     const T* row = x + b * sb + rows(i) * sn;
-    float v[NV * E];
+    uint4 raw[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      const int64_t c0 = static_cast<int64_t>(g + LPV * j) * E;
-      load16<T>(row + (c0 < C ? c0 : 0), v + j * E);
+      const int vj = g + LPV * j;
+      raw[j] = *reinterpret_cast<const uint4*>(row + (vj < vecs ? vj : 0) * E);
     }
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      if (static_cast<int64_t>(g + LPV * j) * E >= C) {
-#pragma unroll
-        for (int e = 0; e < E; ++e) v[j * E + e] = -INFINITY;
+      if (j >= vfull && g + LPV * j >= vecs) {
+        const uint32_t ninf = sizeof(T) == 4 ? 0xff800000u : 0xff80ff80u;
+        raw[j] = make_uint4(ninf, ninf, ninf, ninf);
       }
     }
+    float v[NV * E];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) unpack16<T>(raw[j], v + j * E);
     float m = -INFINITY;
 #pragma unroll
     for (int e = 0; e < NV * E; ++e) m = fmaxf(m, v[e]);
@@ -183,15 +198,20 @@ __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_
     float s = 0.f, w = 0.f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
+      if (j < vfull || g + LPV * j < vecs) {
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const int c = (g + LPV * j) * E + e;
-        if (c < C) accumulate<MODE>(v[j * E + e], m, c, air_bits, s, w);
+        for (int e = 0; e < E; ++e) accumulate<MODE>(v[j * E + e], m, (g + LPV * j) * E + e, air_bits, s, w);
       }
     }
     s = group_sum<LPV>(s);
     w = group_sum<LPV>(w);
     if (g == 0) out.store(voxel, finish_stat<MODE>(s, w), pre);
+    i += smod;
+    b += sdiv;
+    if (i >= n) {
+      i -= n;
+      ++b;
+    }
   }
 }
 
@@ -355,8 +375,8 @@ __device__ __forceinline__ void class_major_pass(const T* __restrict__ x, int64_
         for (int r = 1; r < CH; ++r) cm = fmaxf(cm, v[r][u]);
         const float mn = fmaxf(m[u], cm);
         if (mn > m[u]) {
-          const float d = m[u] - mn;
-          const float rs = fast_exp(d);
+          const float d = (m[u] - mn) * kLog2e;   // log2 units, like w
+          const float rs = __builtin_amdgcn_exp2f(d);
           if constexpr (MODE == kEntropy) {
             w[u] = (s[u] == 0.f) ? 0.f : (w[u] + s[u] * d) * rs;
           } else {
@@ -367,16 +387,7 @@ __device__ __forceinline__ void class_major_pass(const T* __restrict__ x, int64_
         }
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
-          if (c0 + r < C) {
-            const float t = v[r][u] - m[u];
-            const float p = fast_exp(t);
-            s[u] += p;
-            if constexpr (MODE == kEntropy) {
-              w[u] += p * t;
-            } else {
-              if (is_air(air_bits, static_cast<int>(c0 + r))) w[u] += p;
-            }
-          }
+          if (c0 + r < C) accumulate<MODE>(v[r][u], m[u], static_cast<int>(c0 + r), air_bits, s[u], w[u]);
         }
       }
     }
@@ -412,7 +423,7 @@ __host__ inline int64_t stats_grid(int64_t work_items) {
   return g;
 }
 
-constexpr int64_t kShortRowWorkgroups = 8 * 256;  // 8 per CU of MI355X
+constexpr int64_t kShortRowWorkgroups = 24 * 256;  // 24 per CU of MI355X
 
 // Picks the pass for a [batch, C, n] logits tensor with element strides (sb, sc, sn).
 template <typename T>
@@ -424,9 +435,10 @@ __host__ inline StatsPlan plan_stats(const T* x, int64_t batch, int64_t C, int64
   RowPlan rp;
   const bool canon = row_plan<T>(C, &rp);
   if (canon && sc == 1 && aligned_base && ((sn * bytes) % 16) == 0 && ((sb * bytes) % 16) == 0) {
-    // Short rows run faster from a grid of 8 workgroups per CU that loops over the voxels (measured: 304 bf16
-    // classes 99 -> 93 us per 8-window selection); long rows from one pass of workgroups over all voxels (256 fp32
-    // classes: 100 us, 113 us with the capped grid).
+    // Short rows run faster from a grid of 24 workgroups per CU that loops over the voxels (304 bf16 classes in
+    // patch order, per 8-window selection: 74.5 us at 8 per CU, 69.5 at 16, 68.0 at 24, 71 with one pass of
+    // workgroups over all voxels); long rows from one pass of workgroups (256 fp32 classes: 100 us, 113 us with a
+    // capped grid).
     const int64_t grid = rp.lpv == 8 ? std::min<int64_t>(stats_grid(batch * n * rp.lpv), kShortRowWorkgroups)
                                      : stats_grid(batch * n * rp.lpv);
     return StatsPlan{kVoxelMajor, rp.nv, rp.lpv, grid, 0};
