@@ -20,6 +20,7 @@ The device work of a window:
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from streamvoxel_amd import _lib
@@ -28,6 +29,7 @@ from streamvoxel_amd.sampling.low_entropy_last import low_entropy_last_quotas
 from streamvoxel_amd.sampling.schedule import actual_time
 from streamvoxel_amd.stream.patches import PatchLogits
 from streamvoxel_amd.stream.sampler import sample_chosen
+from streamvoxel_amd.stream.step import EaseSelect
 
 ORDER_SEED_OFFSET = 9173
 ENTROPY_NAMES = ('torch', 'triton', 'hip')
@@ -229,21 +231,31 @@ class LowEntropyLastSlot:
 
     # -- solid steps -----------------------------------------------------------------------------------------------
 
-    def prepare(self):
-        """Per-step scalars (device fills, no H2D copy) and, once per window, the deferred mask and the block
-        constants (fast_ops.py:519-532). Returns k."""
-        k = self.quotas[self.solid_calls]
-        committed = sum(self.quotas[:self.solid_calls])
+    def _bind(self):
+        """Once per window: the deferred mask and the block constants into the static buffers."""
         if not self._bound:
             self.last_static.copy_(self.last)
             self.n_total.copy_(block_view((~self.last).contiguous(), self.block_size).sum(1))
             self.pos[self.order] = torch.arange(len(self.order), device=self.device)
             self._bound = True
+
+    def step_scalars(self):
+        """(k, committed, frac, solid step) of the next solid step, host numbers (fast_ops.py:519-532), after the
+        once-per-window binding of the static buffers."""
+        self._bind()
+        k = self.quotas[self.solid_calls]
+        committed = sum(self.quotas[:self.solid_calls])
+        return k, committed, (committed + k) / (self.total - self.last_count), self.solid_calls
+
+    def prepare(self):
+        """Per-step scalars (device fills, no H2D copy) and, once per window, the deferred mask and the block
+        constants (fast_ops.py:519-532). Returns k."""
+        k, committed, frac, step = self.step_scalars()
         self.k.fill_(k)
         self.committed.fill_(committed)
-        self.frac.fill_((committed + k) / (self.total - self.last_count))
+        self.frac.fill_(frac)
         if self.sampler == 'philox':
-            self.step_dev.fill_(self.solid_calls)
+            self.step_dev.fill_(step)
         return k
 
     def _patch_rows(self, logits):
@@ -329,14 +341,9 @@ class LowEntropyLastSlot:
         event.synchronize()
         if host is None:
             # 'philox': the drawn classes of the whole window, -1 where not chosen.
-            if int(self._host_flags[0]):
-                raise AssertionError('low-entropy-last solid step did not meet its quota')
             if int(self._host_flags[1]):
                 raise RuntimeError('probability tensor contains either `inf`, `nan` or element < 0')
-            positions = torch.nonzero(self._host16 >= 0).squeeze(1)
-            if len(positions) != k:
-                raise AssertionError(f'{len(positions)} voxels drawn for a quota of {k}')
-            values_cpu = self._host16[positions].clone()
+            return self.commit_drawn(self._host16.numpy(), bool(self._host_flags[0]), tokens)
         else:
             if int(host[2 * k]):
                 raise AssertionError('low-entropy-last solid step did not meet its quota')
@@ -351,6 +358,41 @@ class LowEntropyLastSlot:
         if self.solid_calls >= len(self.quotas):
             return self._finish(tokens), commit
         return None, commit
+
+    def commit_drawn(self, drawn, bad, tokens):
+        """The host bookkeeping of a solid step from the drawn classes of the window (`drawn`, numpy int16 [N], -1
+        where not chosen) and its quota flag: the commit's positions in ascending flat order and their values, the
+        step and value maps, and the finish record after the last solid step (fast_ops.py:560-575)."""
+        if bad:
+            raise AssertionError('low-entropy-last solid step did not meet its quota')
+        k = self.quotas[self.solid_calls]
+        positions = np.flatnonzero(drawn >= 0)
+        if len(positions) != k:
+            raise AssertionError(f'{len(positions)} voxels drawn for a quota of {k}')
+        values = drawn[positions]
+        self.solid_calls += 1
+        self.actual += 1
+        self.nfe += 1
+        self.step_map.numpy().reshape(-1)[positions] = self.nfe
+        self.values.numpy().reshape(-1)[positions] = values
+        commit = dict(positions=positions.astype('int32'), values=values.copy(), step=int(self.nfe))
+        if self.solid_calls >= len(self.quotas):
+            return self._finish(tokens), commit
+        return None, commit
+
+    def adopt(self, batch, index):
+        """Move this slot's static device buffers into window `index` of a `PhiloxBatch` (contents kept): from then
+        on they are views of the batch's window-by-window arrays, which one launch selects and samples for every
+        window."""
+        sel = batch.sel
+        views = dict(last_static=sel.last[index].view(self.shape), n_total=sel.n_total[index],
+                     pos=sel.pos[index], k=sel.k[index:index + 1], committed=sel.committed[index:index + 1],
+                     frac=sel.frac[index:index + 1], chosen=sel.chosen[index].view(self.shape),
+                     bad=sel.bad[index:index + 1], seed_dev=batch.seeds[index:index + 1],
+                     step_dev=batch.steps[index:index + 1], drawn=batch.drawn[index], sample_err=batch.err)
+        for name, view in views.items():
+            view.copy_(getattr(self, name))
+            setattr(self, name, view)
 
     def consume(self, logits, tokens):
         """One forward for this slot (stream/slot.py:117-164). `tokens` [Y,Z,X] int64 is updated in place, `logits`
@@ -406,6 +448,54 @@ class _NothingSelected:
         return False
 
 
+class PhiloxBatch:
+    """Device state of the solid steps of a batch of 'philox' slots, laid out window by window at fixed
+    addresses, so that one selection launch (`EaseSelect.run`: entropy, block quota, trim / top-up, `bad`) and one
+    sampling launch (`svhip_sample_chosen`) serve every window of a bucket. The slots' own static buffers become
+    views of it (`LowEntropyLastSlot.adopt`), so their eager paths keep working. The per-step scalars of all
+    windows (k, committed, frac, solid step) sit in one device array that one host-to-device copy fills; windows
+    that take no solid step in a forward get k = 0 and select and draw nothing."""
+
+    def __init__(self, slots, tokens):
+        batch = len(tokens)
+        s0 = slots[0]
+        self.batch, self.shape, self.total = batch, s0.shape, s0.total
+        dev = s0.device
+        self.sel = EaseSelect(batch, s0.shape, s0.classes, s0.block_size, dev)
+        self.sel.tokens = tokens.view(batch, -1)
+        self.scal = torch.zeros(4 * batch, dtype=torch.int64, device=dev)
+        self.sel.k, self.sel.committed = self.scal[:batch], self.scal[batch:2 * batch]
+        self.sel.frac = self.scal[2 * batch:3 * batch].view(torch.float64)
+        self.steps = self.scal[3 * batch:]
+        self.seeds = torch.zeros(batch, dtype=torch.int64, device=dev)
+        self.drawn = torch.full((batch, *s0.shape), -1, dtype=torch.int16, device=dev)
+        self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.host_scal = torch.zeros(4 * batch, dtype=torch.int64, pin_memory=True)
+        self.host_drawn = torch.empty((batch, s0.total), dtype=torch.int16, pin_memory=True)
+        self.host_bad = torch.empty(batch, dtype=torch.uint8, pin_memory=True)
+        self.host_err = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        for i, slot in enumerate(slots[:batch]):
+            slot.adopt(self, i)
+
+    @staticmethod
+    def fits(slots, tokens):
+        """Whether `slots` can share one batch over the token rows `tokens` [batch, Y, Z, X]."""
+        batch = len(tokens)
+        if len(slots) < batch or batch < 1:
+            return False
+        s0 = slots[0]
+        return all(isinstance(s, LowEntropyLastSlot) and s.sampler == 'philox' and s.shape == s0.shape
+                   and s.classes == s0.classes and s.block_size == s0.block_size and s.device == s0.device
+                   for s in slots[:batch]) and tuple(tokens.shape[1:]) == s0.shape
+
+    def run(self, logits, size):
+        """Selection and sampling of the first `size` windows (capturable): `logits` is a bucket's output, a
+        PatchLogits or class-major [size, C, Y, Z, X]."""
+        self.sel.run(logits, n=size)
+        sample_chosen(logits, self.sel.chosen[:size].view(size, *self.shape), self.seeds[:size], self.steps[:size],
+                      self.drawn[:size], self.err, self.sel.tokens[:size].view(size, *self.shape))
+
+
 class SelectGraphs:
     """One captured `select` per (bucket, slot) over an engine's static outputs and token rows
     (fast_ops.py:584-623). `engine` provides `device`, `graphs` (non-empty once captured), `outputs`
@@ -419,20 +509,31 @@ class SelectGraphs:
         self.engine, self.slots = engine, slots
         self.graphs = {}
         self._buckets = {}
+        self.batch = None
         if not getattr(engine, 'graphs', None):
             return
         outputs = engine.outputs
         self._buckets = {(out.data_ptr(), len(out)): size for size, out in outputs.items()}
-        keys = [(size, i) for size in sorted(outputs) for i in range(size)]
+        if PhiloxBatch.fits(slots, engine.tokens):
+            # 'philox' slots: one graph per bucket selects and samples all its windows.
+            batch = PhiloxBatch(slots, engine.tokens)
+            keys = sorted(outputs)
 
-        def body(key):
-            size, i = key
-            slots[i].select(outputs[size][i], engine.tokens[i])
+            def body(size):
+                batch.run(outputs[size], size)
+        else:
+            batch = None
+            keys = [(size, i) for size in sorted(outputs) for i in range(size)]
 
-        with _NothingSelected(slots), torch.inference_mode():
+            def body(key):
+                size, i = key
+                slots[i].select(outputs[size][i], engine.tokens[i])
+
+        with _NothingSelected(slots[:len(engine.tokens)]), torch.inference_mode():
             captured = StepGraphs(engine.device, body, keys, warmup=1)
             torch.cuda.synchronize(engine.device)
         self.graphs = captured.graphs
+        self.batch = batch if self.graphs else None
 
     def lookup(self, logits):
         return self._buckets.get((logits.data_ptr(), len(logits)))
@@ -444,6 +545,8 @@ def consume_batch(slots, logits, tokens, count, graphs=None):
     captured select when `logits` is a bucket's output), then the host collects the slots in order. Marking and
     finishing forwards go through `consume`. Returns {index: (finished, commit)} for the non-idle slots."""
     bucket = graphs.lookup(logits) if graphs is not None else None
+    if bucket is not None and graphs.batch is not None and bucket in graphs.graphs:
+        return _consume_batched(graphs, slots, logits, tokens, count, bucket)
     active = [(i, slots[i]) for i in range(count) if not slots[i].idle]
     queued = [(i, slot) for i, slot in active if slot.stageable()]
     handles = {}
@@ -452,4 +555,37 @@ def consume_batch(slots, logits, tokens, count, graphs=None):
         handles[i] = slot.stage(logits[i], tokens[i], graph)
     results = {i: slot.consume(logits[i], tokens[i]) for i, slot in active if i not in handles}
     results.update({i: slot.collect(handles[i]) for i, slot in queued})
+    return {i: results[i] for i in sorted(results)}
+
+
+def _consume_batched(graphs, slots, logits, tokens, count, bucket):
+    """consume_batch over a PhiloxBatch: one host-to-device copy of every window's step scalars, one graph replay
+    that selects and samples the bucket's windows, one device-to-host copy of their drawn classes and flags, and the
+    host bookkeeping per slot from the copied rows (marking and finishing forwards still go through `consume`)."""
+    batch = graphs.batch
+    active = [(i, slots[i]) for i in range(count) if not slots[i].idle]
+    queued = [(i, slot) for i, slot in active if slot.stageable()]
+    B = batch.batch
+    host = batch.host_scal.numpy()
+    host[:] = 0
+    frac = host[2 * B:3 * B].view(np.float64)
+    for i, slot in queued:
+        k, committed, f, step = slot.step_scalars()
+        host[i], host[B + i], frac[i], host[3 * B + i] = k, committed, f, step
+    batch.scal.copy_(batch.host_scal, non_blocking=True)
+    graphs.graphs[bucket].replay()
+    batch.host_drawn[:bucket].copy_(batch.drawn[:bucket].view(bucket, -1), non_blocking=True)
+    batch.host_bad[:bucket].copy_(batch.sel.bad[:bucket].view(torch.uint8), non_blocking=True)
+    batch.host_err.copy_(batch.err, non_blocking=True)
+    event = torch.cuda.Event()
+    event.record()
+    staged = {i for i, _ in queued}
+    results = {i: slot.consume(logits[i], tokens[i]) for i, slot in active if i not in staged}
+    event.synchronize()
+    if queued and int(batch.host_err[0]):
+        raise RuntimeError('probability tensor contains either `inf`, `nan` or element < 0')
+    drawn = batch.host_drawn.numpy()
+    bad = batch.host_bad.numpy()
+    for i, slot in queued:
+        results[i] = slot.commit_drawn(drawn[i], bool(bad[i]), tokens[i])
     return {i: results[i] for i in sorted(results)}

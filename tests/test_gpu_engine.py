@@ -207,13 +207,16 @@ def _drive(engine, slots, seeds, cap, staged):
     return commits, records, engine.tokens.clone(), forwards
 
 
-def test_engine_whole_window_staged_equals_eager_shipped_shape(dev):
+@pytest.mark.parametrize('sampler', ['multinomial', 'philox'])
+def test_engine_whole_window_staged_equals_eager_shipped_shape(dev, sampler):
     """8 slots of the shipped model's shape (304 classes, 256 x 16 x 16, 25 x 768 backbone, 13 x 384 control) with
-    full-capacity-class conditions; 26 forwards per window (marking + 25 solid steps)."""
+    full-capacity-class conditions; 26 forwards per window (marking + 25 solid steps). With the reference's
+    multinomial tail the staged path runs one captured selection per slot; with the counter-based sampler
+    SelectGraphs keeps the slots in one PhiloxBatch and a forward selects and samples all 8 windows in one graph."""
     from streamvoxel_amd import synth
     from streamvoxel_amd.stream.engine import SlotEngine
     from streamvoxel_amd.stream.slot import LowEntropyLastSlot
-    _case('engine shipped shape: whole window staged vs eager')
+    _case(f'engine shipped shape: whole window staged vs eager, sampler={sampler}')
     model = _model(dev, seed=1)
     spec = synth.WindowSpec()
     engine = SlotEngine(model, spec, dev, 8, l1_cap=8, l2_cap=256)
@@ -229,8 +232,11 @@ def test_engine_whole_window_staged_equals_eager_shipped_shape(dev):
     runs = []
     for staged in (True, False):
         slots = [LowEntropyLastSlot(engine.shape, spec.num_classes, (0,), air_token=0, last_eps=1e-4, block_size=4,
-                                    device=dev) for _ in range(8)]
+                                    device=dev, sampler=sampler) for _ in range(8)]
         runs.append(_drive(engine, slots, seeds, cap, staged))
+        if staged:
+            from streamvoxel_amd.stream.slot import PhiloxBatch
+            assert PhiloxBatch.fits(slots, engine.tokens) == (sampler == 'philox')
     (c_a, r_a, t_a, f_a), (c_b, r_b, t_b, f_b) = runs
     assert f_a == f_b == cap + 1
     assert torch.equal(t_a, t_b)
