@@ -85,6 +85,13 @@ constexpr int kKTile = kKB * kRow;  // bf16 elements of one K sub-tile
 constexpr int kThreads = 256;
 constexpr float kSumHigh = 1048576.0f;  // 2^20: a half's row sum above it makes the running max be raised
 constexpr float kMaxHigh = 20.0f;       // the same bound on a single score above the running max (log2 units)
+// The bf16 row-sum form issues a half's second product before it reads the half's row sum back: its stored max
+// is the running max plus kSpecBias, so P = exp2(S - m) stays below 2^-20 of the fast path's while m bounds the
+// scores, and P is clamped to 1 (the exponential's clamp modifier) so that a stale m cannot overflow O. A row sum
+// above kSpecHigh (a score more than about 19 above the running max, every clamped P among them) takes the half
+// back out of O and does it again against the raised max.
+constexpr float kSpecBias = 20.0f;
+constexpr float kSpecHigh = 0.5f;
 constexpr float kFltMax = 3.40282347e38f;
 // e4m3 second product: P is formed 2^4 above the running max and packed only while it stays below 448, the
 // largest e4m3 value: a score more than 4.8 above the running max (2^(4 + 4.8) = 445.7) raises the max first.
@@ -581,6 +588,10 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
   static_assert(!VD8 || (PV8 && VT), "direct e4m3 V^T loads serve the e4m3 second product");
   // bf16 P with no padding row for the row sum: the matrix cores form it from the packed P (see onesb).
   constexpr bool MSUM = !ONES && !PV8;
+  // MSUM over a bf16 cache at head_dim 64: a half's second product is issued before its row sum is read back (see
+  // compute). Every staging and masking takes the same form, so the layouts give the same bits. (Over an e4m3
+  // cache, staged through registers, the form measured no faster.)
+  constexpr bool SPEC = MSUM && !FP8 && DT == 2;
   constexpr int kSubTiles = Width<DT>::kSubTiles;
   // V^T tile: 32 DT rows of 64 keys, bf16 (kRow elements a row) or e4m3 (kRow8 bytes a row).
   constexpr int kVTile = PV8 ? 32 * DT * kRow8 / 2 : 32 * DT * kRow;
@@ -901,12 +912,13 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
     const uint64_t bits = block_bits(kv0);
     [[maybe_unused]] uint32_t pf[8];  // PV8: e4m3 P, bytes 16 t + i
     [[maybe_unused]] int drop = 0;    // PV8: halvings of half 0 since it was packed
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      // S^T of keys 32 t .. 32 t + 31 (LDS rows 32 t + col); k-steps past head_dim (zero in Q) are skipped.
-      SVHIP_TRACE(trace.mark(5 * t);)
+    // S^T of keys 32 t .. 32 t + 31 of the block (LDS rows 32 t + col), keys past L (and, with a key mask, keys
+    // not attended) at -inf; k-steps past head_dim (zero in Q) are skipped.
+    // LEAN: one K operand in registers at a time (the rare path, where registers are short).
+    auto score = [&](int t, auto lean) __attribute__((always_inline)) -> f32x16_t {
+      constexpr bool LEAN = decltype(lean)::value;
       f32x16_t s;
-      if constexpr (FULLK) {
+      if constexpr (FULLK && !LEAN) {
         bf16x8_t a[2 * DT];
 #pragma unroll
         for (int k = 0; k < 2 * DT; ++k) {
@@ -938,6 +950,12 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
           if (KMASK && !((mine >> i) & 1u)) s[i] = -INFINITY;
         }
       }
+      return s;
+    };
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      SVHIP_TRACE(trace.mark(5 * t);)
+      f32x16_t s = score(t, std::false_type{});
       if constexpr (PV8) {
         half_pv8(t, s, pf, drop);
         continue;
@@ -948,6 +966,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
       // The row sum is taken over the packed (bf16-rounded) P that the second product reads, so a dominant key's
       // rounding cancels in O / l.
       bf16x8_t pb[2];
+      [[maybe_unused]] float late;  // SPEC: the half's row sum, read after the second product is issued
       auto exps = [&]() __attribute__((always_inline)) {
         const float nm = -m;
 #pragma unroll
@@ -956,6 +975,10 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
           for (int j = 0; j < 8; j += 2) {
             f32x2_t two = {__builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j], sl2, nm)),
                            __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * ks + j + 1], sl2, nm))};
+            if constexpr (SPEC) {  // folded into the exponentials as their clamp modifier
+              two[0] = __builtin_amdgcn_fmed3f(two[0], 0.f, 1.f);
+              two[1] = __builtin_amdgcn_fmed3f(two[1], 0.f, 1.f);
+            }
             const bf16x2_t c = __builtin_convertvector(two, bf16x2_t);
             pb[ks][j] = c[0];
             pb[ks][j + 1] = c[1];
@@ -976,11 +999,11 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
       // v_permlane32_swap, which gives (x[l % 32], x[l % 32 + 32]) in every lane, scaled to log2 units; m raised to
       // it, O and l rescaled, P redone against the new m. Every query has a key below L in the first half, so m is
       // finite after it.
-      auto raise = [&](float mx) __attribute__((always_inline)) {
+      auto rebase = [&](float mx) __attribute__((always_inline)) {
         first = false;
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
         const float mr = __builtin_amdgcn_fmed3f(__int_as_float(sw[0]), __int_as_float(sw[1]), kFltMax);
-        const float cand = mr * sl2;
+        const float cand = SPEC ? __builtin_fmaf(mr, sl2, kSpecBias) : mr * sl2;
         float mn = (cand > m || (KMASK && placeholder)) ? cand : m;
         // Only with a key mask can a query have seen no attended key yet (every score -inf): its running max is
         // then set to 0, with O and l still 0, so that later scores are taken against a finite bias, and the lane is
@@ -999,23 +1022,50 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
 #pragma unroll
           for (int j = 0; j < DT; ++j) o[j][i] *= alpha;
         }
+      };
+      auto raise = [&](float mx) __attribute__((always_inline)) {
+        rebase(mx);
         exps();
       };
-      auto half_max = [&]() __attribute__((always_inline)) {
-        float mx = __builtin_amdgcn_fmed3f(s[0], s[1], kFltMax);
+      auto half_max = [&](const f32x16_t& x) __attribute__((always_inline)) {
+        float mx = __builtin_amdgcn_fmed3f(x[0], x[1], kFltMax);
 #pragma unroll
-        for (int i = 2; i < 16; i += 2) mx = max3(mx, s[i], s[i + 1]);
+        for (int i = 2; i < 16; i += 2) mx = max3(mx, x[i], x[i + 1]);
         return mx;
+      };
+      // O^T += V^T . P^T: for k-step ks, V^T columns 32 t + 16 ks + 8 hh + 0..7 are logical chunk 2 (2 t + ks) + hh
+      // of rows 32 j + col.
+      auto pv = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          bf16x8_t a[DT];
+#pragma unroll
+          for (int j = 0; j < DT; ++j) {
+            a[j] = *reinterpret_cast<const bf16x8_t*>(vp + rd[2 * t + ks] + j * (32 * kRow * 2));
+          }
+#pragma unroll
+          for (int j = 0; j < DT; ++j) o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], pb[ks], o[j], 0, 0, 0);
+        }
       };
       if constexpr (ONES) {
         // The half's own max decides: a score more than kMaxHigh above m raises it (P of the fast path stays
         // below 2^kMaxHigh); the row sum accumulates in O^T row D.
-        const float mx = half_max();
+        const float mx = half_max(s);
         exps();
         if (first || __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, sl2, -m) > kMaxHigh || (KMASK && placeholder)) !=
                          0ull) {
           raise(mx);
         }
+      } else if constexpr (SPEC) {
+        // The second product does not wait for the row sum: P is formed against m as it stands (on the window's
+        // first half, where m is -inf, against the half's own max), the row sum is issued, then the second
+        // product, and the sum is read back after it (below), when the matrix core has long produced it.
+        if (first) rebase(half_max(s));
+        SVHIP_TRACE(trace.mark_after(5 * t + 1, __builtin_amdgcn_fmed3f(s[15], s[14], kFltMax));)
+        exps();
+        SVHIP_TRACE(trace.mark_after(5 * t + 2, __builtin_bit_cast(float, __builtin_bit_cast(uint4, pb[1]).w));)
+        late = half_sum();
+        __builtin_amdgcn_sched_barrier(0);  // the row sum's products go to the matrix core before the second's
       } else if constexpr (MSUM) {
         // The half's sum shows whether m still bounds its scores: above kSumHigh = 2^20 (or inf / NaN) some
         // score passed m by about 20 (log2 units). Only then (and on the window's first half, where m is -inf)
@@ -1026,20 +1076,36 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
         float hs = half_sum();
         SVHIP_TRACE(trace.mark_after(5 * t + 3, __builtin_amdgcn_fmed3f(hs, hs, kFltMax));)
         if (first || __builtin_amdgcn_ballot_w64(!(hs <= kSumHigh) || (KMASK && placeholder)) != 0ull) {
-          raise(half_max());
+          raise(half_max(s));
           hs = half_sum();
         }
         l += hs;
       }
+      pv();
+      if constexpr (SPEC) {
+        // A row sum above kSpecHigh: some score passed m by about 19 or more (log2 units), and the P of the scores
+        // more than 20 above it were clamped. The half is taken back out of O (the second product again with -P;
+        // l has not taken its sum), m is raised to the half's max, O and l rescaled, and the half done again; the
+        // scores and P are formed again from the tile rather than held through the product. Rare: m is then within 20
+        // of every score to come up to the next raise. With a key mask a query that has seen no attended key yet
+        // (m a placeholder) takes this path too, as it takes the raise in the other forms.
+        SVHIP_TRACE(trace.mark_after(5 * t + 3, __builtin_amdgcn_fmed3f(late, late, kFltMax));)
+        if (__builtin_amdgcn_ballot_w64(!(late <= kSpecHigh) || (KMASK && placeholder)) != 0ull) {
+          s = score(t, std::true_type{});
+          exps();  // the same P again (the same products and m), negated
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        // O^T += V^T . P^T for this k-step: V^T columns 32 t + 16 ks + 8 hh + 0..7 are logical chunk 2 (2 t + ks) + hh
-        // of rows 32 j + col.
-        bf16x8_t a[DT];
-#pragma unroll
-        for (int j = 0; j < DT; ++j) a[j] = *reinterpret_cast<const bf16x8_t*>(vp + rd[2 * t + ks] + j * (32 * kRow * 2));
-#pragma unroll
-        for (int j = 0; j < DT; ++j) o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], pb[ks], o[j], 0, 0, 0);
+          for (int ks = 0; ks < 2; ++ks) {
+            const uint4 x = __builtin_bit_cast(uint4, pb[ks]);
+            pb[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(x.x ^ 0x80008000u, x.y ^ 0x80008000u, x.z ^ 0x80008000u,
+                                                              x.w ^ 0x80008000u));
+          }
+          pv();
+          rebase(half_max(s));
+          exps();
+          late = half_sum();
+          pv();
+        }
+        l += late;
       }
       SVHIP_TRACE(trace.mark_after(5 * t + 4, o[DT - 1][15], l);)
     }

@@ -280,6 +280,47 @@ def test_score_scale_jumps_between_key_halves(dev, transposed, D):
     check(out, ref, BF16_ATOL, BF16_RTOL)
 
 
+@pytest.mark.parametrize('jump', [12.0, 30.0, 100.0, 1000.0])
+def test_second_product_taken_back_on_score_jumps(dev, jump):
+    """Scores (in nats) that jump by `jump`, 2 `jump`, ... above the window's earlier ones at keys past the first
+    half, so that a half's second product was issued against a running max that no longer bounds it: from a few
+    clamped weights (12) to weights far beyond the fp32 range against the stale max (1000). Within the bf16 bar
+    of float64, and the same bits on every staging at head_dim 64: V^T direct, V rows through registers, the packed
+    layout, and a prefix key mask."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, kcap, D = 2, 2, 64, 640, 64
+    lengths = [640, 333]
+    _case(f'xattn score jumps of {jump} nats after the first half, every staging')
+    g = torch.Generator().manual_seed(int(jump))
+    logits = torch.randn(B, H, kcap, generator=g)
+    for i, key in enumerate([40, 100, 170, 300, 600]):
+        logits[:, :, key] += jump * (i + 1)
+    q = torch.zeros(B, H, Q, D)
+    q[..., 0] = 1.0
+    q[..., 1:] = torch.randn(B, H, Q, D - 1, generator=g) * 0.1
+    k = torch.randn(B, H, kcap, D, generator=g) * 0.1
+    k[..., 0] = logits * math.sqrt(D)          # the score of key j is logits[j] plus a little per query
+    v = torch.randn(B, H, kcap, D, generator=g)
+    q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    ref = A.cross_attention(q, k, v, lengths)
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    qd, kd = q.to(dev), k.to(dev)
+    vt = v.transpose(2, 3).contiguous().to(dev).transpose(2, 3)
+    direct = attention(qd, kd, vt, lengths=lt)
+    rows = attention(qd, kd, v.to(dev), lengths=lt)
+    masked = attention(qd, kd, vt, key_mask=torch.arange(kcap, device=dev)[None] < lt[:, None])
+    cu = torch.tensor([0, lengths[0], sum(lengths)], dtype=torch.int32, device=dev)
+    kp = torch.cat([k[i, :, :lengths[i]] for i in range(B)], 1).to(dev)
+    vpt = torch.cat([v[i, :, :lengths[i]] for i in range(B)], 1).transpose(1, 2).contiguous().to(dev)
+    packed = attention(qd, kp, vpt.transpose(1, 2), cu_seqlens=cu)
+    torch.cuda.synchronize()
+    assert torch.isfinite(direct.float()).all()
+    check(direct, ref, BF16_ATOL, BF16_RTOL)
+    assert torch.equal(direct, rows)
+    assert torch.equal(direct, masked)
+    assert torch.equal(direct, packed)
+
+
 @pytest.mark.parametrize('p_dtype', ['e4m3', 'bf16'])
 @pytest.mark.parametrize('transposed,D', [(True, 64), (False, 64), (True, 48), (True, 96)])
 def test_e4m3_score_jumps_between_key_halves(dev, transposed, D, p_dtype):
