@@ -54,7 +54,8 @@ def parse():
     p.add_argument('--forward-only', action='store_true',
                    help='time only the whole-step forward (shipped shape) and print its line')
     p.add_argument('--no-c5', action='store_true', help='skip the 64-slot e4m3 stress component')
-    p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'select', 'select_planes', 'c5_xattn', 'c5'],
+    p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'select', 'select_planes', 'select_c304', 'c5_xattn',
+                                        'c5'],
                    help='build only that kernel\'s inputs (the step\'s layer-0 attention or its first solid '
                         'selection), time 20 back-to-back launches and print one line: the run to profile')
     return p.parse_args()
@@ -503,11 +504,30 @@ def c5_component(dev, seed):
     return out
 
 
+def shipped_select(dev, quotas, reps):
+    """The shipped model's selection input, the class head's bf16 rows of 304 classes (autocast) in patch order, for
+    8 fresh windows with the given step quotas: (seconds per call of `EaseSelect.run`, bytes per call)."""
+    import torch
+    from streamvoxel_amd import synth
+    from streamvoxel_amd.stream.patches import PatchLogits
+    from streamvoxel_amd.stream.step import EaseSelect
+    classes = 304
+    sel = EaseSelect(SLOTS, SHAPE, classes, BLOCK, dev)
+    for b in range(SLOTS):
+        sel.bind_window(b, torch.randperm(VOXELS // BLOCK ** 3, generator=torch.Generator().manual_seed(b)))
+        sel.set_step(b, quotas[b], 0, quotas[b] / VOXELS)
+    rows = synth.bimodal_logits(SLOTS * VOXELS, classes, 0.7, seed=304, device=dev).to(torch.bfloat16)
+    logits = PatchLogits(rows.view(SLOTS, VOXELS // 64, 64 * classes), SHAPE, 4, classes)
+    t = time_graph(lambda: sel.run(logits), reps)
+    return t, SLOTS * VOXELS * (classes * 2 + 8 + 1 + 1)
+
+
 def kernel_only(dev, args):
     """One kernel of the step alone, on the step's own inputs: the cross-attention layer (8 windows, 12 x 64 heads,
     1024 queries, the step's key lengths; bf16 or e4m3 cache) or the first solid selection (8 windows, fp32 logits
-    [8 x 65536, 256] as voxel rows, or as class planes [8, 256, 65536] for `select_planes`; fresh token state). 20
-    launches in one graph, replayed 5 times."""
+    [8 x 65536, 256] as voxel rows, or as class planes [8, 256, 65536] for `select_planes`; the shipped model's bf16
+    rows of 304 classes in patch order for `select_c304`; fresh token state). 20 launches in one graph, replayed 5
+    times."""
     import torch
     from streamvoxel_amd import synth
     from streamvoxel_amd.stream.step import CachedContext, EaseSelect
@@ -534,6 +554,9 @@ def kernel_only(dev, args):
         flops = 4 * HEADS * HEAD_DIM * QUERIES * sum(lengths)
         return dict(kernel=args.kernel, us_per_launch=t * 1e6, TFLOPs=flops / t / 1e12, flops_per_launch=flops,
                     kv_lengths=lengths)
+    if args.kernel == 'select_c304':         # the shipped model's input: bf16 rows of 304 classes in patch order
+        t, nbytes = shipped_select(dev, [VOXELS // (STEPS_PER_WINDOW - 1)] * SLOTS, 20)
+        return dict(kernel=args.kernel, us_per_call=t * 1e6, GBps=nbytes / t / 1e9, bytes_per_call=nbytes)
     sel = EaseSelect(SLOTS, SHAPE, CLASSES, BLOCK, dev, air_ids=(0,))
     logits = torch.empty(SLOTS * VOXELS, CLASSES, device=dev)
     synth.bimodal_logits_(logits, 0.7, generator=g)
@@ -624,18 +647,7 @@ def main():
     t_select_patches = time_graph(lambda: w.sel.run(patch_logits), 20)
     t_permute = time_graph(lambda: patch_logits.class_major(), 20)
     del patch_logits
-    # The shipped model's selection input: the class head's bf16 rows of 304 classes (autocast), in patch order.
-    from streamvoxel_amd.stream.step import EaseSelect
-    shipped_classes = 304
-    sel304 = EaseSelect(SLOTS, SHAPE, shipped_classes, BLOCK, dev)
-    for b in range(SLOTS):
-        sel304.bind_window(b, torch.randperm(VOXELS // BLOCK ** 3, generator=torch.Generator().manual_seed(b)))
-        sel304.set_step(b, w.quotas[b][0], 0, w.quotas[b][0] / VOXELS)
-    rows304 = synth.bimodal_logits(SLOTS * VOXELS, shipped_classes, 0.7, seed=304, device=dev).to(torch.bfloat16)
-    logits304 = PatchLogits(rows304.view(SLOTS, VOXELS // 64, 64 * shipped_classes), SHAPE, 4, shipped_classes)
-    t_select304 = time_graph(lambda: sel304.run(logits304), 20)
-    bytes304 = SLOTS * VOXELS * (shipped_classes * 2 + 8 + 1 + 1)
-    del sel304, logits304, rows304
+    t_select304, bytes304 = shipped_select(dev, [w.quotas[b][0] for b in range(SLOTS)], 20)
     # The same layer over an e4m3 cache (per-(window, head) scales, written by svhip_kv_write from layer 0's keys).
     from streamvoxel_amd.stream.step import CachedContext
     ctx8 = CachedContext(1, SLOTS, HEADS, HEAD_DIM, synth.MAX_KEYS, dev, kv_dtype='fp8')

@@ -75,11 +75,12 @@ __device__ __forceinline__ void load16(const T* p, float* dst) {
 }
 
 // One logit of the canonical order into a lane's sums (the same instructions in every pass), in log2 units:
-// t = (x - max) log2(e) (the difference exact, so the row's max gives t = 0 and a one-hot row entropy 0), p = 2^t,
-// s += p, w += p t (entropy) or w += p (air classes). finish_stat turns (s, w) into the statistic.
+// t = x log2(e) - mL with mL = max log2(e) rounded (one FMA; the row's max gets t = delta, the rounding of mL, the
+// same for every voxel element equal to the max), p = 2^t, s += p, w += p t (entropy) or w += p (air classes). A
+// common shift of t leaves the statistic unchanged; finish_stat turns (s, w) into it.
 template <int MODE>
-__device__ __forceinline__ void accumulate(float x, float m, int c, const uint32_t* air_bits, float& s, float& w) {
-  const float t = (x - m) * kLog2e;
+__device__ __forceinline__ void accumulate(float x, float mL, int c, const uint32_t* air_bits, float& s, float& w) {
+  const float t = __builtin_fmaf(x, kLog2e, -mL);
   const float p = __builtin_amdgcn_exp2f(t);
   s += p;
   if constexpr (MODE == kEntropy) {
@@ -118,10 +119,17 @@ constexpr int kCanonTile = 32;       // voxels per LDS tile
 __host__ inline size_t canon_lds_bytes(int64_t C) { return sizeof(float) * kCanonTile * (C + 1); }
 
 // sum p log p / sum p - log sum p with p = 2^t: (w / s - log2 s) ln 2 (entropy, w = sum p t in log2 units), or the
-// air classes' share w / s.
+// air classes' share w / s. pm = the max's own p (max_p): a sum that is exactly that is a row whose other p vanish
+// beside it (a one-hot row), whose statistic is 0 (within 1e-6 of it whenever the sum takes nothing else).
 template <int MODE>
-__device__ __forceinline__ float finish_stat(float s, float w) {
+__device__ __forceinline__ float max_p(float m, float mL) {
+  return __builtin_amdgcn_exp2f(__builtin_fmaf(m, kLog2e, -mL));
+}
+
+template <int MODE>
+__device__ __forceinline__ float finish_stat(float s, float w, float pm) {
   if constexpr (MODE == kEntropy) {
+    if (s == pm) return 0.f;
     return (w / s - __builtin_amdgcn_logf(s)) * kLn2;
   } else {
     return w / s;
@@ -195,17 +203,18 @@ __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_
 #pragma unroll
     for (int e = 0; e < NV * E; ++e) m = fmaxf(m, v[e]);
     m = group_max<LPV>(m);
+    const float mL = m * kLog2e;
     float s = 0.f, w = 0.f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       if (j < vfull || g + LPV * j < vecs) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) accumulate<MODE>(v[j * E + e], m, (g + LPV * j) * E + e, air_bits, s, w);
+        for (int e = 0; e < E; ++e) accumulate<MODE>(v[j * E + e], mL, (g + LPV * j) * E + e, air_bits, s, w);
       }
     }
     s = group_sum<LPV>(s);
     w = group_sum<LPV>(w);
-    if (g == 0) out.store(voxel, finish_stat<MODE>(s, w), pre);
+    if (g == 0) out.store(voxel, finish_stat<MODE>(s, w, max_p<MODE>(m, mL)), pre);
     i += smod;
     b += sdiv;
     if (i >= n) {
@@ -309,19 +318,20 @@ __device__ __forceinline__ void canonical_tile_pass(const T* __restrict__ x, int
 #pragma unroll
       for (int e = 0; e < 8 * E; ++e) m = fmaxf(m, v[e]);
       m = group_max<LPV>(m);
+      const float mL = m * kLog2e;
       float s = 0.f, w = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
           const int c = (g + LPV * j) * E + e;
-          if (j < nv && c < C) accumulate<MODE>(v[j * E + e], m, c, air_bits, s, w);
+          if (j < nv && c < C) accumulate<MODE>(v[j * E + e], mL, c, air_bits, s, w);
         }
       }
       s = group_sum<LPV>(s);
       w = group_sum<LPV>(w);
       const int64_t i = i0 + vi;
-      if (g == 0 && i < n) out.store(b * n + i, finish_stat<MODE>(s, w), pre[r]);
+      if (g == 0 && i < n) out.store(b * n + i, finish_stat<MODE>(s, w, max_p<MODE>(m, mL)), pre[r]);
     }
   }
 }
@@ -343,10 +353,11 @@ __device__ __forceinline__ void class_major_pass(const T* __restrict__ x, int64_
 #pragma unroll
     for (int u = 0; u < VPL; ++u) pre[u] = out.prefetch(b * n + (i0 + u < n ? i0 + u : n - 1));
     const T* base = x + b * sb + i0 * sn;
-    float m[VPL], s[VPL], w[VPL];
+    float m[VPL], mL[VPL], s[VPL], w[VPL];
 #pragma unroll
     for (int u = 0; u < VPL; ++u) {
       m[u] = -INFINITY;
+      mL[u] = -INFINITY;
       s[u] = 0.f;
       w[u] = 0.f;
     }
@@ -375,7 +386,8 @@ __device__ __forceinline__ void class_major_pass(const T* __restrict__ x, int64_
         for (int r = 1; r < CH; ++r) cm = fmaxf(cm, v[r][u]);
         const float mn = fmaxf(m[u], cm);
         if (mn > m[u]) {
-          const float d = (m[u] - mn) * kLog2e;   // log2 units, like w
+          const float mLn = mn * kLog2e;
+          const float d = mL[u] - mLn;   // the shift of t, log2 units like w
           const float rs = __builtin_amdgcn_exp2f(d);
           if constexpr (MODE == kEntropy) {
             w[u] = (s[u] == 0.f) ? 0.f : (w[u] + s[u] * d) * rs;
@@ -384,16 +396,17 @@ __device__ __forceinline__ void class_major_pass(const T* __restrict__ x, int64_
           }
           s[u] *= rs;
           m[u] = mn;
+          mL[u] = mLn;
         }
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
-          if (c0 + r < C) accumulate<MODE>(v[r][u], m[u], static_cast<int>(c0 + r), air_bits, s[u], w[u]);
+          if (c0 + r < C) accumulate<MODE>(v[r][u], mL[u], static_cast<int>(c0 + r), air_bits, s[u], w[u]);
         }
       }
     }
 #pragma unroll
     for (int u = 0; u < VPL; ++u) {
-      if (i0 + u < n) out.store(b * n + i0 + u, finish_stat<MODE>(s[u], w[u]), pre[u]);
+      if (i0 + u < n) out.store(b * n + i0 + u, finish_stat<MODE>(s[u], w[u], max_p<MODE>(m[u], mL[u])), pre[u]);
     }
   }
 }
