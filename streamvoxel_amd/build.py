@@ -1,6 +1,8 @@
 """Builds libsvhip.so (all HIP sources under csrc/) for gfx950 with hipcc, in-tree next to this file.
 
     python -m streamvoxel_amd.build            # or streamvoxel_amd.build.build()
+    python -m streamvoxel_amd.build --trace    # also the wave-timeline library (libsvhip_trace.so)
+    python -m streamvoxel_amd.build --microbench   # also microbench/xattn_chain (the attention half taken apart)
 """
 from __future__ import annotations
 
@@ -54,6 +56,20 @@ def build_trace(verbose=False):
     return TRACE_LIB
 
 
+MICROBENCH = os.path.join(HERE, 'microbench', 'xattn_chain')
+
+
+def build_microbench():
+    """The standalone program microbench/xattn_chain.hip (no library): the cross-attention half's instructions with
+    its dependencies, one ingredient at a time."""
+    flags = [f for f in FLAGS if f not in ('-shared', '-fPIC')]
+    res = subprocess.run([hipcc(), *flags, MICROBENCH + '.hip', '-o', MICROBENCH], stdout=subprocess.PIPE,
+                         stderr=subprocess.STDOUT)
+    if res.returncode != 0:
+        raise RuntimeError('hipcc failed (microbench):\n' + res.stdout.decode(errors='replace'))
+    return MICROBENCH
+
+
 def build(verbose=False, jobs=4):
     """Compile each source to an object in parallel, then link the shared library. Returns the library path."""
     objdir = os.path.join(HERE, '_build')
@@ -91,3 +107,5 @@ if __name__ == '__main__':
     print(build(verbose='-v' in sys.argv))
     if '--trace' in sys.argv:
         print(build_trace())
+    if '--microbench' in sys.argv:
+        print(build_microbench())
