@@ -12,6 +12,8 @@
 //                        before the barrier; the 8 workgroups that share a block's data sit on one XCD, as the
 //                        kernel places the query tiles of a (window, head)
 //   64 queries a wave    the last form with two query tiles a wave: every LDS operand read feeds two products
+//   priority 1 / 2       the staged form with the wave's issue priority raised (s_setprio 1) while it issues its
+//                        score products (1), or its score and second products (2), and lowered for its softmax
 //
 // Build: python -m streamvoxel_amd.build --microbench   Run: streamvoxel_amd/microbench/xattn_chain
 #include <hip/hip_runtime.h>
@@ -53,8 +55,9 @@ __device__ __forceinline__ void softmax(const f32x16_t& s, float sl2, float nm, 
   }
 }
 
-// QT query tiles of 32 a wave (1 or 2); `kv` holds 96 units of `ublocks` 16 KB blocks (staged forms only).
-template <int FORM, int WAVES, int QT = 1>
+// QT query tiles of 32 a wave (1 or 2); `kv` holds 96 units of `ublocks` 16 KB blocks (staged forms only). PRIO:
+// 0 none, 1 raised around the score products, 2 around the score and the second products.
+template <int FORM, int WAVES, int QT = 1, int PRIO = 0>
 __global__ __launch_bounds__(256, WAVES) void half_kernel(float* out, const float* in, const uint16_t* kv,
                                                           int ublocks, int iters) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[2][kTileElems];
@@ -121,12 +124,14 @@ __global__ __launch_bounds__(256, WAVES) void half_kernel(float* out, const floa
       }
     }
     f32x16_t s[QT];
+    if constexpr (PRIO >= 1) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int u = 0; u < QT; ++u) {
       s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak[0], q[u][0], f32x16_t{0}, 0, 0, 0);
 #pragma unroll
       for (int k = 1; k < 4; ++k) s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak[k], q[u][k], s[u], 0, 0, 0);
     }
+    if constexpr (PRIO >= 1) __builtin_amdgcn_s_setprio(0);
     bf16x8_t pb[QT][2];
     f32x4_t h[QT];
 #pragma unroll
@@ -143,6 +148,7 @@ __global__ __launch_bounds__(256, WAVES) void half_kernel(float* out, const floa
       h[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[u][0], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
       h[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[u][1], h[u], 0, 0, 0);
     }
+    if constexpr (PRIO >= 2) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       bf16x8_t av[2];
@@ -160,6 +166,7 @@ __global__ __launch_bounds__(256, WAVES) void half_kernel(float* out, const floa
         o[u][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[1], pb[u][ks], o[u][1], 0, 0, 0);
       }
     }
+    if constexpr (PRIO >= 2) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int u = 0; u < QT; ++u) {
       if constexpr (FORM >= kBlock) {
@@ -182,18 +189,18 @@ __global__ __launch_bounds__(256, WAVES) void half_kernel(float* out, const floa
 
 constexpr int kUnits = 96, kUnitBlocks = 128;  // 2 MB of blocks a unit, 192 MB in all
 
-template <int FORM, int WAVES, int QT = 1>
+template <int FORM, int WAVES, int QT = 1, int PRIO = 0>
 double run(const char* name, float* out, const float* in, const uint16_t* kv, int iters, double ref_ns) {
   const int grid = 256 * WAVES;  // WAVES workgroups of 4 waves per CU: WAVES waves on every SIMD
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
-  half_kernel<FORM, WAVES, QT><<<grid, 256>>>(out, in, kv, kUnitBlocks, iters);
+  half_kernel<FORM, WAVES, QT, PRIO><<<grid, 256>>>(out, in, kv, kUnitBlocks, iters);
   CHECK(hipGetLastError());
   CHECK(hipDeviceSynchronize());
   const int reps = 5;
   CHECK(hipEventRecord(e0));
-  for (int r = 0; r < reps; ++r) half_kernel<FORM, WAVES, QT><<<grid, 256>>>(out, in, kv, kUnitBlocks, iters);
+  for (int r = 0; r < reps; ++r) half_kernel<FORM, WAVES, QT, PRIO><<<grid, 256>>>(out, in, kv, kUnitBlocks, iters);
   CHECK(hipEventRecord(e1));
   CHECK(hipEventSynchronize(e1));
   float ms;
@@ -233,6 +240,9 @@ int main() {
   run<kStaged, 1>("+ staging", out, in, kv, iters, p3);
   run<kStaged, 3, 2>("64 queries a wave", out, in, kv, iters, p3);
   run<kStaged, 2, 2>("64 queries a wave", out, in, kv, iters, p3);
+  run<kStaged, 3, 1, 1>("+ staging, priority 1", out, in, kv, iters, p3);
+  run<kStaged, 3, 1, 2>("+ staging, priority 2", out, in, kv, iters, p3);
+  run<kStaged, 2, 1, 2>("+ staging, priority 2", out, in, kv, iters, p3);
   CHECK(hipFree(kv));
   CHECK(hipFree(out));
   CHECK(hipFree(in));
