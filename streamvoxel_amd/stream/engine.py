@@ -42,6 +42,20 @@ class Encoded(NamedTuple):
     positions: torch.Tensor
 
 
+def default_encoder(model, spec, device):
+    """The encoder a worker gets when it passes none, as `worker.py:272` constructs `FastSlotForward`: for the
+    reference's models (those with `encode_group`) the reference package's own `encode_item`
+    (streamvoxel/stream/engine.py:75-87) when that package is importable, its (prefix, local, positions) as an
+    `Encoded`; otherwise None (`load_slot` then takes an `Encoded` itself)."""
+    if not hasattr(model, 'encode_group'):
+        return None
+    try:
+        from streamvoxel.stream.engine import encode_item
+    except ImportError:
+        return None
+    return lambda item: Encoded(*encode_item(model, item, spec, device))
+
+
 def condition_widths(model, spec):
     """Tokens one L1 tile, one L2 tile and the biome window contribute (streamvoxel/stream/engine.py:62-74): an L1
     tile is its 4^3 patches, an L2 tile its 16^3 patches, the biome window (height/4) x 12 x 12 cells at halo 16
@@ -164,8 +178,9 @@ class SlotEngine:
 
     Capacity per slot: l2_cap L2 tiles of prefix keys and l1_cap L1 tiles plus the biome window of local keys
     (`condition_widths`), rounded up to the kernel's 64-key block. `encoder(item) -> Encoded` turns a scheduler
-    item into the condition (for the reference's model: `lambda item: encode_item(model, item, spec, device)`);
-    without one, `load_slot` takes an `Encoded` (or a (prefix, local, positions) tuple) itself.
+    item into the condition (for the reference's model: `lambda item: encode_item(model, item, spec, device)`, which
+    `default_encoder` supplies when none is passed and the reference's package is importable); without one,
+    `load_slot` takes an `Encoded` (or a (prefix, local, positions) tuple) itself.
     `kv_dtype` 'bf16' (the reference's cache) or 'fp8' (e4m3 with per-(window, head) scales). `concurrent` runs the
     control branch on its own stream inside the step. `patchify`, `attention` and `compile` are the reference's
     option names (fast_ops.py:168-171): 'gather' and 'conv' both run the HIP gather patchify, bit for bit the
@@ -182,7 +197,8 @@ class SlotEngine:
             raise RuntimeError('SlotEngine runs on a HIP device; there is no CPU path')
         if self.device.index is None:
             self.device = torch.device('cuda', torch.cuda.current_device())
-        self.model, self.spec, self.encoder = model, spec, encoder
+        self.model, self.spec = model, spec
+        self.encoder = encoder if encoder is not None else default_encoder(model, spec, self.device)
         self.batch, self.l1_cap, self.l2_cap = int(batch), int(l1_cap), int(l2_cap)
         if self.batch < 1:
             raise ValueError('batch must be at least 1')

@@ -68,3 +68,37 @@ def test_synthetic_condition_layout():
     assert isinstance(c, Encoded) and len(c.prefix) == 1
     assert c.prefix[0][0].shape == (4, 5, 12) and c.prefix[0][0].dtype == torch.bfloat16
     assert c.local.shape == (1, 7, 48) and c.positions.shape == (1, 7, 3)
+
+
+def test_default_encoder_is_the_reference_packages_encode_item(monkeypatch):
+    """A worker constructs the engine without an encoder (worker.py:272): for a model with `encode_group` the engine
+    takes the reference package's `encode_item` when that package is importable (here a stand-in module), and
+    wraps its (prefix, local, positions) as an Encoded; a model without `encode_group`, or no package, gives None."""
+    import sys
+    import types
+    from streamvoxel_amd.stream.engine import Encoded, default_encoder
+
+    calls = []
+
+    def encode_item(model, item, spec, device):
+        calls.append((model, item, spec, device))
+        return ['prefix'], 'local', 'positions'
+
+    class RefModel:
+        def encode_group(self, group):
+            return group
+
+    pkg, sub, mod = types.ModuleType('streamvoxel'), types.ModuleType('streamvoxel.stream'), \
+        types.ModuleType('streamvoxel.stream.engine')
+    mod.encode_item = encode_item
+    monkeypatch.setitem(sys.modules, 'streamvoxel', pkg)
+    monkeypatch.setitem(sys.modules, 'streamvoxel.stream', sub)
+    monkeypatch.setitem(sys.modules, 'streamvoxel.stream.engine', mod)
+    model, spec = RefModel(), object()
+    enc = default_encoder(model, spec, 'cuda:0')
+    out = enc('item')
+    assert isinstance(out, Encoded) and out.prefix == ['prefix'] and out.local == 'local'
+    assert calls == [(model, 'item', spec, 'cuda:0')]
+    assert default_encoder(object(), spec, 'cuda:0') is None          # not a reference model
+    monkeypatch.setitem(sys.modules, 'streamvoxel.stream.engine', None)  # the package is not importable
+    assert default_encoder(model, spec, 'cuda:0') is None
