@@ -1,7 +1,8 @@
 """The slot engine (`SlotEngine`, the reference's `FastSlotForward` surface) on the GPU: slot loads into the cache,
-one graph per bucket equal to the eager step bit for bit, the numerical gate, and whole windows driven the way the
-reference's worker drives them (`replay(timesteps, count)` + `SelectGraphs` + `consume_batch`) equal to the eager
-path (`eager` + per-slot `consume`) commit for commit."""
+the captured step against the float64 oracle step over the engine's own cache, one graph per bucket equal to the
+eager step bit for bit, the numerical gate, and whole windows driven the way the reference's worker drives them
+(`replay(timesteps, count)` + `SelectGraphs` + `consume_batch`) equal to the eager path (`eager` + per-slot
+`consume`) commit for commit."""
 import numpy as np
 import pytest
 import torch
@@ -78,6 +79,38 @@ def test_engine_layout_and_loads(dev):
         engine.load_slot(0, synth.condition(model, 33, 10, seed=1, device=dev))
     with pytest.raises(IndexError):
         engine.load_slot(5, conds[0])
+
+
+def test_engine_replay_against_oracle(dev):
+    """The engine's captured step over slots it loaded itself (the prefix keys, and the local keys it projected and
+    rotated) against the float64 oracle step over the cache it wrote: the engine's numbers pinned to the oracle, not
+    only to its own eager path. Tolerances as the step forward's (tests/test_gpu_forward.py): the class-head rows
+    within 4e-2 of max |reference| (max-abs) and 1e-2 of mean |reference| (mean-abs)."""
+    from oracle import backbone as O
+    from streamvoxel_amd import synth
+    _case('engine small: replay against the float64 oracle step over the engine\'s own cache')
+    model, spec, engine = _small_engine(dev, batch=2)
+    sizes = [(32, 300), (5, 61)]
+    for i, (P, L) in enumerate(sizes):
+        engine.load_slot(i, synth.condition(model, P, L, seed=70 + i, device=dev))
+    engine.wait_loads()
+    g = torch.Generator().manual_seed(12)
+    tokens = torch.randint(0, spec.num_classes + 1, tuple(engine.tokens.shape), generator=g)
+    engine.tokens.copy_(tokens.to(dev))
+    times = [0.35, 0.8]
+    got = engine.replay(times).patches.float().cpu().double()
+    torch.cuda.synchronize()
+    keys = [engine.context.k[j].cpu() for j in range(len(model.cross))]
+    values = [engine.context.vt[j].cpu().transpose(2, 3) for j in range(len(model.cross))]
+    params = {k: v.cpu() for k, v in model.state_dict().items()}
+    ref = O.step_forward(params, tokens, torch.tensor(times), engine.origin.cpu(), engine.group_origin.cpu(), keys,
+                         values, [P + L for P, L in sizes], depth=SMALL['depth'], heads=SMALL['heads'],
+                         control_heads=int(model.cross[0].heads), layer_map=model.layer_map, patch=4,
+                         y_range=model.backbone.y_range, time_dim=model.backbone.time_dim,
+                         voxel_shape=SMALL['voxel_shape'])
+    err = (got - ref).abs()
+    assert float(err.max()) <= 4e-2 * float(ref.abs().max()), (float(err.max()), float(ref.abs().max()))
+    assert float(err.mean()) <= 1e-2 * float(ref.abs().mean()), (float(err.mean()), float(ref.abs().mean()))
 
 
 def test_engine_bucket_graphs_equal_eager(dev):
