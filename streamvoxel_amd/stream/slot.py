@@ -153,14 +153,15 @@ class LowEntropyLastSlot:
         self.air_p = torch.zeros(self.shape, dtype=torch.float32, device=dev)
         self.workspace = QuotaWorkspace(1, self.shape, b, dev, fused=True)
         self._bound = False
-        self._host = torch.empty(2 * self.total + 1, dtype=torch.int64, pin_memory=True)
+        # A solid step ends on the device as `drawn` (the drawn class of every chosen voxel, -1 elsewhere), the
+        # quota flag and the sampler's error flag; one copy of each to pinned host memory, then `commit_drawn`.
+        self.sample_err = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.drawn = torch.full(self.shape, -1, dtype=torch.int16, device=dev)
+        self._host16 = torch.empty(self.total, dtype=torch.int16, pin_memory=True)
+        self._host_flags = torch.empty(2, dtype=torch.int32, pin_memory=True)
         if sampler == 'philox':
             self.seed_dev = torch.zeros(1, dtype=torch.int64, device=dev)
             self.step_dev = torch.zeros(1, dtype=torch.int64, device=dev)
-            self.sample_err = torch.zeros(1, dtype=torch.int32, device=dev)
-            self.drawn = torch.full(self.shape, -1, dtype=torch.int16, device=dev)
-            self._host16 = torch.empty(self.total, dtype=torch.int16, pin_memory=True)
-            self._host_flags = torch.empty(2, dtype=torch.int32, pin_memory=True)
 
     @property
     def idle(self):
@@ -314,50 +315,33 @@ class LowEntropyLastSlot:
             self.select(logits, tokens)
         else:
             graph.replay()
-        if self.sampler == 'philox':
-            self._host16.copy_(self.drawn.view(-1), non_blocking=True)
-            self._host_flags[:1].copy_(self.bad.int(), non_blocking=True)
-            self._host_flags[1:].copy_(self.sample_err, non_blocking=True)
-            event = torch.cuda.Event()
-            event.record()
-            return k, None, event, tokens
-        index = torch.nonzero_static(self.chosen.reshape(-1), size=k).squeeze(1)
-        if isinstance(logits, PatchLogits):
-            rows = logits.gather(index)                                     # [k, C], voxels in index order
-        else:
-            rows = logits.reshape(self.classes, -1).index_select(1, index).t().contiguous()
-        probabilities = rows.float().softmax(-1)
-        values = torch.multinomial(probabilities, 1, generator=self.generator).squeeze(-1)
-        tokens.view(-1).index_copy_(0, index, values)
-        host = self._host[:2 * k + 1]
-        host.copy_(torch.cat((index, values, self.bad.long())), non_blocking=True)
+        if self.sampler == 'multinomial':
+            # The reference's draw: one multinomial row per chosen voxel, in ascending voxel order, from the slot's
+            # generator (the order fixes the random stream); the draws go into `drawn` like the counter-based
+            # sampler's.
+            index = torch.nonzero_static(self.chosen.reshape(-1), size=k).squeeze(1)
+            if isinstance(logits, PatchLogits):
+                rows = logits.gather(index)                                 # [k, C], voxels in index order
+            else:
+                rows = logits.reshape(self.classes, -1).index_select(1, index).t().contiguous()
+            values = torch.multinomial(rows.float().softmax(-1), 1, generator=self.generator).squeeze(-1)
+            tokens.view(-1).index_copy_(0, index, values)
+            self.drawn.fill_(-1)
+            self.drawn.view(-1).index_copy_(0, index, values.to(torch.int16))
+        self._host16.copy_(self.drawn.view(-1), non_blocking=True)
+        self._host_flags[:1].copy_(self.bad.int(), non_blocking=True)
+        self._host_flags[1:].copy_(self.sample_err, non_blocking=True)
         event = torch.cuda.Event()
         event.record()
-        return k, host, event, tokens
+        return event, tokens
 
     def collect(self, staged):
-        """Wait for the step's copy and do the host bookkeeping (fast_ops.py:560-575)."""
-        k, host, event, tokens = staged
+        """Wait for the step's copy of the drawn classes and flags, then the host bookkeeping (`commit_drawn`)."""
+        event, tokens = staged
         event.synchronize()
-        if host is None:
-            # 'philox': the drawn classes of the whole window, -1 where not chosen.
-            if int(self._host_flags[1]):
-                raise RuntimeError('probability tensor contains either `inf`, `nan` or element < 0')
-            return self.commit_drawn(self._host16.numpy(), bool(self._host_flags[0]), tokens)
-        else:
-            if int(host[2 * k]):
-                raise AssertionError('low-entropy-last solid step did not meet its quota')
-            positions = host[:k].clone()
-            values_cpu = host[k:2 * k].to(torch.int16)
-        self.solid_calls += 1
-        self.actual += 1
-        self.nfe += 1
-        self.step_map.reshape(-1)[positions] = self.nfe
-        self.values.reshape(-1)[positions] = values_cpu
-        commit = dict(positions=positions.numpy().astype('int32'), values=values_cpu.numpy(), step=int(self.nfe))
-        if self.solid_calls >= len(self.quotas):
-            return self._finish(tokens), commit
-        return None, commit
+        if int(self._host_flags[1]):
+            raise RuntimeError('probability tensor contains either `inf`, `nan` or element < 0')
+        return self.commit_drawn(self._host16.numpy(), bool(self._host_flags[0]), tokens)
 
     def commit_drawn(self, drawn, bad, tokens):
         """The host bookkeeping of a solid step from the drawn classes of the window (`drawn`, numpy int16 [N], -1
