@@ -156,10 +156,7 @@ class Workload:
             self.sel.mark(self.mark_logits, LAST_EPS)
             return
         s = step - 1
-        self.sel.k.copy_(self.k_tab[s])
-        self.sel.committed.copy_(self.com_tab[s])
-        self.sel.frac.copy_(self.frac_tab[s])
-        self.sel.run(self.logits[s])
+        self.sel.run(self.logits[s], scalars=(self.k_tab[s], self.com_tab[s], self.frac_tab[s]))
         self.bad_seen |= self.sel.bad
         self.sel.tokens.masked_fill_(self.sel.chosen.view(SLOTS, VOXELS), 1)
         if s == STEPS_PER_WINDOW - 2:

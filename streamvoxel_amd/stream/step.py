@@ -184,21 +184,31 @@ class EaseSelect:
             raise ValueError(f'patch logits of {logits.shape} windows, the selection is for {self.shape}')
         return logits.rows
 
-    def run(self, logits, n=None, keep_scores=False):
+    def run(self, logits, n=None, keep_scores=False, scalars=None):
         """Entropy + selectable + block-quota select + bad flag for the first n windows (capturable). With
         keep_scores the fp32 scores are also left in `self.scores`. `logits` may be a PatchLogits (the class
-        head's output read in place)."""
+        head's output read in place). `scalars`: the windows' (k, committed, frac) as device tensors of at least
+        n entries (int64, int64, float64) to read in place of this selection's own buffers (`set_step`), e.g. a
+        row of per-step tables that a captured step reads directly."""
         n = self.batch if n is None else n
         Y, Z, X = self.shape
         lib = _lib.load()
+        k, committed, frac = self.k, self.committed, self.frac
+        if scalars is not None:
+            k, committed, frac = scalars
+            for t, dtype, name in ((k, torch.int64, 'k'), (committed, torch.int64, 'committed'),
+                                   (frac, torch.float64, 'frac')):
+                if not (torch.is_tensor(t) and t.device == self.k.device and t.dtype == dtype and t.dim() == 1
+                        and t.numel() >= n and t.is_contiguous()):
+                    raise ValueError(f'scalars: {name} must be a contiguous {dtype} device vector of at least {n}')
         if isinstance(logits, PatchLogits):
             rows = self._patch_rows(logits)
             _lib.require_gpu(rows)
             _lib.check(lib.svhip_ease_select_patches(
                 _lib.ptr(rows), _lib.dtype_code(rows.dtype), logits.classes, logits.patch, rows.stride(0),
                 rows.stride(1), _lib.ptr(self.tokens), self.classes, _lib.ptr(self.last.view(torch.uint8)), n, Y, Z,
-                X, self.block, _lib.ptr(self.k), _lib.ptr(self.pos), _lib.ptr(self.frac), _lib.ptr(self.n_total),
-                _lib.ptr(self.committed), _lib.ptr(self.chosen.view(torch.uint8)), _lib.ptr(self.bad.view(torch.uint8)),
+                X, self.block, _lib.ptr(k), _lib.ptr(self.pos), _lib.ptr(frac), _lib.ptr(self.n_total),
+                _lib.ptr(committed), _lib.ptr(self.chosen.view(torch.uint8)), _lib.ptr(self.bad.view(torch.uint8)),
                 _lib.ptr(self.scores) if keep_scores else None, _lib.ptr(self.ws.buffer), self.ws.buffer.numel(),
                 _lib.stream_of(rows)), 'svhip_ease_select_patches')
             return
@@ -206,8 +216,8 @@ class EaseSelect:
         code, C, sb, sc, sn = self._layout(logits, n, self.n)
         _lib.check(lib.svhip_ease_select(
             _lib.ptr(logits), code, C, sb, sc, sn, _lib.ptr(self.tokens), self.classes,
-            _lib.ptr(self.last.view(torch.uint8)), n, Y, Z, X, self.block, _lib.ptr(self.k), _lib.ptr(self.pos),
-            _lib.ptr(self.frac), _lib.ptr(self.n_total), _lib.ptr(self.committed),
+            _lib.ptr(self.last.view(torch.uint8)), n, Y, Z, X, self.block, _lib.ptr(k), _lib.ptr(self.pos),
+            _lib.ptr(frac), _lib.ptr(self.n_total), _lib.ptr(committed),
             _lib.ptr(self.chosen.view(torch.uint8)), _lib.ptr(self.bad.view(torch.uint8)),
             _lib.ptr(self.scores) if keep_scores else None,
             _lib.ptr(self.ws.buffer), self.ws.buffer.numel(), _lib.stream_of(logits)), 'svhip_ease_select')

@@ -132,11 +132,14 @@ def test_twelve_layer_context_graph_replays(dev):
         sel.bind_window(b, torch.randperm(N // 64, generator=torch.Generator().manual_seed(b)))
         sel.set_step(b, 1000 + b, 0, (1000 + b) / N)
     logits = torch.empty(B * N, CLASSES, device=dev)
+    # the captured step reads the step's scalars from table rows in place (scalars=), the eager one from the
+    # selection's own buffers: the same values, so the same bits
+    tables = (sel.k.clone(), sel.committed.clone(), sel.frac.clone())
 
-    def step():
+    def step(scalars=None):
         for layer in range(layers):
             ctx.attend(layer, qbuf[layer].transpose(1, 2), out=obuf[layer].transpose(1, 2))
-        sel.run(logits)
+        sel.run(logits, scalars=scalars)
 
     def fill(seed):
         gg = torch.Generator(device=dev).manual_seed(seed)
@@ -148,11 +151,11 @@ def test_twelve_layer_context_graph_replays(dev):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        step()
+        step(tables)
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        step()
+        step(tables)
     for replay in range(3):
         fill(100 + replay)
         graph.replay()
@@ -165,6 +168,10 @@ def test_twelve_layer_context_graph_replays(dev):
             assert torch.equal(got_o[layer], obuf[layer]), (replay, layer)
         assert torch.equal(got_c, sel.chosen), replay
         assert not bool(sel.bad.any())
+    with pytest.raises(ValueError, match='frac'):
+        sel.run(logits, scalars=(tables[0], tables[1], tables[2].float()))
+    with pytest.raises(ValueError, match='k must'):
+        sel.run(logits, scalars=(tables[0][:B - 1], tables[1], tables[2]))
     # Spot check of the last replay against float64: two windows, two heads, every 16th query, layers 0 and 11.
     for layer in (0, layers - 1):
         for b in (0, 5):
