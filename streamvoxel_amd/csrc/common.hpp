@@ -98,12 +98,19 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // The same over groups of LPV (8 or 16) lanes: quad xor 1, quad xor 2, half-row mirror (8 lanes), row mirror (16).
+// A max step moves the neighbour with bound control (every lane of these patterns reads a lane of its own row, so
+// no old value is needed and none is materialised).
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_step(float v) {
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true)));
+}
+
 template <int LPV>
 __device__ __forceinline__ float group_max(float v) {
-  v = fmaxf(v, dpp_f<0xB1>(v));
-  v = fmaxf(v, dpp_f<0x4E>(v));
-  v = fmaxf(v, dpp_f<0x141>(v));
-  if constexpr (LPV == 16) v = fmaxf(v, dpp_f<0x140>(v));
+  v = dpp_max_step<0xB1>(v);
+  v = dpp_max_step<0x4E>(v);
+  v = dpp_max_step<0x141>(v);
+  if constexpr (LPV == 16) v = dpp_max_step<0x140>(v);
   return v;
 }
 

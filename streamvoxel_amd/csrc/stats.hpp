@@ -180,9 +180,9 @@ __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_
   int64_t b = voxel / n;
   int64_t i = voxel - b * n;
   const int64_t sdiv = stride / n, smod = stride - sdiv * n;
-  for (; voxel < total; voxel += stride) {
-    const auto pre = out.prefetch(voxel);
-    const T* row = x + b * sb + rows(i) * sn;
+  // One voxel's row: load, the canonical arithmetic, the output.
+  auto one = [&](int64_t vox, const T* row) __attribute__((always_inline)) {
+    const auto pre = out.prefetch(vox);
     uint4 raw[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
@@ -214,12 +214,24 @@ __device__ __forceinline__ void voxel_major_pass(const T* __restrict__ x, int64_
     }
     s = group_sum<LPV>(s);
     w = group_sum<LPV>(w);
-    if (g == 0) out.store(voxel, finish_stat<MODE>(s, w, max_p<MODE>(m, mL)), pre);
-    i += smod;
-    b += sdiv;
-    if (i >= n) {
-      i -= n;
-      ++b;
+    if (g == 0) out.store(vox, finish_stat<MODE>(s, w, max_p<MODE>(m, mL)), pre);
+  };
+  // Element offsets of the lane's window and of its voxel's row in it. A stride of whole windows (smod == 0, e.g.
+  // 24 workgroups a CU over 65536-voxel windows) leaves a lane's voxel index, so its row offset, unchanged: the
+  // (uniform) branch that steps them is then skipped and an iteration only steps the window offset.
+  int64_t boff = b * sb;
+  const int64_t bstep = sdiv * sb;
+  int64_t roff = rows(i) * sn;
+  for (; voxel < total; voxel += stride) {
+    one(voxel, x + boff + roff);
+    boff += bstep;
+    if (smod != 0) {
+      i += smod;
+      if (i >= n) {
+        i -= n;
+        boff += sb;
+      }
+      roff = rows(i) * sn;
     }
   }
 }
@@ -450,8 +462,9 @@ __host__ inline StatsPlan plan_stats(const T* x, int64_t batch, int64_t C, int64
   if (canon && sc == 1 && aligned_base && ((sn * bytes) % 16) == 0 && ((sb * bytes) % 16) == 0) {
     // Short rows run faster from a grid of 24 workgroups per CU that loops over the voxels (304 bf16 classes in
     // patch order, per 8-window selection: 74.5 us at 8 per CU, 69.5 at 16, 68.0 at 24, 71 with one pass of
-    // workgroups over all voxels); long rows from one pass of workgroups (256 fp32 classes: 100 us, 113 us with a
-    // capped grid).
+    // workgroups over all voxels; with the loop that keeps a whole-window stride's row offset, 8, 16 and 32 per CU
+    // measured 1-5 % slower than 24); long rows from one pass of workgroups (256 fp32 classes: 100 us, 113 us with
+    // a capped grid).
     const int64_t grid = rp.lpv == 8 ? std::min<int64_t>(stats_grid(batch * n * rp.lpv), kShortRowWorkgroups)
                                      : stats_grid(batch * n * rp.lpv);
     return StatsPlan{kVoxelMajor, rp.nv, rp.lpv, grid, 0};
