@@ -20,6 +20,8 @@ The device work of a window:
 """
 from __future__ import annotations
 
+from collections.abc import Mapping
+
 import numpy as np
 import torch
 
@@ -135,8 +137,9 @@ class LowEntropyLastSlot:
         self.quotas = None
         self.solid_calls = self.actual = self.nfe = self.last_count = 0
         self.order = self.generator = None
-        self.step_map = torch.zeros(self.shape, dtype=torch.int16)
-        self.values = torch.full(self.shape, -1, dtype=torch.int16)
+        self._step_map = torch.zeros(self.shape, dtype=torch.int16)
+        self._values = torch.full(self.shape, -1, dtype=torch.int16)
+        self._pending = None
         blocks = self.total // b ** 3
         dev = self.device
         # Static buffers at fixed addresses, so a captured `select` stays valid across windows.
@@ -167,6 +170,23 @@ class LowEntropyLastSlot:
     def idle(self):
         return self.phase == 'idle'
 
+    @property
+    def step_map(self):
+        """[Y,Z,X] int16 host map: the forward that committed each voxel (0 where none yet)."""
+        self._settle()
+        return self._step_map
+
+    @property
+    def values(self):
+        """[Y,Z,X] int16 host map: each committed voxel's class (-1 where none yet)."""
+        self._settle()
+        return self._values
+
+    def _settle(self):
+        """Run the host work of this slot's deferred commit, if one is waiting."""
+        if self._pending is not None:
+            self._pending.materialize()
+
     def arm(self, seed, cap, target):
         """stream/slot.py:86-103."""
         self.phase = 'marking'
@@ -183,8 +203,9 @@ class LowEntropyLastSlot:
         if self.sampler == 'philox':
             self.seed_dev.fill_(self.seed)
             self.sample_err.zero_()
-        self.step_map = torch.zeros(self.shape, dtype=torch.int16)
-        self.values = torch.full(self.shape, -1, dtype=torch.int16)
+        self._settle()
+        self._step_map = torch.zeros(self.shape, dtype=torch.int16)
+        self._values = torch.full(self.shape, -1, dtype=torch.int16)
         self._bound = False
 
     def drop(self):
@@ -343,25 +364,27 @@ class LowEntropyLastSlot:
             raise RuntimeError('probability tensor contains either `inf`, `nan` or element < 0')
         return self.commit_drawn(self._host16.numpy(), bool(self._host_flags[0]), tokens)
 
-    def commit_drawn(self, drawn, bad, tokens):
+    def commit_drawn(self, drawn, bad, tokens, defer=False):
         """The host bookkeeping of a solid step from the drawn classes of the window (`drawn`, numpy int16 [N], -1
         where not chosen) and its quota flag: the commit's positions in ascending flat order and their values, the
-        step and value maps, and the finish record after the last solid step (fast_ops.py:560-575)."""
+        step and value maps, and the finish record after the last solid step (fast_ops.py:560-575).
+        The step counters advance at once. With `defer` (and unless the step ends the window) the rest, a pass over
+        the window's N drawn classes, waits in a `DeferredCommit` until it is read or `_settle` runs it; `drawn` must
+        then stay unchanged until that happens."""
         if bad:
             raise AssertionError('low-entropy-last solid step did not meet its quota')
+        self._settle()
         k = self.quotas[self.solid_calls]
-        positions = np.flatnonzero(drawn >= 0)
-        if len(positions) != k:
-            raise AssertionError(f'{len(positions)} voxels drawn for a quota of {k}')
-        values = drawn[positions]
         self.solid_calls += 1
         self.actual += 1
         self.nfe += 1
-        self.step_map.numpy().reshape(-1)[positions] = self.nfe
-        self.values.numpy().reshape(-1)[positions] = values
-        commit = dict(positions=positions.astype('int32'), values=values.copy(), step=int(self.nfe))
+        commit = DeferredCommit(self, drawn, k, self.nfe)
         if self.solid_calls >= len(self.quotas):
+            commit = commit.materialize()
             return self._finish(tokens), commit
+        if not defer:
+            return None, commit.materialize()
+        self._pending = commit
         return None, commit
 
     def adopt(self, batch, index):
@@ -395,13 +418,14 @@ class LowEntropyLastSlot:
 
     def _finish(self, tokens):
         """stream/slot.py:166-176: the deferred voxels become `air_token`; the window record."""
+        self._settle()
         tokens[self.last] = self.air_token
         last_cpu = self.last.cpu()
-        self.step_map[last_cpu] = self.nfe
-        self.values[last_cpu] = self.air_token
+        self._step_map[last_cpu] = self.nfe
+        self._values[last_cpu] = self.air_token
         record = dict(target=self.target, seed=self.seed, cap=self.cap, nfe=int(self.nfe), actual=int(self.actual),
                       last_count=int(self.last_count), last_frac=float(self.last_count) / self.total,
-                      step_map=self.step_map.clone(), values=self.values.clone())
+                      step_map=self._step_map.clone(), values=self._values.clone())
         self.phase = 'idle'
         self.target = None
         return record
@@ -409,6 +433,50 @@ class LowEntropyLastSlot:
 
 # The solid steps above already run the fast (staged, capturable) path; the reference's name for that class.
 FastLowEntropyLastSlot = LowEntropyLastSlot
+
+
+class DeferredCommit(Mapping):
+    """A solid step's commit record ({positions, values, step}, as `commit_drawn` returns it) whose host work runs
+    on first read or when its slot settles: the positions of the drawn voxels in ascending flat order (a pass over
+    the window's drawn classes), their values, and their entries in the slot's step and value maps. The batched
+    `consume_batch` hands these out and settles them at its next call, before it overwrites the drawn classes, so
+    in a worker loop that launches the next forward first that work runs while the GPU computes."""
+
+    __slots__ = ('_slot', '_drawn', '_k', '_step', '_maps', '_data')
+
+    def __init__(self, slot, drawn, k, step):
+        self._slot, self._drawn, self._k, self._step = slot, drawn, int(k), int(step)
+        self._maps = (slot._step_map, slot._values)   # this window's maps (a re-arm replaces the slot's)
+        self._data = None
+
+    def materialize(self):
+        """The commit as a plain dict (computed once)."""
+        if self._data is None:
+            drawn = self._drawn
+            positions = np.flatnonzero(drawn >= 0)
+            if len(positions) != self._k:
+                raise AssertionError(f'{len(positions)} voxels drawn for a quota of {self._k}')
+            values = drawn[positions]
+            step_map, vals = self._maps
+            step_map.numpy().reshape(-1)[positions] = self._step
+            vals.numpy().reshape(-1)[positions] = values
+            self._data = dict(positions=positions.astype('int32'), values=values.copy(), step=self._step)
+            self._drawn = None
+            if self._slot._pending is self:
+                self._slot._pending = None
+        return self._data
+
+    def __getitem__(self, key):
+        return self.materialize()[key]
+
+    def __iter__(self):
+        return iter(self.materialize())
+
+    def __len__(self):
+        return len(self.materialize())
+
+    def __repr__(self):
+        return f'DeferredCommit({self.materialize()!r})'
 
 
 class _NothingSelected:
@@ -458,6 +526,7 @@ class PhiloxBatch:
         self.host_drawn = torch.empty((batch, s0.total), dtype=torch.int16, pin_memory=True)
         self.host_bad = torch.empty(batch, dtype=torch.uint8, pin_memory=True)
         self.host_err = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        self.pending = []       # DeferredCommits over rows of host_drawn, settled before the next copy into it
         for i, slot in enumerate(slots[:batch]):
             slot.adopt(self, i)
 
@@ -531,6 +600,8 @@ def consume_batch(slots, logits, tokens, count, graphs=None):
     bucket = graphs.lookup(logits) if graphs is not None else None
     if bucket is not None and graphs.batch is not None and bucket in graphs.graphs:
         return _consume_batched(graphs, slots, logits, tokens, count, bucket)
+    for slot in slots:
+        slot._settle()
     active = [(i, slots[i]) for i in range(count) if not slots[i].idle]
     queued = [(i, slot) for i, slot in active if slot.stageable()]
     handles = {}
@@ -545,8 +616,14 @@ def consume_batch(slots, logits, tokens, count, graphs=None):
 def _consume_batched(graphs, slots, logits, tokens, count, bucket):
     """consume_batch over a PhiloxBatch: one host-to-device copy of every window's step scalars, one graph replay
     that selects and samples the bucket's windows, one device-to-host copy of their drawn classes and flags, and the
-    host bookkeeping per slot from the copied rows (marking and finishing forwards still go through `consume`)."""
+    host bookkeeping per slot from the copied rows (marking and finishing forwards still go through `consume`).
+    The commits of steps that do not end their window are `DeferredCommit`s over the copied rows: the previous
+    call's are settled first thing here (before this call's copy overwrites those rows), which in a loop that
+    launches the next forward before calling this runs them while that forward is on the GPU."""
     batch = graphs.batch
+    for commit in batch.pending:
+        commit.materialize()
+    batch.pending.clear()
     active = [(i, slots[i]) for i in range(count) if not slots[i].idle]
     queued = [(i, slot) for i, slot in active if slot.stageable()]
     B = batch.batch
@@ -571,5 +648,7 @@ def _consume_batched(graphs, slots, logits, tokens, count, bucket):
     drawn = batch.host_drawn.numpy()
     bad = batch.host_bad.numpy()
     for i, slot in queued:
-        results[i] = slot.commit_drawn(drawn[i], bool(bad[i]), tokens[i])
+        results[i] = slot.commit_drawn(drawn[i], bool(bad[i]), tokens[i], defer=True)
+        if isinstance(results[i][1], DeferredCommit):
+            batch.pending.append(results[i][1])
     return {i: results[i] for i in sorted(results)}

@@ -102,3 +102,38 @@ def test_default_encoder_is_the_reference_packages_encode_item(monkeypatch):
     assert default_encoder(object(), spec, 'cuda:0') is None          # not a reference model
     monkeypatch.setitem(sys.modules, 'streamvoxel.stream.engine', None)  # the package is not importable
     assert default_encoder(model, spec, 'cuda:0') is None
+
+
+def test_deferred_commit_runs_its_host_work_once_on_first_read():
+    """A batched solid step's commit: nothing is written to the slot's maps until it is read or settled; then the
+    positions are the drawn voxels in ascending flat order, the values their classes, the maps updated at those
+    voxels only, and the slot's pending reference cleared. A drawn count that misses the quota raises then."""
+    import types
+
+    import numpy as np
+
+    from streamvoxel_amd.stream.slot import DeferredCommit
+    shape = (2, 4, 4)
+    slot = types.SimpleNamespace(_step_map=torch.zeros(shape, dtype=torch.int16),
+                                 _values=torch.full(shape, -1, dtype=torch.int16), _pending=None)
+    drawn = np.full(32, -1, np.int16)
+    drawn[[3, 7, 8, 30]] = [5, 0, 17, 2]
+    commit = DeferredCommit(slot, drawn, 4, 6)
+    slot._pending = commit
+    assert int((slot._step_map != 0).sum()) == 0 and int((slot._values != -1).sum()) == 0
+    assert commit['step'] == 6
+    assert slot._pending is None
+    assert np.array_equal(commit['positions'], [3, 7, 8, 30]) and commit['positions'].dtype == np.int32
+    assert np.array_equal(commit['values'], [5, 0, 17, 2])
+    copied = dict(commit, target=(1, 0))                   # the reference worker's progressive record
+    assert sorted(copied) == ['positions', 'step', 'target', 'values']
+    assert copied['positions'] is commit['positions'] and copied['values'] is commit['values']
+    assert sorted(commit) == ['positions', 'step', 'values'] and len(commit) == 3
+    assert np.array_equal(np.flatnonzero(slot._step_map.numpy().reshape(-1)), [3, 7, 8, 30])
+    assert set(slot._step_map.numpy().reshape(-1)[[3, 7, 8, 30]]) == {6}
+    assert np.array_equal(slot._values.numpy().reshape(-1)[[3, 7, 8, 30]], [5, 0, 17, 2])
+    drawn[0] = 1                                            # the row is no longer read once materialised
+    assert np.array_equal(commit['positions'], [3, 7, 8, 30])
+    short = DeferredCommit(slot, np.full(32, -1, np.int16), 2, 7)
+    with pytest.raises(AssertionError, match='0 voxels drawn for a quota of 2'):
+        short.materialize()
