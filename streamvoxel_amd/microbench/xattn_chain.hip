@@ -14,6 +14,10 @@
 //   64 queries a wave    the last form with two query tiles a wave: every LDS operand read feeds two products
 //   priority 1 / 2       the staged form with the wave's issue priority raised (s_setprio 1) while it issues its
 //                        score products (1), or its score and second products (2), and lowered for its softmax
+//   two halves at once   the staged form with a block's two halves in one stretch of code: half 1's score product
+//                        issued before half 0's softmax, half 0's row sum and second product before half 1's
+//                        softmax (the compiler's order), so a wave's own products run beside its own softmax;
+//                        "+ rare rescales" adds the two row-sum checks as branches that rescale O (never taken)
 //
 // Build: python -m streamvoxel_amd.build --microbench   Run: streamvoxel_amd/microbench/xattn_chain
 #include <hip/hip_runtime.h>
@@ -189,18 +193,121 @@ __global__ __launch_bounds__(256, WAVES) void half_kernel(float* out, const floa
 
 constexpr int kUnits = 96, kUnitBlocks = 128;  // 2 MB of blocks a unit, 192 MB in all
 
+// Both halves of a block in one stretch (see the top). RESCALE: the row-sum checks as branches that rescale O.
+template <int WAVES, bool RESCALE>
+__global__ __launch_bounds__(256, WAVES) void block_kernel(float* out, const float* in, const uint16_t* kv,
+                                                           int ublocks, int iters) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[2][kTileElems];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int i = tid; i < 2 * kTileElems; i += 256) tile[i / kTileElems][i % kTileElems] = 0x3c00 + (i & 255);
+  __syncthreads();
+  bf16x8_t q[4], ones;
+  for (int k = 0; k < 4; ++k) {
+    for (int i = 0; i < 8; ++i) q[k][i] = (__bf16)(in[8 + i] - 0.01f * k);
+  }
+  for (int i = 0; i < 8; ++i) ones[i] = (__bf16)((tid & 31) == 0 ? 1.f : 0.f);
+  const float sl2 = in[24] * 1e-3f, nm = -in[25];
+  f32x16_t o[2];
+  o[0] = o[1] = f32x16_t{0};
+  float l = 0.f;
+  const int unit = (blockIdx.x % 8) * (gridDim.x / 64) + (blockIdx.x / 8) / 8;
+  const uint32_t ubytes = static_cast<uint32_t>(ublocks) * 16384u;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(kv) + static_cast<size_t>(unit) * (ubytes / 2), 0, static_cast<int>(ubytes), 0x00020000);
+  auto stage = [&](int blk, int buf) __attribute__((always_inline)) {
+    const uint32_t soff = static_cast<uint32_t>(blk % ublocks) * 16384u;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int j = w + 4 * t;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)(&tile[buf][512 * j]), 16,
+                                               static_cast<uint32_t>(1024 * j + 16 * lane), soff, 0, 0);
+    }
+  };
+  stage(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int blk = 0; blk < iters / 2; ++blk) {
+    const int buf = blk & 1;
+    stage(blk + 1, buf ^ 1);
+    const char* tp = reinterpret_cast<const char*>(tile[buf]);
+    auto score = [&](int t) __attribute__((always_inline)) {
+      bf16x8_t a[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a[k] = *reinterpret_cast<const bf16x8_t*>(tp + ((lane * 16 + k * 1024 + t * 4096) & 8191));
+      f32x16_t x = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], q[0], f32x16_t{0}, 0, 0, 0);
+#pragma unroll
+      for (int k = 1; k < 4; ++k) x = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[k], q[k], x, 0, 0, 0);
+      return x;
+    };
+    auto row_sum = [&](const bf16x8_t (&pb)[2]) __attribute__((always_inline)) {
+      f32x4_t h = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[0], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      h = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[1], h, 0, 0, 0);
+      return h[0];
+    };
+    auto second = [&](int t, const bf16x8_t (&pb)[2]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const char* vp = tp + 8192;
+        const bf16x8_t v0 = *reinterpret_cast<const bf16x8_t*>(vp + ((lane * 16 + (2 * ks) * 1024 + t * 4096) & 8191));
+        const bf16x8_t v1 = *reinterpret_cast<const bf16x8_t*>(vp + ((lane * 16 + (2 * ks + 1) * 1024 + t * 4096) & 8191));
+        o[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v0, pb[ks], o[0], 0, 0, 0);
+        o[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v1, pb[ks], o[1], 0, 0, 0);
+      }
+    };
+    const f32x16_t s0 = score(0);
+    const f32x16_t s1 = score(1);
+    bf16x8_t pb0[2], pb1[2];
+    softmax(s0, sl2, nm, pb0);
+    const float h0 = row_sum(pb0);
+    __builtin_amdgcn_sched_barrier(0);
+    second(0, pb0);
+    softmax(s1, sl2, nm, pb1);
+    const float h1 = row_sum(pb1);
+    if (RESCALE && __builtin_amdgcn_ballot_w64(!(h0 <= 1e30f)) != 0ull) {
+      o[0] *= 0.5f;
+      o[1] *= 0.5f;
+      l *= 0.5f;
+    }
+    l += h0;
+    if (RESCALE && __builtin_amdgcn_ballot_w64(!(h1 <= 1e30f)) != 0ull) {
+      o[0] *= 0.25f;
+      o[1] *= 0.25f;
+      l *= 0.25f;
+    }
+    second(1, pb1);
+    l += h1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+  float r = l;
+  for (int i = 0; i < 16; ++i) r += o[0][i] + o[1][i];
+  out[blockIdx.x * blockDim.x + tid] = r;
+}
+
+// FORM kBlockPair: block_kernel (PRIO then means RESCALE).
+constexpr int kBlockPair = 100;
+
+template <int FORM, int WAVES, int QT, int PRIO>
+void launch(int grid, float* out, const float* in, const uint16_t* kv, int iters) {
+  if constexpr (FORM == kBlockPair) {
+    block_kernel<WAVES, PRIO != 0><<<grid, 256>>>(out, in, kv, kUnitBlocks, iters);
+  } else {
+    half_kernel<FORM, WAVES, QT, PRIO><<<grid, 256>>>(out, in, kv, kUnitBlocks, iters);
+  }
+}
+
 template <int FORM, int WAVES, int QT = 1, int PRIO = 0>
 double run(const char* name, float* out, const float* in, const uint16_t* kv, int iters, double ref_ns) {
   const int grid = 256 * WAVES;  // WAVES workgroups of 4 waves per CU: WAVES waves on every SIMD
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
-  half_kernel<FORM, WAVES, QT, PRIO><<<grid, 256>>>(out, in, kv, kUnitBlocks, iters);
+  launch<FORM, WAVES, QT, PRIO>(grid, out, in, kv, iters);
   CHECK(hipGetLastError());
   CHECK(hipDeviceSynchronize());
   const int reps = 5;
   CHECK(hipEventRecord(e0));
-  for (int r = 0; r < reps; ++r) half_kernel<FORM, WAVES, QT, PRIO><<<grid, 256>>>(out, in, kv, kUnitBlocks, iters);
+  for (int r = 0; r < reps; ++r) launch<FORM, WAVES, QT, PRIO>(grid, out, in, kv, iters);
   CHECK(hipEventRecord(e1));
   CHECK(hipEventSynchronize(e1));
   float ms;
@@ -243,6 +350,11 @@ int main() {
   run<kStaged, 3, 1, 1>("+ staging, priority 1", out, in, kv, iters, p3);
   run<kStaged, 3, 1, 2>("+ staging, priority 2", out, in, kv, iters, p3);
   run<kStaged, 2, 1, 2>("+ staging, priority 2", out, in, kv, iters, p3);
+  run<kStaged, 3>("+ staging", out, in, kv, iters, p3);
+  run<kBlockPair, 3>("two halves at once", out, in, kv, iters, p3);
+  run<kBlockPair, 3, 1, 1>("+ rare rescales", out, in, kv, iters, p3);
+  run<kBlockPair, 2>("two halves at once", out, in, kv, iters, p3);
+  run<kBlockPair, 1>("two halves at once", out, in, kv, iters, p3);
   CHECK(hipFree(kv));
   CHECK(hipFree(out));
   CHECK(hipFree(in));
