@@ -54,8 +54,8 @@ def parse():
     p.add_argument('--forward-only', action='store_true',
                    help='time only the whole-step forward (shipped shape) and print its line')
     p.add_argument('--no-c5', action='store_true', help='skip the 64-slot e4m3 stress component')
-    p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'select', 'select_planes', 'select_c304', 'c5_xattn',
-                                        'c5'],
+    p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'xattn_layouts', 'select', 'select_planes',
+                                        'select_c304', 'c5_xattn', 'c5'],
                    help='build only that kernel\'s inputs (the step\'s layer-0 attention or its first solid '
                         'selection), time 20 back-to-back launches and print one line: the run to profile')
     return p.parse_args()
@@ -519,6 +519,50 @@ def shipped_select(dev, quotas, reps):
     return t, SLOTS * VOXELS * (classes * 2 + 8 + 1 + 1)
 
 
+def xattn_layouts(dev, seed):
+    """The step's attention layer (8 windows, 12 x 64 heads, 1024 queries, the step's key lengths, bf16) over the
+    K/V layouts a caller may pass: padded V^T (the cached-context layout), padded and packed (cu_seqlens) row-major
+    V, packed V^T, and a prefix key mask over either padded V. Microseconds per launch (20 launches a graph) and
+    whether each layout gives the bits of the padded V^T one."""
+    import torch
+    from streamvoxel_amd import synth
+    from streamvoxel_amd.stream.attention import attention
+    g = torch.Generator(device=dev).manual_seed(seed)
+    lengths = synth.kv_lengths(SLOTS, seed)
+    kcap = max(lengths) + (-max(lengths)) % 64
+    k = (torch.randn(SLOTS, HEADS, kcap, HEAD_DIM, device=dev, generator=g) / 8).bfloat16()
+    v = (torch.randn(SLOTS, HEADS, kcap, HEAD_DIM, device=dev, generator=g) / 8).bfloat16()
+    q = torch.randn(SLOTS, HEADS, QUERIES, HEAD_DIM, device=dev, generator=g).bfloat16()
+    vt = v.transpose(2, 3).contiguous()                                          # [B, H, D, Kcap]
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    cu = torch.zeros(SLOTS + 1, dtype=torch.int32)
+    cu[1:] = torch.tensor(lengths).cumsum(0)
+    cu = cu.to(dev)
+    kp = torch.cat([k[b, :, :L] for b, L in enumerate(lengths)], 1).contiguous()  # [H, sum L, D]
+    vp = torch.cat([v[b, :, :L] for b, L in enumerate(lengths)], 1).contiguous()
+    vtp = torch.cat([vt[b, :, :, :L] for b, L in enumerate(lengths)], 2).contiguous()  # [H, D, sum L]
+    prefix = torch.arange(kcap, device=dev)[None] < lt[:, None]
+    out = torch.empty_like(q)
+    forms = {
+        'padded_vt': lambda: attention(q, k, vt.transpose(2, 3), lengths=lt, out=out),
+        'padded_v_rows': lambda: attention(q, k, v, lengths=lt, out=out),
+        'packed_v_rows': lambda: attention(q, kp, vp, cu_seqlens=cu, out=out),
+        'packed_vt': lambda: attention(q, kp, vtp.transpose(1, 2), cu_seqlens=cu, out=out),
+        'key_mask_v_rows': lambda: attention(q, k, v, key_mask=prefix, out=out),
+        'key_mask_vt': lambda: attention(q, k, vt.transpose(2, 3), key_mask=prefix, out=out),
+    }
+    flops = 4 * HEADS * HEAD_DIM * QUERIES * sum(lengths)
+    res, first = {}, None
+    for name, fn in forms.items():
+        t = time_graph(fn, 20)
+        fn()
+        torch.cuda.synchronize()
+        if first is None:
+            first = out.clone()
+        res[name] = dict(us_per_launch=t * 1e6, TFLOPs=flops / t / 1e12, same_bits=bool(torch.equal(out, first)))
+    return dict(kernel='xattn_layouts', kv_lengths=lengths, flops_per_launch=flops, layouts=res)
+
+
 def kernel_only(dev, args):
     """One kernel of the step alone, on the step's own inputs: the cross-attention layer (8 windows, 12 x 64 heads,
     1024 queries, the step's key lengths; bf16 or e4m3 cache) or the first solid selection (8 windows, fp32 logits
@@ -530,6 +574,8 @@ def kernel_only(dev, args):
     from streamvoxel_amd.stream.step import CachedContext, EaseSelect
     if args.kernel == 'c5':
         return dict(kernel='c5', **c5_component(dev, args.seed))
+    if args.kernel == 'xattn_layouts':
+        return xattn_layouts(dev, args.seed)
     if args.kernel == 'c5_xattn':            # the 64-slot e4m3 layer alone (for the profilers)
         ctx, q, lengths = c5_context(dev, args.seed, 'fp8')
         o = torch.empty_like(q)

@@ -45,12 +45,15 @@
 //
 // Staging. An LDS tile holds 64 rows of 128 bytes, the eight 16-byte chunks of row r XOR-swizzled by (r / 2) % 8
 // so that the 16-byte operand reads are bank-conflict-free; a K row is one key's head_dim, a V^T row one
-// head_dim element's 64 keys. bf16 K and V^T of the padded [B,H,Kcap,*] layout with 16-byte aligned rows take
-// buffer_load_dwordx4 ... lds, which moves a full block straight into LDS without registers, addressed by a
-// per-lane offset fixed for the window plus a scalar block offset. Every other form goes through registers,
-// prefetched one block ahead in its storage format and converted when it is written to LDS: OCP e4m3fn K/V
-// converted exactly to bf16 (v_cvt_scalef32_pk_bf16_fp8 with scale 1; the fp8 scales are folded into the softmax
-// scale (k_scale) and the output (v_scale)), row-major V transposed on the way, the packed cu_seqlens layout.
+// head_dim element's 64 keys. Row-major V with a bf16 second product stays one key a row (in K's tile layout,
+// swizzled by swzv) and the second product reads its V^T operand with ds_read_b64_tr_b16, the LDS transpose load
+// of gfx950, so V rows are stored as they come. bf16 K and V with 16-byte aligned rows (V^T of the padded
+// [B,H,Kcap,*] layout, V rows of the padded or the packed layout) take buffer_load_dwordx4 ... lds, which moves a
+// full block straight into LDS without registers, addressed by a per-lane offset fixed for the window plus a
+// scalar block offset. Every other form goes through registers, prefetched one block ahead in its storage format
+// and converted when it is written to LDS: OCP e4m3fn K/V converted exactly to bf16 (v_cvt_scalef32_pk_bf16_fp8
+// with scale 1; the fp8 scales are folded into the softmax scale (k_scale) and the output (v_scale)), V^T of the
+// packed cu_seqlens layout, key masks.
 // The last, partial block of a window is peeled out of the loop and staged through registers (its loads issued
 // before the last full block is computed), keys >= L as zeros.
 //
@@ -61,7 +64,8 @@
 //
 // Head widths: DT = 2, 3 or 4 output tiles of 32 head_dim elements (head_dim <= 64, 96, 128). A K block is DT / 2
 // rounded up 64 x 64 sub-tiles (head_dim 0..63 and 64..127 of every key, same layout and swizzle), V^T one tile of
-// 32 DT rows; the score product takes up to 2 DT k-steps, the second product DT accumulators. DT = 2 is the
+// 32 DT rows (V rows: K's sub-tiles); the score product takes up to 2 DT k-steps, the second product DT
+// accumulators. DT = 2 is the
 // 384-wide (8 x 48) and the 64-wide heads, DT = 3 the 768-wide model's 8 x 96.
 #include <type_traits>
 
@@ -217,6 +221,13 @@ __device__ __forceinline__ int pv8_row(int key) {
 // XOR-swizzled by (r / 4) % 4, so that 16 consecutive rows read at one logical chunk hit 16 distinct bank groups.
 constexpr int kRow8 = 64;
 __device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 2) & 3); }
+
+// Row-major V with a bf16 second product (VROWS): V stays one key a row in LDS, in K's tile layout (64 keys x 64
+// head_dim elements a sub-tile, keys in natural order), and the second product reads its V^T operand transposed
+// (ds_read_b64_tr_b16). The eight 16-byte chunks of row r are XOR-swizzled by 4 ((r / 2) % 2): the 32 lanes a
+// transposed read serves per cycle touch rows r0 .. r0 + 3 (r0 a multiple of 4), 64 contiguous bytes each, and the
+// swizzle puts rows r0 and r0 + 2 (which share banks, as do r0 + 1 and r0 + 3) on different 64-byte halves.
+__device__ __forceinline__ int swzv(int r, int c) { return c ^ (((r >> 1) & 1) << 2); }
 
 // 8 OCP e4m3fn bytes (two dwords) -> 8 bf16 packed in a uint4 (exact: every e4m3 value is a bf16 value).
 __device__ __forceinline__ uint4 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
@@ -382,9 +393,10 @@ __device__ __forceinline__ void stage_load(Stage<FP8, VT, DT>& st, const XattnPa
   }
 }
 
-// Registers -> LDS (K rows under sigma in their sub-tile; V as V^T [d][key]; both swizzled), with zeros past
-// head_dim and, with ONES, the ones row D. PV8: K rows under pv8_row, V^T kept in e4m3 in its own tile (keys in
-// natural order).
+// Registers -> LDS (K rows under sigma in their sub-tile; V^T [d][key] from V^T, row-major V kept as rows in K's
+// layout; all swizzled), with zeros past head_dim and, with ONES, the ones row D of V^T (for V rows: the ones
+// column D). PV8: K rows under pv8_row, V^T kept in e4m3 in its own tile (keys in natural order), transposed from
+// row-major V byte by byte.
 template <bool FP8, bool VT, int DT, bool ONES, bool PV8 = false, bool VREG = true>
 __device__ __forceinline__ void stage_store(const Stage<FP8, VT, DT>& st, uint16_t* sK, uint16_t* sV, int dchunks,
                                             int D) {
@@ -413,15 +425,8 @@ __device__ __forceinline__ void stage_store(const Stage<FP8, VT, DT>& st, uint16
           }
         }
       } else {
-        const uint4 vb = to_bf16x8<FP8>(vv);
-        const uint32_t w[4] = {vb.x, vb.y, vb.z, vb.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int d = kSub * (r >> 1) + dc * 8 + e;
-          if (d < 32 * DT) {
-            sV[d * kRow + swz(d, key >> 3) * 8 + (key & 7)] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
-          }
-        }
+        // V rows kept as rows (VROWS): key c / 8, head_dim chunk 8 (r / 2) + dc, swizzled by swzv.
+        *reinterpret_cast<uint4*>(sV + (r >> 1) * kKTile + key * kRow + swzv(key, dc) * 8) = to_bf16x8<FP8>(vv);
       }
     }
   }
@@ -507,7 +512,7 @@ __device__ __forceinline__ DirectLanes<DT> direct_lanes(const XattnParams& p, co
 
 // FULL_D: head_dim = 32 DT, every lane of V^T and of K sub-tile 0 loads (no exec masking); sub-tile 1 at DT = 3
 // still masks head_dim 96..127. w: the wave index (uniform).
-template <int DT, bool FULL_D>
+template <int DT, bool FULL_D, bool VT_TOO = true>
 __device__ __forceinline__ void stage_direct(const DirectLanes<DT>& dl, uint32_t k_soff, uint32_t v_soff, int w,
                                              uint16_t* sK, uint16_t* sV) {
 #pragma unroll
@@ -521,11 +526,56 @@ __device__ __forceinline__ void stage_direct(const DirectLanes<DT>& dl, uint32_t
       }
     }
   }
+  if constexpr (VT_TOO) {
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
+    for (int t = 0; t < DT; ++t) {
+      const int j = w + 4 * t;
+      if (FULL_D || dl.v_ok[t]) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(dl.v_rsrc, (lds_ptr_t)(sV + 512 * j), 16, dl.v[t], v_soff, 0, 0);
+      }
+    }
+  }
+}
+
+// Row-major bf16 V of the padded layout (VROWS, direct): the instruction layout of a K sub-tile (instruction j
+// fills rows 8 j .. 8 j + 7, two a wave), keys in natural order under swzv; the descriptor bounds the reads to the
+// window's full blocks.
+template <int DT>
+struct DirectRows {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off[2];                       // byte offsets of instructions w and w + 4 for the block at key 0
+  bool ok[Width<DT>::kSubTiles][2];      // the lane's chunk lies inside head_dim
+};
+
+template <int DT>
+__device__ __forceinline__ DirectRows<DT> direct_rows(const XattnParams& p, const uint16_t* V, int dchunks, int nfull,
+                                                      int w) {
+  DirectRows<DT> dr;
+  const int lane = threadIdx.x & 63;
+  const uint32_t bytes = static_cast<uint32_t>(((static_cast<int64_t>(nfull) * kKB - 1) * p.sv_k + p.D) * 2);
+  dr.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(V), 0, bytes, kRsrcFlags);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int R = 8 * (w + 4 * t) + (lane >> 3);
+    const int c = swzv(R, lane & 7);  // swzv is an involution in c
+    dr.off[t] = static_cast<uint32_t>((R * p.sv_k + 8 * c) * 2);
+#pragma unroll
+    for (int u = 0; u < Width<DT>::kSubTiles; ++u) dr.ok[u][t] = 8 * u + c < dchunks;
+  }
+  return dr;
+}
+
+template <int DT, bool FULL_D>
+__device__ __forceinline__ void stage_rows(const DirectRows<DT>& dr, uint32_t soff, int w, uint16_t* sV) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
     const int j = w + 4 * t;
-    if (FULL_D || dl.v_ok[t]) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dl.v_rsrc, (lds_ptr_t)(sV + 512 * j), 16, dl.v[t], v_soff, 0, 0);
+#pragma unroll
+    for (int u = 0; u < Width<DT>::kSubTiles; ++u) {
+      if ((FULL_D && 64 * (u + 1) <= 32 * DT) || dr.ok[u][t]) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(dr.rsrc, (lds_ptr_t)(sV + u * kKTile + 512 * j), 16, dr.off[t],
+                                                 soff + 2 * kSub * u, 0, 0);
+      }
     }
   }
 }
@@ -575,15 +625,16 @@ enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2, kRegisterFull = 3 };
 // ONES: head_dim below 32 DT, the row sum comes from the matrix cores (V^T row D of ones). The e4m3 V^T kernel up
 // to head_dim 64 is held to 168 VGPRs (three waves per SIMD; it needs 170 unbounded, without spilling at 168); the
 // bf16 direct-staged ones fit by themselves.
-// KMASK: a key mask (p.kv_mask) on top of the window length; every block then masks its keys.
+// KMASK: a key mask (p.kv_mask) on top of the window length; every block masks its scores (with row-major V a
+// block whose keys it all masks is skipped and one whose keys it all attends is computed as without a mask).
 // PV8: e4m3 K/V take the second product on the fp8 matrix cores (see the comment at the top).
 // VD8: with PV8, V^T takes direct loads for full blocks (e4m3 rows of 16-byte aligned runs).
 template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false, bool PV8 = false, bool VD8 = false>
-__global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
+__global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
   constexpr bool DIRECT = STAGING == kDirect || STAGING == kDirectFull;
   constexpr bool FULLK = STAGING == kDirectFull || STAGING == kRegisterFull;  // head_dim 32 DT
-  static_assert(!KMASK || !DIRECT, "the key-mask path stages through registers");
   static_assert(!ONES || !FULLK, "a full-width head has no padding row");
+  static_assert(!KMASK || !DIRECT, "the key-mask path stages through registers");
   static_assert(!PV8 || (FP8 && !DIRECT && !KMASK), "the e4m3 second product stages e4m3 K/V through registers");
   static_assert(!VD8 || (PV8 && VT), "direct e4m3 V^T loads serve the e4m3 second product");
   // bf16 P with no padding row for the row sum: the matrix cores form it from the packed P (see onesb).
@@ -593,8 +644,11 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
   // cache, staged through registers, the form measured no faster.)
   constexpr bool SPEC = MSUM && !FP8 && DT == 2;
   constexpr int kSubTiles = Width<DT>::kSubTiles;
-  // V^T tile: 32 DT rows of 64 keys, bf16 (kRow elements a row) or e4m3 (kRow8 bytes a row).
-  constexpr int kVTile = PV8 ? 32 * DT * kRow8 / 2 : 32 * DT * kRow;
+  // Row-major V with a bf16 second product: V rows in LDS, read transposed (see swzv).
+  constexpr bool VROWS = !VT && !PV8;
+  // V tile: V^T, 32 DT rows of 64 keys, bf16 (kRow elements a row) or e4m3 (kRow8 bytes a row); V rows in K's
+  // sub-tiles.
+  constexpr int kVTile = PV8 ? 32 * DT * kRow8 / 2 : (VROWS ? kSubTiles * kKTile : 32 * DT * kRow);
   // Four distinct LDS objects (not one indexed array): the compiler can then tell the direct loads into one
   // buffer from the operand reads of the other and does not wait for the loads in flight before those reads.
   __shared__ __attribute__((aligned(16))) uint16_t sK0[kSubTiles * kKTile], sK1[kSubTiles * kKTile];
@@ -705,12 +759,29 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
         }
       }
     }
-    if (ONES && threadIdx.x < 16) {
+    if constexpr (VROWS) {
+      // Direct loads never write the chunks of V rows past head_dim: zeros, and with ONES the ones column D.
+      if (dchunks < 8 * kSubTiles) {
+        for (int i = threadIdx.x; i < kSubTiles * kKB * 8; i += kThreads) {
+          const int u = i / (kKB * 8), R = (i >> 3) % kKB, c = i & 7;
+          if (8 * u + c >= dchunks) {
+            const int e = u * kKTile + R * kRow + swzv(R, c) * 8;
+            const uint4 x = (ONES && 8 * u + c == dchunks) ? raw_one_first<false>() : make_uint4(0u, 0u, 0u, 0u);
+            *reinterpret_cast<uint4*>(sV0 + e) = x;
+            *reinterpret_cast<uint4*>(sV1 + e) = x;
+          }
+        }
+      }
+    } else if (ONES && threadIdx.x < 16) {
       // Direct loads never write V^T rows >= D: row D of both buffers holds ones for the whole kernel.
       const int R = static_cast<int>(p.D), c = threadIdx.x & 7;
       uint16_t* buf = threadIdx.x < 8 ? sV0 : sV1;
       *reinterpret_cast<uint4*>(buf + R * kRow + swz(R, c) * 8) = raw_one<false>();
     }
+  }
+  [[maybe_unused]] DirectRows<DT> dr;
+  if constexpr (DIRECT && VROWS) {
+    dr = direct_rows<DT>(p, reinterpret_cast<const uint16_t*>(V), dchunks, nfull, w);
   }
 
   [[maybe_unused]] DirectV8<DT> dv;
@@ -735,6 +806,22 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
   [[maybe_unused]] uint32_t rdv[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) rdv[s] = static_cast<uint32_t>(col * kRow8 + swz8(col, 2 * hh + s) * 16);
+  // VROWS: byte offsets of the transposed reads of output tile j (head_dim 32 j .. 32 j + 31). Within each 16-lane
+  // group a ds_read_b64_tr_b16 gives lane i element i % 4 of the 8-byte reads of lanes 4 n + i / 4 (n = 0..3), so
+  // lane L reads key 8 (L / 32) + (L % 16) / 4 of the k-step, head_dim 16 ((L / 16) % 2) + 4 (L % 4) .. + 3: lane
+  // l then holds keys 8 (l / 32) + 0..3 of column l % 32 (and + 4..7 from the read 4 rows further), the A operand
+  // of the second product. The swizzle of those rows depends on the lane only.
+  [[maybe_unused]] uint32_t rvt[DT];
+  if constexpr (VROWS) {
+    const int row_lane = 8 * (lane >> 5) + ((lane & 15) >> 2);
+    const int flip = (row_lane >> 1) & 1;
+    const int c_lane = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+#pragma unroll
+    for (int j = 0; j < DT; ++j) {
+      rvt[j] = static_cast<uint32_t>(((j >> 1) * kKTile + row_lane * kRow) * 2 + 16 * (4 * ((j & 1) ^ flip) + c_lane) +
+                                     8 * (lane & 1));
+    }
+  }
   // 16-wide k-steps of the score product that head_dim reaches (2 DT at head_dim 32 DT).
   const int ksteps = FULLK ? 2 * DT : __builtin_amdgcn_readfirstlane(static_cast<int>((p.D + 15) / 16));
 
@@ -779,8 +866,9 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
   auto stage_issue = [&](int blk, uint16_t* sK, uint16_t* sV) __attribute__((always_inline)) {
     if constexpr (DIRECT) {
       const int kv0 = blk * kKB;
-      stage_direct<DT, STAGING == kDirectFull>(dl, static_cast<uint32_t>(kv0 * p.sk_k * 2), static_cast<uint32_t>(kv0 * 2),
-                                         w, sK, sV);
+      stage_direct<DT, STAGING == kDirectFull, VT>(dl, static_cast<uint32_t>(kv0 * p.sk_k * 2),
+                                                   static_cast<uint32_t>(kv0 * 2), w, sK, sV);
+      if constexpr (VROWS) stage_rows<DT, STAGING == kDirectFull>(dr, static_cast<uint32_t>(kv0 * p.sv_k * 2), w, sV);
     } else {
       stage_load<FP8, VT, DT, false, ONES, !VD8>(st, p, K, V, L, blk * kKB, dchunks, vt_vec);
       if constexpr (VD8) {
@@ -910,6 +998,10 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
     const char* kp = reinterpret_cast<const char*>(Ks);
     const char* vp = reinterpret_cast<const char*>(Vt);
     const uint64_t bits = block_bits(kv0);
+    // A key mask that masks every key of the block: the block adds nothing to O, l or m (its P are all 0), so it
+    // is skipped (wave-uniform; the block's barrier is outside). Row-major V only: the V^T form has no registers
+    // to spare for it.
+    if (KMASK && VROWS && bits == 0ull) return;
     [[maybe_unused]] uint32_t pf[8];  // PV8: e4m3 P, bytes 16 t + i
     [[maybe_unused]] int drop = 0;    // PV8: halvings of half 0 since it was packed
     // S^T of keys 32 t .. 32 t + 31 of the block (LDS rows 32 t + col), keys past L (and, with a key mask, keys
@@ -938,7 +1030,9 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
           }
         }
       }
-      if constexpr (MASKED || KMASK) {
+      // A key mask that attends every key of a full block changes none of its scores: no masking then (row-major
+      // V; the V^T form, short of registers, always masks).
+      if (MASKED || (KMASK && (!VROWS || bits != ~0ull))) {
         // Entry i is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8) (PV8: 32 hh + 16 t + i); with a key mask,
         // bit i of `mine`.
         const uint32_t hb = static_cast<uint32_t>(bits >> (32 * t));
@@ -1041,7 +1135,16 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
           bf16x8_t a[DT];
 #pragma unroll
           for (int j = 0; j < DT; ++j) {
-            a[j] = *reinterpret_cast<const bf16x8_t*>(vp + rd[2 * t + ks] + j * (32 * kRow * 2));
+            if constexpr (VROWS) {
+              typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+              typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+              char* b = const_cast<char*>(vp) + rvt[j] + (32 * t + 16 * ks) * kRow * 2;
+              const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(b));
+              const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(b + 4 * kRow * 2));
+              a[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            } else {
+              a[j] = *reinterpret_cast<const bf16x8_t*>(vp + rd[2 * t + ks] + j * (32 * kRow * 2));
+            }
           }
 #pragma unroll
           for (int j = 0; j < DT; ++j) o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], pb[ks], o[j], 0, 0, 0);
@@ -1243,8 +1346,8 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && VT) ? 3 : 2) void xattn_fwd_k
   }
 }
 
-// The instantiation for DT = head_dim / 32 rounded up: e4m3 and row-major forms through registers, bf16 V^T
-// directly to LDS (head_dim 32 DT without exec masking).
+// The instantiation for DT = head_dim / 32 rounded up: e4m3, the packed layout and key masks through registers,
+// bf16 K and V (V^T or V rows) of the padded layout directly to LDS (head_dim 32 DT without exec masking).
 template <int DT, bool ONES>
 void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool pv8, bool vt, bool direct) {
   constexpr int RS = ONES ? kRegister : kRegisterFull;
@@ -1271,9 +1374,17 @@ void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool p
       xattn_fwd_kernel<true, false, RS, DT, ONES, false, false><<<g, kThreads, 0, s>>>(p);
     }
   } else if (direct && !ONES) {
-    xattn_fwd_kernel<false, true, kDirectFull, DT, false><<<g, kThreads, 0, s>>>(p);
+    if (vt) {
+      xattn_fwd_kernel<false, true, kDirectFull, DT, false><<<g, kThreads, 0, s>>>(p);
+    } else {
+      xattn_fwd_kernel<false, false, kDirectFull, DT, false><<<g, kThreads, 0, s>>>(p);
+    }
   } else if (direct) {
-    xattn_fwd_kernel<false, true, kDirect, DT, true><<<g, kThreads, 0, s>>>(p);
+    if (vt) {
+      xattn_fwd_kernel<false, true, kDirect, DT, true><<<g, kThreads, 0, s>>>(p);
+    } else {
+      xattn_fwd_kernel<false, false, kDirect, DT, true><<<g, kThreads, 0, s>>>(p);
+    }
   } else if (vt) {
     xattn_fwd_kernel<false, true, RS, DT, ONES><<<g, kThreads, 0, s>>>(p);
   } else {
@@ -1281,8 +1392,8 @@ void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool p
   }
 }
 
-// The instantiation for DT = head_dim / 32 rounded up: e4m3 and row-major forms through registers, bf16 V^T
-// directly to LDS; head_dim below 32 DT takes the row sum from the matrix cores.
+// The instantiation for DT = head_dim / 32 rounded up (see launch_dt); head_dim below 32 DT takes the row sum from
+// the matrix cores.
 template <int DT>
 void launch(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool pv8, bool vt, bool direct) {
   if (p.D < 32 * DT) {
@@ -1363,14 +1474,17 @@ static int xattn_impl(const void* q, const void* k, const void* v, void* o, int 
   p.q_tiles = static_cast<int>(cdiv(Q, kQTile));
   const int64_t grid = static_cast<int64_t>(p.q_tiles) * H * B;
   SVHIP_REQUIRE(grid < (1ll << 31), "%s: grid too large", name);
-  // Direct-to-LDS staging: bf16 K and V^T of the padded layout whose rows (and every 8-key run of V^T) start on
-  // 16-byte boundaries, whose byte offsets from a (window, head) base fit 32 bits.
+  // Direct-to-LDS staging: bf16 K and V whose rows (and every 8-key run of V^T) start on 16-byte boundaries and
+  // whose byte offsets from a (window, head) base fit 32 bits: V^T of the padded layout, row-major V of either
+  // layout (a packed window starts at any key, which keeps its rows aligned but not the 8-key runs of V^T).
   // e4m3 with the fp8 second product: V^T alone takes direct loads, rows of 16-byte aligned 16-key runs.
   const bool direct =
       fp8 ? (pv8 && vt && !cu_seqlens && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_d % 16 == 0 &&
              sv_h % 16 == 0 && sv_b % 16 == 0 && D * sv_d + kv_cap < (1ll << 32))
-          : (vt && !cu_seqlens && reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_d % 8 == 0 && sv_h % 8 == 0 &&
-             sv_b % 8 == 0 && (kv_cap * sk_k + D) * 2 < (1ll << 32) && (D * sv_d + kv_cap) * 2 < (1ll << 32));
+          : (reinterpret_cast<uintptr_t>(v) % 16 == 0 && sv_h % 8 == 0 && sv_b % 8 == 0 &&
+             (kv_cap * sk_k + D) * 2 < (1ll << 32) &&
+             (vt ? !cu_seqlens && sv_d % 8 == 0 && (D * sv_d + kv_cap) * 2 < (1ll << 32)
+                 : sv_k % 8 == 0 && (kv_cap * sv_k + D) * 2 < (1ll << 32)));
   hipStream_t s = as_stream(stream);
   const unsigned g = static_cast<unsigned>(grid);
   if (D <= 64) {

@@ -212,7 +212,7 @@ def test_fp8_decode_is_exact_for_every_code(dev):
 def test_transposed_v_padded_layout_fast_path(dev, D):
     """V stored transposed in a padded [B,H,D,Kcap] buffer (the cached-context layout) takes the direct-to-LDS
     staging: full blocks, a partial last block, a window shorter than one block; NaN in the padding must not
-    leak, and the result must equal the row-major-V path bit for bit."""
+    leak, and the result must equal the row-major-V path (V rows in LDS, read transposed) bit for bit."""
     from streamvoxel_amd.stream.attention import attention
     B, H, Q, kcap = 4, 3, 160, 448
     lengths = [448, 100, 64, 7]
@@ -238,8 +238,8 @@ def test_direct_staging_every_block_count(dev, D):
     """Direct staging alternates two LDS tile pairs and peels the last full block and the partial one: windows of
     0..10 full blocks, with and without a partial last block, cover every entry into and exit from its unrolled
     loop and both tile parities at the end. The result must match the float64 oracle and equal the row-major-V
-    path (staged through registers) bit for bit; every key block carries its own score scale and value offset, so
-    a block read from the wrong tile changes the result."""
+    path (also direct, V rows read transposed) bit for bit; every key block carries its own score scale and value
+    offset, so a block read from the wrong tile changes the result."""
     from streamvoxel_amd.stream.attention import attention
     lengths = [64 * n + t for n in range(11) for t in (0, 29) if 64 * n + t > 0]
     B, H, Q, kcap = len(lengths), 2, 96, 704
@@ -538,6 +538,73 @@ def test_key_mask_prefix_equals_lengths_and_packed(dev):
     out = attention(qd, kp.to(dev), vp.to(dev), cu_seqlens=cu.to(dev), key_mask=mask.to(dev))
     torch.cuda.synchronize()
     check(out, _masked_reference(q, k, v, mask, lengths), BF16_ATOL, BF16_RTOL)
+
+
+@pytest.mark.parametrize('D', [64, 48, 96, 128, 32])
+def test_row_major_v_every_block_count_padded_packed_and_registers(dev, D):
+    """Row-major V stays one key a row in LDS and the second product reads it transposed (ds_read_b64_tr_b16):
+    direct loads in the padded and in the packed cu_seqlens layout, through registers with a key mask. Windows of
+    0..10 full blocks with and without a partial one (every key block its own score scale and value offset, NaN in
+    the padding past each window); all three forms must match the float64 oracle and give the bits of the V^T
+    layout."""
+    from streamvoxel_amd.stream.attention import attention
+    lengths = [64 * n + t for n in range(11) for t in (0, 37) if 64 * n + t > 0]
+    B, H, Q, kcap = len(lengths), 2, 96, 704
+    _case(f'xattn row-major V (direct, packed, registers) D={D} lengths={lengths}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=301 + D)
+    block = torch.arange(kcap) // 64
+    k = (k.float() * (1 + 0.29 * (block % 7)).view(1, 1, -1, 1)).to(torch.bfloat16)
+    v = (v.float() + 0.04 * (block % 5).view(1, 1, -1, 1)).to(torch.bfloat16)
+    ref = A.cross_attention(q, k, v, lengths)
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    vt = v.transpose(2, 3).contiguous().to(dev)
+    qd, kd = q.to(dev), k.to(dev)
+    out_vt = attention(qd, kd, vt.transpose(2, 3), lengths=lt)
+    vn = v.clone()
+    for b, n in enumerate(lengths):
+        vn[b, :, n:] = float('nan')
+    out_rows = attention(qd, kd, vn.to(dev), lengths=lt)
+    cu = torch.zeros(B + 1, dtype=torch.int32)
+    cu[1:] = torch.tensor(lengths).cumsum(0)
+    kp = torch.cat([k[b, :, :lengths[b]] for b in range(B)], 1).to(dev)
+    vp = torch.cat([v[b, :, :lengths[b]] for b in range(B)], 1).to(dev)
+    out_packed = attention(qd, kp, vp, cu_seqlens=cu.to(dev))
+    every = torch.ones(B, kcap, dtype=torch.bool, device=dev)
+    out_regs = attention(qd, kd, v.to(dev), lengths=lt, key_mask=every)
+    torch.cuda.synchronize()
+    check(out_rows, ref, BF16_ATOL, BF16_RTOL)
+    assert torch.equal(out_rows, out_vt)
+    assert torch.equal(out_packed, out_vt)
+    assert torch.equal(out_regs, out_vt)
+
+
+@pytest.mark.parametrize('D', [64, 48, 96])
+def test_key_mask_row_major_v_whole_blocks(dev, D):
+    """A key mask over row-major V skips the blocks it wholly masks and computes the blocks it wholly attends as
+    without a mask: masks that alternate whole masked, whole attended and mixed blocks (and a window that starts
+    with masked blocks) must match the float64 oracle and give the bits of the same mask over V^T, which masks
+    every block's scores."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, kcap = 4, 3, 130, 640
+    _case(f'xattn key mask over row-major V, whole blocks D={D}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=401 + D)
+    g = torch.Generator().manual_seed(9 + D)
+    blk = torch.arange(kcap) // 64
+    mixed = torch.rand(B, kcap, generator=g) < 0.6
+    mask = torch.where((blk % 3 == 0)[None], torch.zeros(B, kcap, dtype=torch.bool),
+                       torch.where((blk % 3 == 1)[None], torch.ones(B, kcap, dtype=torch.bool), mixed))
+    mask[1, :200] = False                   # three whole blocks and more before the first attended key
+    mask[2] = True                          # every key attended
+    mask[3, 320:] = False                   # a masked tail of whole blocks
+    lengths = [640, 600, 411, 640]
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    qd, kd = q.to(dev), k.to(dev)
+    md = mask.to(dev)
+    out_rows = attention(qd, kd, v.to(dev), lengths=lt, key_mask=md)
+    out_vt = attention(qd, kd, v.transpose(2, 3).contiguous().to(dev).transpose(2, 3), lengths=lt, key_mask=md)
+    torch.cuda.synchronize()
+    check(out_rows, _masked_reference(q, k, v, mask, lengths), BF16_ATOL, BF16_RTOL)
+    assert torch.equal(out_rows, out_vt)
 
 
 @pytest.mark.parametrize('D', [64, 48])
