@@ -57,16 +57,19 @@ def build_trace(verbose=False):
 
 
 MICROBENCH = os.path.join(HERE, 'microbench', 'xattn_chain')
+TR16_PROBE = os.path.join(HERE, 'microbench', 'tr16_probe')
 
 
 def build_microbench():
-    """The standalone program microbench/xattn_chain.hip (no library): the cross-attention half's instructions with
-    its dependencies, one ingredient at a time."""
+    """The standalone programs under microbench/ (no library): xattn_chain.hip, the cross-attention half's
+    instructions with its dependencies, one ingredient at a time; tr16_probe.hip, the lane layout of the LDS
+    transpose load the kernel reads row-major V with."""
     flags = [f for f in FLAGS if f not in ('-shared', '-fPIC')]
-    res = subprocess.run([hipcc(), *flags, MICROBENCH + '.hip', '-o', MICROBENCH], stdout=subprocess.PIPE,
-                         stderr=subprocess.STDOUT)
-    if res.returncode != 0:
-        raise RuntimeError('hipcc failed (microbench):\n' + res.stdout.decode(errors='replace'))
+    for prog in (MICROBENCH, TR16_PROBE):
+        res = subprocess.run([hipcc(), *flags, prog + '.hip', '-o', prog], stdout=subprocess.PIPE,
+                             stderr=subprocess.STDOUT)
+        if res.returncode != 0:
+            raise RuntimeError('hipcc failed (microbench):\n' + res.stdout.decode(errors='replace'))
     return MICROBENCH
 
 
