@@ -578,6 +578,31 @@ def test_row_major_v_every_block_count_padded_packed_and_registers(dev, D):
     assert torch.equal(out_regs, out_vt)
 
 
+@pytest.mark.parametrize('D', [64, 48])
+def test_kv_as_views_of_the_projection_output(dev, D):
+    """K and V as the views `local_kv` returns (streamvoxel/stream/fast_ops.py:90-95): [B, L, 2, H, D] projection
+    output, K = [:, :, 0] and V = [:, :, 1] transposed to [B, H, L, D], so consecutive keys lie 2 H D elements apart
+    and the heads D apart. Row-major V from such a view takes the direct loads; the result must match float64 and
+    give the bits of the same K/V made contiguous."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, L = 3, 4, 100, 333
+    lengths = [333, 200, 64]
+    _case(f'xattn K/V as projection views D={D}')
+    g = torch.Generator().manual_seed(77 + D)
+    kv = (torch.randn(B, L, 2, H, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    q = (torch.randn(B, H, Q, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    kvd = kv.to(dev)
+    k_view, v_view = kvd[:, :, 0].transpose(1, 2), kvd[:, :, 1].transpose(1, 2)    # [B, H, L, D] views
+    assert k_view.stride(2) == 2 * H * D and v_view.stride(1) == D
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    out_view = attention(q.to(dev), k_view, v_view, lengths=lt)
+    out_dense = attention(q.to(dev), k_view.contiguous(), v_view.contiguous(), lengths=lt)
+    torch.cuda.synchronize()
+    k = kv[:, :, 0].transpose(1, 2).contiguous()
+    v = kv[:, :, 1].transpose(1, 2).contiguous()
+    check(out_view, A.cross_attention(q, k, v, lengths), BF16_ATOL, BF16_RTOL)
+    assert torch.equal(out_view, out_dense)
+
 @pytest.mark.parametrize('D', [64, 48, 96])
 def test_key_mask_row_major_v_whole_blocks(dev, D):
     """A key mask over row-major V skips the blocks it wholly masks and computes the blocks it wholly attends as
