@@ -162,7 +162,8 @@ int svhip_ease_select_patches(const void* logits, int dtype, int64_t classes, in
  * inside the packed K/V, as for the reference's packed attention.
  * Q, O: bf16, element (b,h,q,d) at b*s?_b + h*s?_h + q*s?_q + d. K: element (b,h,j,d) at
  * b*sk_b + h*sk_h + row*sk_k + d; V: at b*sv_b + h*sv_h + row*sv_k + d*sv_d, where either sv_d == 1 (rows of
- * head_dim, the reference layout) or sv_k == 1 (V stored transposed, keys contiguous: the fast staging path);
+ * head_dim, the reference layout) or sv_k == 1 (V stored transposed, keys contiguous). bf16 K and V with
+ * 16-byte aligned rows take the fast staging path (V^T of the padded layout, V rows of either layout);
  * row = j, or cu_seqlens[b] + j in the packed layout (sk_b / sv_b are then ignored). kv_dtype SVHIP_BF16, or
  * e4m3 (OCP e4m3fn bytes) with per-(window, head) fp32 dequantisation scales k_scale/v_scale [B,H]:
  * SVHIP_FP8_E4M3 decodes K and V exactly to bf16 in the kernel and keeps P in bf16 (the reference's in-kernel
