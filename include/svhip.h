@@ -200,6 +200,17 @@ int svhip_xattn_fwd_masked(const void* q, const void* k, const void* v, void* o,
                            int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream);
 
 /*
+ * The effective window lengths of a key mask: out[b] (int32, device) = 1 + the last key j < n_b with
+ * kv_mask[b * sm_b + j] != 0, or 0 when there is none, where n_b = min(kv_len[b], kv_cap) (kv_cap when kv_len is
+ * NULL). Passed to svhip_xattn_fwd_masked as kv_len it gives the same output (the keys past a window's last
+ * attended key add nothing) and lets the kernel rank the windows by the keys they really attend.
+ * Serves: the masked SDPA of cross_sdpa (streamvoxel/stream/fast_ops.py:111-115), whose `valid` mask holds the
+ * window lengths.
+ */
+int svhip_mask_lengths(const uint8_t* kv_mask, int64_t sm_b, const int32_t* kv_len, int64_t B, int64_t kv_cap,
+                       int32_t* out, void* stream);
+
+/*
  * Cross attention in fp32 arithmetic: fp32 q/k/v/o with the layouts and strides of svhip_xattn_fwd (elements, not
  * bytes; rows 16-byte aligned; V as rows or as V^T), padded with kv_len or packed with cu_seqlens; head_dim 16, 32,
  * 48 or 64. Every product, sum and exponential is fp32 (the VALU; no rounding of the operands), at the fp32 FMA

@@ -47,6 +47,7 @@ SIGNATURES = {
     'svhip_xattn_fwd': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, ctypes.c_int, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
                                        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f, _c_p]),
+    'svhip_mask_lengths': (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     'svhip_xattn_fwd_masked': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p] + [_c_i64] * 18
                                + [_c_f, _c_p]),
     'svhip_xattn_fwd_f32': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p] + [_c_i64] * 18 + [_c_f, _c_p]),

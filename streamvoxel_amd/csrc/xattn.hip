@@ -616,6 +616,38 @@ __device__ __forceinline__ void direct_v8_load(__amdgpu_buffer_rsrc_t rsrc, uint
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// The highest index j < n with row[j] != 0 among the ones this thread reads (thread t of kThreads: 16-byte chunks
+// t, t + kThreads, ... of a 16-byte aligned row, four loads in flight; the rest, or an unaligned row, byte by byte
+// with eight loads in flight), or -1. The caller takes the maximum over the workgroup.
+__device__ __forceinline__ int last_attended(const uint8_t* row, int n) {
+  int last = -1;
+  const int nvec = (reinterpret_cast<uintptr_t>(row) & 15) == 0 ? n / 16 : 0;
+  for (int c0 = threadIdx.x; c0 < nvec; c0 += 4 * kThreads) {
+    uint4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + u * kThreads;
+      x[u] = c < nvec ? reinterpret_cast<const uint4*>(row)[c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {  // the highest nonzero byte of word q: byte 4 q + (31 - clz) / 8
+        if (w[q] != 0u) last = max(last, 16 * (c0 + u * kThreads) + 4 * q + ((31 - __clz(w[q])) >> 3));
+      }
+    }
+  }
+  for (int j0 = 16 * nvec + threadIdx.x; j0 < n; j0 += 8 * kThreads) {
+    uint8_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = row[min(j0 + u * kThreads, n - 1)];  // no branch around the loads
+#pragma unroll
+    for (int u = 0; u < 8; ++u) last = (v[u] && j0 + u * kThreads < n) ? max(last, j0 + u * kThreads) : last;
+  }
+  return last;
+}
+
 // STAGING: kRegister (registers for every block), kDirect (direct loads for full blocks, any head_dim),
 // kDirectFull (the same at head_dim 32 DT), kRegisterFull (registers at head_dim 32 DT). The last, partial block
 // of a window always goes through registers. At head_dim 32 DT the score product's k-steps are all known at
@@ -625,16 +657,20 @@ enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2, kRegisterFull = 3 };
 // ONES: head_dim below 32 DT, the row sum comes from the matrix cores (V^T row D of ones). The e4m3 V^T kernel up
 // to head_dim 64 is held to 168 VGPRs (three waves per SIMD; it needs 170 unbounded, without spilling at 168); the
 // bf16 direct-staged ones fit by themselves.
-// KMASK: a key mask (p.kv_mask) on top of the window length; every block masks its scores (with row-major V a
-// block whose keys it all masks is skipped and one whose keys it all attends is computed as without a mask).
+// KMASK: a key mask (p.kv_mask) on top of the window length: a block whose keys it all masks is skipped, one whose
+// keys it all attends is computed as without a mask, any other masks its scores (the register-staged V^T form
+// masks every block).
 // PV8: e4m3 K/V take the second product on the fp8 matrix cores (see the comment at the top).
 // VD8: with PV8, V^T takes direct loads for full blocks (e4m3 rows of 16-byte aligned runs).
 template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false, bool PV8 = false, bool VD8 = false>
 __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void xattn_fwd_kernel(XattnParams p) {
+  // The body is compiled in the device pass only: the host pass, which needs just the launch stub, otherwise
+  // instantiates the staging lambdas of the key-mask kernels with direct loads and rejects their calls of the
+  // device-only staging functions.
+#if defined(__HIP_DEVICE_COMPILE__)
   constexpr bool DIRECT = STAGING == kDirect || STAGING == kDirectFull;
   constexpr bool FULLK = STAGING == kDirectFull || STAGING == kRegisterFull;  // head_dim 32 DT
   static_assert(!ONES || !FULLK, "a full-width head has no padding row");
-  static_assert(!KMASK || !DIRECT, "the key-mask path stages through registers");
   static_assert(!PV8 || (FP8 && !DIRECT && !KMASK), "the e4m3 second product stages e4m3 K/V through registers");
   static_assert(!VD8 || (PV8 && VT), "direct e4m3 V^T loads serve the e4m3 second product");
   // bf16 P with no padding row for the row sum: the matrix cores form it from the packed P (see onesb).
@@ -703,8 +739,23 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
   const int64_t q = static_cast<int64_t>(qt) * kQTile + w * 32 + col;
   const bool q_ok = q < p.Q;
 
-  const int L = window_length(p, b);
   const int64_t off = p.cu_seqlens ? p.cu_seqlens[b] : 0;
+  const int L = [&]() __attribute__((always_inline)) {
+    const int n = window_length(p, b);
+    if constexpr (!KMASK) {
+      return n;
+    } else {
+      // With a key mask the window ends at its last attended key: the blocks after it add nothing to O, l or m.
+      // One scan of the window's mask row (a wave-uniform result; no attended key gives L = 0 and zeros).
+      __shared__ int s_last;
+      if (threadIdx.x == 0) s_last = -1;
+      __syncthreads();
+      const int last = last_attended(p.kv_mask + b * p.sm_b, n);
+      if (last >= 0) atomicMax(&s_last, last);
+      __syncthreads();
+      return s_last + 1;
+    }
+  }();
 
   const uint16_t* Qp = static_cast<const uint16_t*>(p.q) + b * p.sq_b + h * p.sq_h;
   uint16_t* Op = static_cast<uint16_t*>(p.o) + b * p.so_b + h * p.so_h;
@@ -891,13 +942,23 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
   };
 
 
-  // The key mask of the block starting at kv0 as 64 bits (bit i: key kv0 + i is attended), wave-uniform.
+  // The key mask of the block starting at kv0 as 64 bits (bit i: key kv0 + i is attended), wave-uniform. The
+  // blocks are computed in order, so each call takes the byte the previous one fetched (lane l: key kv0 + l) and
+  // fetches the next block's: its load completes under the block's compute instead of stalling the next block.
   const uint8_t* mrow = KMASK ? p.kv_mask + b * p.sm_b : nullptr;
-  auto block_bits = [&](int kv0) __attribute__((always_inline)) -> uint64_t {
+  [[maybe_unused]] int mask_on = 0;
+  auto mask_fetch = [&](int kv0) __attribute__((always_inline)) {
     if constexpr (KMASK) {
       const int j = kv0 + lane;
-      const bool on = j < L && mrow[j] != 0;
-      return __builtin_amdgcn_ballot_w64(on);
+      mask_on = (j < L && mrow[j] != 0) ? 1 : 0;
+    }
+  };
+  mask_fetch(0);
+  auto block_bits = [&](int kv0) __attribute__((always_inline)) -> uint64_t {
+    if constexpr (KMASK) {
+      const uint64_t bits = __builtin_amdgcn_ballot_w64(mask_on != 0);
+      mask_fetch(kv0 + kKB);
+      return bits;
     } else {
       return ~0ull;
     }
@@ -999,9 +1060,9 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
     const char* vp = reinterpret_cast<const char*>(Vt);
     const uint64_t bits = block_bits(kv0);
     // A key mask that masks every key of the block: the block adds nothing to O, l or m (its P are all 0), so it
-    // is skipped (wave-uniform; the block's barrier is outside). Row-major V only: the V^T form has no registers
-    // to spare for it.
-    if (KMASK && VROWS && bits == 0ull) return;
+    // is skipped (wave-uniform; the block's barrier is outside). Not in the register-staged V^T form, which has no
+    // registers to spare for it.
+    if (KMASK && (DIRECT || VROWS) && bits == 0ull) return;
     [[maybe_unused]] uint32_t pf[8];  // PV8: e4m3 P, bytes 16 t + i
     [[maybe_unused]] int drop = 0;    // PV8: halvings of half 0 since it was packed
     // S^T of keys 32 t .. 32 t + 31 of the block (LDS rows 32 t + col), keys past L (and, with a key mask, keys
@@ -1030,9 +1091,9 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
           }
         }
       }
-      // A key mask that attends every key of a full block changes none of its scores: no masking then (row-major
-      // V; the V^T form, short of registers, always masks).
-      if (MASKED || (KMASK && (!VROWS || bits != ~0ull))) {
+      // A key mask that attends every key of a full block changes none of its scores: no masking then (except in
+      // the register-staged V^T form, short of registers, which always masks).
+      if (MASKED || (KMASK && (!(DIRECT || VROWS) || bits != ~0ull))) {
         // Entry i is key 32 t + (i < 8 ? 8 hh + i : 16 + 8 hh + i - 8) (PV8: 32 hh + 16 t + i); with a key mask,
         // bit i of `mine`.
         const uint32_t hb = static_cast<uint32_t>(bits >> (32 * t));
@@ -1344,6 +1405,7 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
       }
     }
   }
+#endif  // __HIP_DEVICE_COMPILE__
 }
 
 // The instantiation for DT = head_dim / 32 rounded up: e4m3, V^T of the packed layout and key masks through
@@ -1352,8 +1414,13 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
 template <int DT, bool ONES>
 void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool pv8, bool vt, bool direct) {
   constexpr int RS = ONES ? kRegister : kRegisterFull;
-  if (p.kv_mask) {  // bf16 only (checked by the entry point), through registers
-    if (vt) {
+  if (p.kv_mask) {  // bf16 only (checked by the entry point)
+    constexpr int DS = ONES ? kDirect : kDirectFull;
+    if (direct && vt) {
+      xattn_fwd_kernel<false, true, DS, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
+    } else if (direct) {
+      xattn_fwd_kernel<false, false, DS, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
+    } else if (vt) {
       xattn_fwd_kernel<false, true, RS, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
     } else {
       xattn_fwd_kernel<false, false, RS, DT, ONES, true><<<g, kThreads, 0, s>>>(p);
@@ -1499,9 +1566,39 @@ static int xattn_impl(const void* q, const void* k, const void* v, void* o, int 
   return SVHIP_OK;
 }
 
+// One workgroup per window: out[b] = 1 + the last attended key among the window's first min(kv_len[b], kv_cap)
+// keys (kv_cap without kv_len), 0 when it has none.
+__global__ __launch_bounds__(kThreads) void mask_lengths_kernel(const uint8_t* mask, int64_t sm_b,
+                                                                const int32_t* kv_len, int64_t kv_cap, int32_t* out) {
+  __shared__ int s_last;
+  const int64_t b = blockIdx.x;
+  int64_t n = kv_cap;
+  if (kv_len) n = min(max(static_cast<int64_t>(kv_len[b]), int64_t{0}), kv_cap);
+  if (threadIdx.x == 0) s_last = -1;
+  __syncthreads();
+  const int last = last_attended(mask + b * sm_b, static_cast<int>(n));
+  if (last >= 0) atomicMax(&s_last, last);
+  __syncthreads();
+  if (threadIdx.x == 0) out[b] = s_last + 1;
+}
+
 }  // namespace svhip
 
 using namespace svhip;
+
+extern "C" int svhip_mask_lengths(const uint8_t* kv_mask, int64_t sm_b, const int32_t* kv_len, int64_t B,
+                                  int64_t kv_cap, int32_t* out, void* stream) {
+  const char* name = "svhip_mask_lengths";
+  clear_error();
+  SVHIP_REQUIRE(kv_mask && out, "%s: null pointer", name);
+  SVHIP_REQUIRE(B >= 0 && B < (1ll << 31), "%s: bad window count", name);
+  SVHIP_REQUIRE(kv_cap >= 0 && kv_cap < (1ll << 31), "%s: kv_cap out of range", name);
+  if (B == 0) return SVHIP_OK;
+  mask_lengths_kernel<<<static_cast<unsigned>(B), kThreads, 0, as_stream(stream)>>>(kv_mask, sm_b, kv_len, kv_cap,
+                                                                                      out);
+  SVHIP_LAUNCHED(name);
+  return SVHIP_OK;
+}
 
 #ifdef SVHIP_XATTN_TRACE
 // Trace build only: the device buffer the instrumented kernel writes (kTraceWords words per wave), or NULL to stop.

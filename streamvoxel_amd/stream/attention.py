@@ -99,10 +99,19 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
             raise TypeError('the key mask takes bf16 K/V')
         if cu_seqlens is None and key_mask.shape[1] < kcap:
             raise ValueError(f'key_mask holds {key_mask.shape[1]} keys per window, the cache {kcap}')
+        mask_cap = kcap if cu_seqlens is None else key_mask.shape[1]
+        if cu_seqlens is None:
+            # The windows' lengths cut at their last attended keys (the same output): the kernel ranks the
+            # windows by them, which balances the CUs when the mask, not `lengths`, holds the window lengths.
+            cut = torch.empty(B, dtype=torch.int32, device=query.device)
+            _lib.check(lib.svhip_mask_lengths(_lib.ptr(key_mask.view(torch.uint8)), key_mask.stride(0),
+                                              _lib.ptr(lengths), B, mask_cap, _lib.ptr(cut), _lib.stream_of(query)),
+                       'svhip_mask_lengths')
+            lengths = cut
         _lib.check(lib.svhip_xattn_fwd_masked(
             _lib.ptr(query), _lib.ptr(key), _lib.ptr(val), _lib.ptr(out), _lib.ptr(key_mask.view(torch.uint8)),
-            key_mask.stride(0), _lib.ptr(lengths), _lib.ptr(cu_seqlens), B, H, Q, D,
-            kcap if cu_seqlens is None else key_mask.shape[1], query.stride(0), query.stride(1), query.stride(2),
+            key_mask.stride(0), _lib.ptr(lengths), _lib.ptr(cu_seqlens), B, H, Q, D, mask_cap,
+            query.stride(0), query.stride(1), query.stride(2),
             *sk, *sv, out.stride(0), out.stride(1), out.stride(2), scale, _lib.stream_of(query)),
             'svhip_xattn_fwd_masked')
         return out

@@ -135,6 +135,12 @@ def test_argument_errors_of_the_newer_entry_points(lib):
     assert rc == -1 and b'null' in lib.svhip_last_error()
     # the cache writer's workspace query grows with heads and capacity
     assert lib.svhip_kv_write_workspace_bytes(16, 12672) >= lib.svhip_kv_write_workspace_bytes(8, 9792) > 0
+    # mask lengths: null mask or output, negative window count or capacity
+    assert lib.svhip_mask_lengths(None, 64, None, 2, 64, fake, None) == -1 and b'null' in lib.svhip_last_error()
+    assert lib.svhip_mask_lengths(fake, 64, None, 2, 64, None, None) == -1 and b'null' in lib.svhip_last_error()
+    assert lib.svhip_mask_lengths(fake, 64, None, -1, 64, fake, None) == -1 and b'window' in lib.svhip_last_error()
+    assert lib.svhip_mask_lengths(fake, 64, None, 2, -5, fake, None) == -1 and b'kv_cap' in lib.svhip_last_error()
+    assert lib.svhip_mask_lengths(fake, 64, None, 0, 64, fake, None) == 0      # nothing to do, no launch
 
 
 def test_argument_errors_of_the_sampling_tail(lib):

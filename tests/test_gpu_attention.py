@@ -632,6 +632,43 @@ def test_key_mask_row_major_v_whole_blocks(dev, D):
     assert torch.equal(out_rows, out_vt)
 
 
+def test_mask_lengths_cut_windows_at_their_last_attended_key(dev):
+    """svhip_mask_lengths: 1 + the last attended key of each window among its first min(kv_len, kv_cap) keys, 0
+    when none; aligned rows (16-byte vector reads) and unaligned ones (a slice of a wider mask: byte reads), with
+    and without kv_len, 300 windows, attended keys only in a row's last 16-byte chunk, only in its tail bytes,
+    only at key 0, none."""
+    import ctypes
+    from streamvoxel_amd import _lib
+    lib = _lib.load()
+    _case('svhip_mask_lengths')
+    B, kcap = 300, 1000
+    g = torch.Generator().manual_seed(5)
+    base = torch.rand(B, kcap + 8, generator=g) < 0.01
+    base[0] = False                                    # nothing attended
+    base[1] = False
+    base[1, 0] = True                                  # only key 0
+    base[2] = False
+    base[2, 990] = True                                # in the last whole 16-byte chunk of an aligned row
+    base[3] = False
+    base[3, 998] = True                                # in the tail past the last whole chunk
+    kv_len = torch.randint(0, kcap + 40, (B,), generator=g, dtype=torch.int32)
+    for mask in (base[:, :kcap].contiguous(), base[:, 3:kcap + 3]):      # aligned rows; rows 3 bytes in, stride 1008
+        md = mask.to(dev) if mask.is_contiguous() else base.to(dev)[:, 3:kcap + 3]
+        for lens in (None, kv_len):
+            out = torch.empty(B, dtype=torch.int32, device=dev)
+            lp = None if lens is None else lens.to(dev)
+            rc = lib.svhip_mask_lengths(ctypes.c_void_p(md.data_ptr()), md.stride(0), _lib.ptr(lp), B, kcap,
+                                        ctypes.c_void_p(out.data_ptr()), None)
+            assert rc == 0, lib.svhip_last_error()
+            torch.cuda.synchronize()
+            n = torch.full((B,), kcap) if lens is None else lens.clamp(0, kcap)
+            want = torch.zeros(B, dtype=torch.int32)
+            for b in range(B):
+                hit = mask[b, :int(n[b])].nonzero()
+                want[b] = int(hit[-1]) + 1 if len(hit) else 0
+            assert torch.equal(out.cpu(), want), (out.cpu() - want).abs().max()
+
+
 @pytest.mark.parametrize('D', [64, 48])
 def test_sharp_softmax_rows_take_no_extra_query_rounding(dev, D):
     """Sharp softmax rows (attention logits of standard deviation 4 and 8): the kernel stays within the bf16 bar of
