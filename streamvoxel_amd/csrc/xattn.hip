@@ -1408,9 +1408,9 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-// The instantiation for DT = head_dim / 32 rounded up: e4m3, V^T of the packed layout and key masks through
-// registers, bf16 K and V directly to LDS (V^T of the padded layout, V rows of either layout; head_dim 32 DT
-// without exec masking).
+// The instantiation for DT = head_dim / 32 rounded up: bf16 K and V directly to LDS (V^T of the padded layout,
+// V rows of either layout; head_dim 32 DT without exec masking), with or without a key mask; e4m3, V^T of the
+// packed layout and K/V spans past 32-bit offsets through registers.
 template <int DT, bool ONES>
 void launch_dt(const XattnParams& p, unsigned g, hipStream_t s, bool fp8, bool pv8, bool vt, bool direct) {
   constexpr int RS = ONES ? kRegister : kRegisterFull;

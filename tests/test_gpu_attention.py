@@ -285,8 +285,8 @@ def test_second_product_taken_back_on_score_jumps(dev, jump):
     """Scores (in nats) that jump by `jump`, 2 `jump`, ... above the window's earlier ones at keys past the first
     half, so that a half's second product was issued against a running max that no longer bounds it: from a few
     clamped weights (12) to weights far beyond the fp32 range against the stale max (1000). Within the bf16 bar
-    of float64, and the same bits on every staging at head_dim 64: V^T direct, V rows through registers, the packed
-    layout, and a prefix key mask."""
+    of float64, and the same bits on every staging at head_dim 64: V^T direct, V rows, the packed layout, and a
+    prefix key mask."""
     from streamvoxel_amd.stream.attention import attention
     B, H, Q, kcap, D = 2, 2, 64, 640, 64
     lengths = [640, 333]
@@ -543,14 +543,14 @@ def test_key_mask_prefix_equals_lengths_and_packed(dev):
 @pytest.mark.parametrize('D', [64, 48, 96, 128, 32])
 def test_row_major_v_every_block_count_padded_packed_and_registers(dev, D):
     """Row-major V stays one key a row in LDS and the second product reads it transposed (ds_read_b64_tr_b16):
-    direct loads in the padded and in the packed cu_seqlens layout, through registers with a key mask. Windows of
+    direct loads in the padded and in the packed cu_seqlens layout, and in the key-mask kernel (an all-true mask). Windows of
     0..10 full blocks with and without a partial one (every key block its own score scale and value offset, NaN in
     the padding past each window); all three forms must match the float64 oracle and give the bits of the V^T
     layout."""
     from streamvoxel_amd.stream.attention import attention
     lengths = [64 * n + t for n in range(11) for t in (0, 37) if 64 * n + t > 0]
     B, H, Q, kcap = len(lengths), 2, 96, 704
-    _case(f'xattn row-major V (direct, packed, registers) D={D} lengths={lengths}')
+    _case(f'xattn row-major V (direct, packed, key mask) D={D} lengths={lengths}')
     q, k, v = make_qkv(B, H, Q, kcap, D, seed=301 + D)
     block = torch.arange(kcap) // 64
     k = (k.float() * (1 + 0.29 * (block % 7)).view(1, 1, -1, 1)).to(torch.bfloat16)
@@ -570,12 +570,12 @@ def test_row_major_v_every_block_count_padded_packed_and_registers(dev, D):
     vp = torch.cat([v[b, :, :lengths[b]] for b in range(B)], 1).to(dev)
     out_packed = attention(qd, kp, vp, cu_seqlens=cu.to(dev))
     every = torch.ones(B, kcap, dtype=torch.bool, device=dev)
-    out_regs = attention(qd, kd, v.to(dev), lengths=lt, key_mask=every)
+    out_mask = attention(qd, kd, v.to(dev), lengths=lt, key_mask=every)
     torch.cuda.synchronize()
     check(out_rows, ref, BF16_ATOL, BF16_RTOL)
     assert torch.equal(out_rows, out_vt)
     assert torch.equal(out_packed, out_vt)
-    assert torch.equal(out_regs, out_vt)
+    assert torch.equal(out_mask, out_vt)
 
 
 @pytest.mark.parametrize('D', [64, 48])
@@ -630,6 +630,80 @@ def test_key_mask_row_major_v_whole_blocks(dev, D):
     torch.cuda.synchronize()
     check(out_rows, _masked_reference(q, k, v, mask, lengths), BF16_ATOL, BF16_RTOL)
     assert torch.equal(out_rows, out_vt)
+
+
+@pytest.mark.parametrize('D', [64, 48, 96, 80, 128, 112])
+def test_key_mask_register_staging_gives_the_direct_bits(dev, D):
+    """The key-mask kernels that stage K/V through registers (V^T of the packed cu_seqlens layout; padded V^T whose
+    rows of keys are an odd number of elements apart, read without vectors) against the direct-loaded padded V^T
+    under the same mask: whole masked, whole attended and mixed blocks; the same bits, within the bf16 bar of
+    float64."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, kcap = 3, 2, 100, 600
+    lengths = [600, 333, 130]
+    _case(f'xattn key mask through registers D={D}')
+    q, k, v = make_qkv(B, H, Q, kcap, D, seed=501 + D)
+    g = torch.Generator().manual_seed(13 + D)
+    blk = torch.arange(kcap) // 64
+    mixed = torch.rand(B, kcap, generator=g) < 0.5
+    mask = torch.where((blk % 3 == 0)[None], torch.zeros(B, kcap, dtype=torch.bool),
+                       torch.where((blk % 3 == 1)[None], torch.ones(B, kcap, dtype=torch.bool), mixed))
+    mask[2, 100] = True
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    qd, kd, md = q.to(dev), k.to(dev), mask.to(dev)
+    out_vt = attention(qd, kd, v.transpose(2, 3).contiguous().to(dev).transpose(2, 3), lengths=lt, key_mask=md)
+    wide = torch.zeros(B, H, D, kcap + 3, dtype=torch.bfloat16)
+    wide[..., :kcap] = v.transpose(2, 3)
+    vt_odd = wide.to(dev)[..., :kcap].transpose(2, 3)  # V^T rows kcap + 3 elements apart: no 16-byte runs
+    assert vt_odd.stride(3) % 2 == 1
+    out_odd = attention(qd, kd, vt_odd, lengths=lt, key_mask=md)
+    cu = torch.zeros(B + 1, dtype=torch.int32)
+    cu[1:] = torch.tensor(lengths).cumsum(0)
+    kp = torch.cat([k[b, :, :lengths[b]] for b in range(B)], 1).to(dev)
+    vpt = torch.cat([v[b, :, :lengths[b]] for b in range(B)], 1).transpose(1, 2).contiguous().to(dev)
+    out_packed_vt = attention(qd, kp, vpt.transpose(1, 2), cu_seqlens=cu.to(dev), key_mask=md)
+    torch.cuda.synchronize()
+    check(out_vt, _masked_reference(q, k, v, mask, lengths), BF16_ATOL, BF16_RTOL)
+    assert torch.equal(out_odd, out_vt)
+    assert torch.equal(out_packed_vt, out_vt)
+
+
+def test_row_major_v_past_32_bit_offsets(dev):
+    """Row-major V whose keys lie 16 MiB apart, so that a (window, head)'s keys span more than 4 GiB: past the 32-bit
+    offsets of the direct loads, it is staged through registers (64-bit addresses). Head widths 48-128 (one to
+    four output tiles, with and without the ones column), with and without a key mask: the bits of the same V made
+    contiguous (direct loads), within the bf16 bar of float64."""
+    from streamvoxel_amd.stream.attention import attention
+    B, H, Q, kcap, Dmax = 2, 2, 64, 300, 128
+    key_stride = 1 << 23                               # elements: 299 keys span 5.0 GB
+    lengths = [300, 171]
+    _case(f'xattn row-major V, keys {2 * key_stride} bytes apart, kv_cap {kcap}')
+    storage = torch.empty((kcap - 1) * key_stride + B * H * Dmax, dtype=torch.bfloat16, device=dev)
+    lt = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    g = torch.Generator().manual_seed(12)
+    mask = torch.rand(B, kcap, generator=g) < 0.6
+    mask[:, 64:128] = True
+    mask[:, 192:256] = False
+    md = mask.to(dev)
+    try:
+        for D in (48, 64, 80, 96, 112, 128):
+            q, k, v = make_qkv(B, H, Q, kcap, D, seed=700 + D)
+            v_far = storage.as_strided((B, H, kcap, D), (H * Dmax, Dmax, key_stride, 1))
+            v_far.copy_(v.to(dev))
+            assert (kcap - 1) * v_far.stride(2) * 2 >= 1 << 32
+            qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+            out_far = attention(qd, kd, v_far, lengths=lt)
+            out_near = attention(qd, kd, vd, lengths=lt)
+            mask_far = attention(qd, kd, v_far, lengths=lt, key_mask=md)
+            mask_near = attention(qd, kd, vd, lengths=lt, key_mask=md)
+            torch.cuda.synchronize()
+            check(out_far, A.cross_attention(q, k, v, lengths), BF16_ATOL, BF16_RTOL)
+            check(mask_far, _masked_reference(q, k, v, mask, lengths), BF16_ATOL, BF16_RTOL)
+            assert torch.equal(out_far, out_near), D
+            assert torch.equal(mask_far, mask_near), D
+    finally:
+        del storage
+        torch.cuda.empty_cache()
 
 
 def test_mask_lengths_cut_windows_at_their_last_attended_key(dev):
