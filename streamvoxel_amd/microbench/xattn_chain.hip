@@ -191,7 +191,8 @@ __global__ __launch_bounds__(256, WAVES) void half_kernel(float* out, const floa
   out[blockIdx.x * blockDim.x + tid] = r;
 }
 
-constexpr int kUnits = 96, kUnitBlocks = 128;  // 2 MB of blocks a unit, 192 MB in all
+constexpr int kUnits = 128, kUnitBlocks = 128;  // 2 MB of blocks a unit, 256 MB in all (4 waves per SIMD: 1024
+                                                // workgroups, units 0..127)
 
 // Both halves of a block in one stretch (see the top). RESCALE: the row-sum checks as branches that rescale O.
 template <int WAVES, bool RESCALE>
@@ -330,7 +331,7 @@ int main() {
   float *out, *in;
   uint16_t* kv;
   const int iters = 4000;
-  CHECK(hipMalloc(&out, sizeof(float) * 256 * 256 * 3));
+  CHECK(hipMalloc(&out, sizeof(float) * 256 * 256 * 4));  // one float per thread at up to 4 waves per SIMD
   CHECK(hipMalloc(&in, sizeof(float) * 32));
   CHECK(hipMalloc(&kv, static_cast<size_t>(kUnits) * kUnitBlocks * 16384));
   CHECK(hipMemset(kv, 0x3c, static_cast<size_t>(kUnits) * kUnitBlocks * 16384));
@@ -345,6 +346,8 @@ int main() {
   run<kStaged, 3>("+ staging", out, in, kv, iters, p3);
   run<kStaged, 2>("+ staging", out, in, kv, iters, p3);
   run<kStaged, 1>("+ staging", out, in, kv, iters, p3);
+  run<kStaged, 4>("+ staging", out, in, kv, iters, p3);
+  run<kChain, 4>("chain", out, in, kv, iters, p3);
   run<kStaged, 3, 2>("64 queries a wave", out, in, kv, iters, p3);
   run<kStaged, 2, 2>("64 queries a wave", out, in, kv, iters, p3);
   run<kStaged, 3, 1, 1>("+ staging, priority 1", out, in, kv, iters, p3);
