@@ -741,7 +741,8 @@ def main():
                       traffic=profiled_traffic('xattn_fwd_kernel'),
                       flops_per_launch=w.flops_per_layer, avg_launch_us=t_layer * 1e6,
                       layer0_back_to_back_us=t_layer_alone * 1e6,
-                      e4m3_cache_us=t_layer_e4m3 * 1e6, e4m3_cache_TFLOPs=w.flops_per_layer / t_layer_e4m3 / 1e12),
+                      e4m3_cache_us=t_layer_e4m3 * 1e6, e4m3_cache_TFLOPs=w.flops_per_layer / t_layer_e4m3 / 1e12,
+                      frac_of_box_bf16_gemm=xattn_tflops / peaks['bf16_gemm_TFLOPs']),
         roofline_select=dict(kernel='svhip_ease_select (entropy + apportion + in-block + fix)', bound='hbm',
                              achieved=select_gbs, peak=PEAK_HBM_GBS, unit='GB/s', frac=select_gbs / PEAK_HBM_GBS,
                              traffic=profiled_traffic('ease_select'), bytes_per_call=w.select_bytes,
@@ -750,7 +751,8 @@ def main():
                              patch_order_us=t_select_patches * 1e6,
                              patch_order_GBps=w.select_bytes / t_select_patches / 1e9,
                              shipped_bf16_c304_patch_order_us=t_select304 * 1e6,
-                             shipped_bf16_c304_GBps=bytes304 / t_select304 / 1e9),
+                             shipped_bf16_c304_GBps=bytes304 / t_select304 / 1e9,
+                             frac_of_box_copy=select_gbs / peaks['copy_GBps']),
         components=dict(xattn_ms_per_step=LAYERS * t_layer * 1e3, select_ms_per_step=t_select * 1e3,
                         select_from_patch_order_ms_per_step=t_select_patches * 1e3,
                         class_major_permute_ms_avoided=t_permute * 1e3,
