@@ -55,7 +55,7 @@ def parse():
                    help='time only the whole-step forward (shipped shape) and print its line')
     p.add_argument('--no-c5', action='store_true', help='skip the 64-slot e4m3 stress component')
     p.add_argument('--kernel', choices=['xattn', 'xattn_e4m3', 'xattn_layouts', 'select', 'select_planes',
-                                        'select_c304', 'c5_xattn', 'c5'],
+                                        'select_c304', 'c5_xattn', 'c5', 'gemm_bf16'],
                    help='build only that kernel\'s inputs (the step\'s layer-0 attention or its first solid '
                         'selection), time 20 back-to-back launches and print one line: the run to profile')
     return p.parse_args()
@@ -576,6 +576,12 @@ def kernel_only(dev, args):
         return dict(kernel='c5', **c5_component(dev, args.seed))
     if args.kernel == 'xattn_layouts':
         return xattn_layouts(dev, args.seed)
+    if args.kernel == 'gemm_bf16':           # the box's dense bf16 rate: torch.mm (hipBLASLt), 8192^3, random operands
+        m = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+        n = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+        t = time_events(lambda: torch.mm(m, n), 20)
+        return dict(kernel=args.kernel, us_per_launch=t * 1e6, TFLOPs=2 * 8192 ** 3 / t / 1e12,
+                    flops_per_launch=2 * 8192 ** 3)
     if args.kernel == 'c5_xattn':            # the 64-slot e4m3 layer alone (for the profilers)
         ctx, q, lengths = c5_context(dev, args.seed, 'fp8')
         o = torch.empty_like(q)
