@@ -215,14 +215,30 @@ int svhip_mask_lengths(const uint8_t* kv_mask, int64_t sm_b, const int32_t* kv_l
  * bytes; rows 16-byte aligned; V as rows or as V^T), padded with kv_len or packed with cu_seqlens; head_dim 16, 32,
  * 48 or 64. Every product, sum and exponential is fp32 (the VALU; no rounding of the operands), at the fp32 FMA
  * rate. A window with no key gives zeros.
- * Replaces: the masked SDPA of SlotCrossAttention.forward (streamvoxel/stream/engine.py:28-47) as the reference runs
- * it on fp32 tensors (its CPU path, the single-column configuration).
+ * Replaces: the SDPA of SlotCrossAttention.forward (streamvoxel/stream/engine.py:28-47) as the reference runs it on
+ * fp32 tensors (its CPU path, the single-column configuration) where the window lengths hold its mask; any other
+ * mask takes svhip_xattn_fwd_f32_masked.
  */
 int svhip_xattn_fwd_f32(const float* q, const float* k, const float* v, float* o, const int32_t* kv_len,
                         const int32_t* cu_seqlens, int64_t B, int64_t H, int64_t Q, int64_t D, int64_t kv_cap,
                         int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b, int64_t sk_h, int64_t sk_k,
                         int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d, int64_t so_b, int64_t so_h,
                         int64_t so_q, float scale, void* stream);
+
+/*
+ * svhip_xattn_fwd_f32 with a key mask, in fp32 arithmetic: key j of window b is attended only where
+ * kv_mask[b * sm_b + j] != 0 (one byte per key, any pattern; keys counted from the window's first, also in the
+ * packed layout, whose windows are then cut at kv_cap keys). kv_len and cu_seqlens may both be NULL: every window
+ * then spans kv_cap keys and the mask decides. A query with no attended key gets zeros (as torch's SDPA returns
+ * for a fully masked row on the CPU).
+ * Replaces: the masked SDPA of SlotCrossAttention.forward (streamvoxel/stream/engine.py:28-47) on fp32 tensors, its
+ * mask `prefix_valid ++ local_valid` over the padded prefix and the padded local keys (engine.py:44-46).
+ */
+int svhip_xattn_fwd_f32_masked(const float* q, const float* k, const float* v, float* o, const uint8_t* kv_mask,
+                               int64_t sm_b, const int32_t* kv_len, const int32_t* cu_seqlens, int64_t B, int64_t H,
+                               int64_t Q, int64_t D, int64_t kv_cap, int64_t sq_b, int64_t sq_h, int64_t sq_q,
+                               int64_t sk_b, int64_t sk_h, int64_t sk_k, int64_t sv_b, int64_t sv_h, int64_t sv_k,
+                               int64_t sv_d, int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream);
 
 /*
  * AxialRoPE of bf16 activations: x [B,H,N,D] (element (b,h,n,d) at b*sx_b + h*sx_h + n*sx_n + d) -> out (same

@@ -51,6 +51,8 @@ SIGNATURES = {
     'svhip_xattn_fwd_masked': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p] + [_c_i64] * 18
                                + [_c_f, _c_p]),
     'svhip_xattn_fwd_f32': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p] + [_c_i64] * 18 + [_c_f, _c_p]),
+    'svhip_xattn_fwd_f32_masked': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p] + [_c_i64] * 18
+                                   + [_c_f, _c_p]),
     'svhip_axial_rope': (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p] + [_c_i64] * 12 + [_c_p]),
     'svhip_kv_write_workspace_bytes': (_c_sz, [_c_i64, _c_i64]),
     'svhip_kv_write': (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64,

@@ -12,6 +12,11 @@
 // current one is computed, keys >= L as zeros), reads each row back with one address for all lanes (an LDS
 // broadcast), forms the 16 scores, raises its running max m (log2 units) to the block's, rescales O and l once and
 // adds the 16 weighted V rows. The eight partial (m, l, O) are merged pairwise through LDS in three rounds.
+//
+// KMASK: a key mask on top of the window length (the reference's `prefix_valid ++ local_valid`): key j of window b
+// is attended only where kv_mask[b * sm_b + j] != 0. A block's 16 mask bytes are read one per lane and gathered
+// by a ballot; a block (and every block before it) may then hold no attended key, so the running max may stay
+// -inf, against which nothing is added.
 #include "common.hpp"
 
 namespace svhip {
@@ -28,6 +33,8 @@ struct XattnF32Params {
   float* o;
   const int32_t* kv_len;
   const int32_t* cu_seqlens;
+  const uint8_t* kv_mask;  // KMASK: [B, kv_cap] bytes, rows sm_b apart
+  int64_t sm_b;
   int64_t B, H, Q, kv_cap;
   int64_t sq_b, sq_h, sq_q;
   int64_t sk_b, sk_h, sk_k;
@@ -39,7 +46,7 @@ struct XattnF32Params {
 
 // VT: V given as V^T rows (keys contiguous, element (key, d) at d * sv_d + key), else V rows (head_dim
 // contiguous). Rows start 16-byte aligned (checked by the entry point).
-template <int D, bool VT>
+template <int D, bool VT, bool KMASK>
 __global__ __launch_bounds__(kF32Threads) void xattn_f32_kernel(XattnF32Params p) {
   constexpr int kBlock = kF32Keys * D;   // floats of one staged K (or V) block
   constexpr int kPer = kBlock / 256;     // float4 per lane and block
@@ -58,11 +65,13 @@ __global__ __launch_bounds__(kF32Threads) void xattn_f32_kernel(XattnF32Params p
   if (p.cu_seqlens) {
     off = p.cu_seqlens[b];
     L = static_cast<int64_t>(p.cu_seqlens[b + 1]) - off;
+    if (KMASK && L > p.kv_cap) L = p.kv_cap;  // the mask rows hold kv_cap keys
   } else {
-    L = p.kv_len[b];
+    L = p.kv_len ? p.kv_len[b] : p.kv_cap;    // no kv_len (key mask only): every key of the row
     if (L > p.kv_cap) L = p.kv_cap;
   }
   if (L < 0) L = 0;
+  const uint8_t* mrow = KMASK ? p.kv_mask + b * p.sm_b : nullptr;
   const int64_t q = static_cast<int64_t>(qt) * 64 + lane;
   const bool q_ok = q < p.Q;
   const float* K = p.k + (p.cu_seqlens ? 0 : b * p.sk_b) + h * p.sk_h + off * p.sk_k;
@@ -141,6 +150,15 @@ __global__ __launch_bounds__(kF32Threads) void xattn_f32_kernel(XattnF32Params p
     store_block();
   }
   for (; kv0 < L; kv0 += kF32Waves * kF32Keys) {
+    // KMASK: bit i of `attended` = key kv0 + i below L and attended (lane i reads its byte; lanes 16-63 repeat
+    // lanes 0-15); wave-uniform.
+    uint32_t attended = 0xffffu;
+    if constexpr (KMASK) {
+      const int left = static_cast<int>(L - kv0);  // keys of the window from kv0 on (>= 1; L < 2^31)
+      const int kk = min(lane & (kF32Keys - 1), left - 1);
+      attended = static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(mrow[kv0 + kk] != 0)) & 0xffffu;
+      if (left < kF32Keys) attended &= (1u << left) - 1u;
+    }
     const int64_t next = kv0 + kF32Waves * kF32Keys;
     load_block(next);  // in flight while this block is computed (zeros past the window)
     float t[kF32Keys];
@@ -159,19 +177,22 @@ __global__ __launch_bounds__(kF32Threads) void xattn_f32_kernel(XattnF32Params p
       }
       // Branch-free: keys >= L (zero rows, acc = 0) take the bias -inf. A select on acc would let the compiler put
       // each row's products under a branch and hoist every row's LDS reads above all of them.
-      const float bias = kv0 + i < L ? 0.f : -INFINITY;
+      const float bias = (KMASK ? ((attended >> i) & 1u) != 0u : kv0 + i < L) ? 0.f : -INFINITY;
       t[i] = __builtin_fmaf(acc, sl2, bias);
       mb = fmaxf(mb, t[i]);
     }
-    const float mn = fmaxf(m, mb);                       // finite: the block holds at least one key
-    const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the wave's first block
+    const float mn = fmaxf(m, mb);  // finite without a key mask: the block holds at least one key
+    // With a key mask mn is -inf while no attended key has come: the exponentials are then taken against 0, which
+    // gives 0 for every weight and for alpha (O and l hold nothing yet).
+    const float mref = (KMASK && mn == -INFINITY) ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - mref);  // 0 on the wave's first block
     m = mn;
     l *= alpha;
 #pragma unroll
     for (int d = 0; d < D; ++d) o[d] *= alpha;
 #pragma unroll
     for (int i = 0; i < kF32Keys; ++i) {
-      const float pw = __builtin_amdgcn_exp2f(t[i] - mn);  // 0 for keys >= L
+      const float pw = __builtin_amdgcn_exp2f(t[i] - mref);  // 0 for keys >= L and keys not attended
       l += pw;
       const float* vr = sV + i * D;
 #pragma unroll
@@ -214,7 +235,7 @@ __global__ __launch_bounds__(kF32Threads) void xattn_f32_kernel(XattnF32Params p
     }
   }
   if (w == 0 && q_ok) {
-    // No key at all (L = 0): zeros, as the bf16 kernel writes.
+    // No key at all (L = 0, or no attended key): zeros, as the bf16 kernel writes.
     const float inv = l > 0.f ? 1.f / l : 0.f;
     float* out = p.o + b * p.so_b + h * p.so_h + q * p.so_q;
 #pragma unroll
@@ -222,12 +243,21 @@ __global__ __launch_bounds__(kF32Threads) void xattn_f32_kernel(XattnF32Params p
   }
 }
 
-template <int D>
+template <int D, bool KMASK>
 static void launch_f32(const XattnF32Params& p, unsigned grid, hipStream_t s, bool vt) {
   if (vt) {
-    xattn_f32_kernel<D, true><<<grid, kF32Threads, 0, s>>>(p);
+    xattn_f32_kernel<D, true, KMASK><<<grid, kF32Threads, 0, s>>>(p);
   } else {
-    xattn_f32_kernel<D, false><<<grid, kF32Threads, 0, s>>>(p);
+    xattn_f32_kernel<D, false, KMASK><<<grid, kF32Threads, 0, s>>>(p);
+  }
+}
+
+template <int D>
+static void launch_f32(const XattnF32Params& p, unsigned grid, hipStream_t s, bool vt) {
+  if (p.kv_mask) {
+    launch_f32<D, true>(p, grid, s, vt);
+  } else {
+    launch_f32<D, false>(p, grid, s, vt);
   }
 }
 
@@ -235,15 +265,19 @@ static void launch_f32(const XattnF32Params& p, unsigned grid, hipStream_t s, bo
 
 using namespace svhip;
 
-extern "C" int svhip_xattn_fwd_f32(const float* q, const float* k, const float* v, float* o, const int32_t* kv_len,
-                                   const int32_t* cu_seqlens, int64_t B, int64_t H, int64_t Q, int64_t D,
-                                   int64_t kv_cap, int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b,
-                                   int64_t sk_h, int64_t sk_k, int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d,
-                                   int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream) {
-  const char* name = "svhip_xattn_fwd_f32";
+static int xattn_f32_impl(const float* q, const float* k, const float* v, float* o, const uint8_t* kv_mask,
+                          int64_t sm_b, const int32_t* kv_len, const int32_t* cu_seqlens, int64_t B, int64_t H,
+                          int64_t Q, int64_t D, int64_t kv_cap, int64_t sq_b, int64_t sq_h, int64_t sq_q,
+                          int64_t sk_b, int64_t sk_h, int64_t sk_k, int64_t sv_b, int64_t sv_h, int64_t sv_k,
+                          int64_t sv_d, int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream,
+                          const char* name) {
   clear_error();
   SVHIP_REQUIRE(q && k && v && o, "%s: null pointer", name);
-  SVHIP_REQUIRE(kv_len || cu_seqlens, "%s: need kv_len or cu_seqlens", name);
+  if (kv_mask) {
+    SVHIP_REQUIRE(sm_b >= 0, "%s: negative mask row stride", name);
+  } else {
+    SVHIP_REQUIRE(kv_len || cu_seqlens, "%s: need kv_len or cu_seqlens", name);
+  }
   SVHIP_REQUIRE(!(kv_len && cu_seqlens), "%s: kv_len and cu_seqlens are exclusive", name);
   SVHIP_REQUIRE(B >= 0 && H >= 1 && Q >= 0, "%s: bad sizes", name);
   SVHIP_REQUIRE(D == 16 || D == 32 || D == 48 || D == 64, "%s: head_dim %lld unsupported (16, 32, 48 or 64)", name,
@@ -267,6 +301,8 @@ extern "C" int svhip_xattn_fwd_f32(const float* q, const float* k, const float* 
   p.o = o;
   p.kv_len = kv_len;
   p.cu_seqlens = cu_seqlens;
+  p.kv_mask = kv_mask;
+  p.sm_b = sm_b;
   p.B = B;
   p.H = H;
   p.Q = Q;
@@ -306,4 +342,27 @@ extern "C" int svhip_xattn_fwd_f32(const float* q, const float* k, const float* 
   }
   SVHIP_LAUNCHED(name);
   return SVHIP_OK;
+}
+
+extern "C" int svhip_xattn_fwd_f32(const float* q, const float* k, const float* v, float* o, const int32_t* kv_len,
+                                   const int32_t* cu_seqlens, int64_t B, int64_t H, int64_t Q, int64_t D,
+                                   int64_t kv_cap, int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b,
+                                   int64_t sk_h, int64_t sk_k, int64_t sv_b, int64_t sv_h, int64_t sv_k, int64_t sv_d,
+                                   int64_t so_b, int64_t so_h, int64_t so_q, float scale, void* stream) {
+  return xattn_f32_impl(q, k, v, o, nullptr, 0, kv_len, cu_seqlens, B, H, Q, D, kv_cap, sq_b, sq_h, sq_q, sk_b, sk_h,
+                        sk_k, sv_b, sv_h, sv_k, sv_d, so_b, so_h, so_q, scale, stream, "svhip_xattn_fwd_f32");
+}
+
+extern "C" int svhip_xattn_fwd_f32_masked(const float* q, const float* k, const float* v, float* o,
+                                          const uint8_t* kv_mask, int64_t sm_b, const int32_t* kv_len,
+                                          const int32_t* cu_seqlens, int64_t B, int64_t H, int64_t Q, int64_t D,
+                                          int64_t kv_cap, int64_t sq_b, int64_t sq_h, int64_t sq_q, int64_t sk_b,
+                                          int64_t sk_h, int64_t sk_k, int64_t sv_b, int64_t sv_h, int64_t sv_k,
+                                          int64_t sv_d, int64_t so_b, int64_t so_h, int64_t so_q, float scale,
+                                          void* stream) {
+  const char* name = "svhip_xattn_fwd_f32_masked";
+  clear_error();
+  SVHIP_REQUIRE(kv_mask, "%s: null key mask", name);
+  return xattn_f32_impl(q, k, v, o, kv_mask, sm_b, kv_len, cu_seqlens, B, H, Q, D, kv_cap, sq_b, sq_h, sq_q, sk_b,
+                        sk_h, sk_k, sv_b, sv_h, sv_k, sv_d, so_b, so_h, so_q, scale, stream, name);
 }

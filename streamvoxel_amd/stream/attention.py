@@ -39,14 +39,14 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
     5e-2 of fp32 attention over the unquantised K/V), 'e4m3' takes P . V on the fp8 matrix cores with the weights
     rounded to e4m3 (an opt-in outside that bar: every weight carries a 2^-4 relative rounding).
     `out` (optional) [B,H,Q,D] bf16 with head_dim contiguous, e.g. a [B,Q,H,D] buffer's transpose(1, 2) view.
-    fp32 query, key and val (head_dim 16, 32, 48 or 64, rows 16-byte aligned, lengths or cu_seqlens) take fp32
-    arithmetic throughout and return fp32 (`svhip_xattn_fwd_f32`, the reference's fp32 SDPA; no key mask).
+    fp32 query, key and val (head_dim 16, 32, 48 or 64, rows 16-byte aligned) take fp32 arithmetic throughout and
+    return fp32 (`svhip_xattn_fwd_f32`, or `svhip_xattn_fwd_f32_masked` with a key mask: the reference's fp32 SDPA).
     Returns out."""
     _lib.require_gpu(query, key, val, lengths, cu_seqlens, k_scale, v_scale, out)
     if query.dtype == torch.float32:
-        if key_mask is not None or k_scale is not None or v_scale is not None:
-            raise TypeError('fp32 attention takes neither a key mask nor fp8 scales')
-        return _attention_f32(query, key, val, lengths, cu_seqlens, scale, out)
+        if k_scale is not None or v_scale is not None:
+            raise TypeError('fp32 attention takes no fp8 scales')
+        return _attention_f32(query, key, val, lengths, cu_seqlens, scale, out, key_mask)
     if query.dtype != torch.bfloat16:
         raise TypeError('query must be bfloat16 (or float32 with float32 K/V)')
     B, H, Q, D = query.shape
@@ -124,13 +124,20 @@ def attention(query, key, val, lengths=None, cu_seqlens=None, scale=None, k_scal
     return out
 
 
-def _attention_f32(query, key, val, lengths, cu_seqlens, scale, out):
-    """fp32 Q/K/V -> fp32 O with fp32 arithmetic throughout (svhip_xattn_fwd_f32): the reference's fp32 SDPA."""
+def _attention_f32(query, key, val, lengths, cu_seqlens, scale, out, key_mask=None):
+    """fp32 Q/K/V -> fp32 O with fp32 arithmetic throughout (svhip_xattn_fwd_f32; with a key mask
+    svhip_xattn_fwd_f32_masked, SlotCrossAttention.forward's masked SDPA, streamvoxel/stream/engine.py:28-47)."""
     if key.dtype != torch.float32 or val.dtype != torch.float32:
         raise TypeError('fp32 query takes fp32 key and val')
     B, H, Q, D = query.shape
-    if (lengths is None) == (cu_seqlens is None):
-        raise ValueError('pass exactly one of lengths / cu_seqlens')
+    if lengths is not None and cu_seqlens is not None:
+        raise ValueError('pass at most one of lengths / cu_seqlens')
+    if key_mask is None and lengths is None and cu_seqlens is None:
+        raise ValueError('pass lengths, cu_seqlens or key_mask')
+    if key_mask is not None:
+        _lib.require_gpu(key_mask)
+        if key_mask.dtype != torch.bool or key_mask.dim() != 2 or key_mask.shape[0] != B or key_mask.stride(1) != 1:
+            raise ValueError('key_mask must be bool [B, keys] with contiguous keys')
     if query.stride(-1) != 1 or key.stride(-1) != 1:
         raise ValueError('query and key need a contiguous head_dim')
     if out is None:
@@ -148,7 +155,7 @@ def _attention_f32(query, key, val, lengths, cu_seqlens, scale, out):
     else:
         if key.dim() != 4 or key.shape[:2] != (B, H) or val.shape != key.shape:
             raise ValueError('padded K/V are [B,H,Kcap,D] like the query')
-        if lengths.dtype != torch.int32 or lengths.numel() != B:
+        if lengths is not None and (lengths.dtype != torch.int32 or lengths.numel() != B):
             raise ValueError('lengths must be int32 [B]')
         kcap = key.shape[2]
         sk = (key.stride(0), key.stride(1), key.stride(2))
@@ -157,6 +164,16 @@ def _attention_f32(query, key, val, lengths, cu_seqlens, scale, out):
         raise ValueError('head_dim mismatch')
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     lib = _lib.load()
+    if key_mask is not None:
+        if cu_seqlens is None and key_mask.shape[1] < kcap:
+            raise ValueError(f'key_mask holds {key_mask.shape[1]} keys per window, the cache {kcap}')
+        mask_cap = kcap if cu_seqlens is None else key_mask.shape[1]
+        _lib.check(lib.svhip_xattn_fwd_f32_masked(
+            _lib.ptr(query), _lib.ptr(key), _lib.ptr(val), _lib.ptr(out), _lib.ptr(key_mask.view(torch.uint8)),
+            key_mask.stride(0), _lib.ptr(lengths), _lib.ptr(cu_seqlens), B, H, Q, D, mask_cap,
+            query.stride(0), query.stride(1), query.stride(2), *sk, *sv, out.stride(0), out.stride(1), out.stride(2),
+            scale, _lib.stream_of(query)), 'svhip_xattn_fwd_f32_masked')
+        return out
     _lib.check(lib.svhip_xattn_fwd_f32(
         _lib.ptr(query), _lib.ptr(key), _lib.ptr(val), _lib.ptr(out), _lib.ptr(lengths), _lib.ptr(cu_seqlens),
         B, H, Q, D, kcap, query.stride(0), query.stride(1), query.stride(2), *sk, *sv,

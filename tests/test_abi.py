@@ -189,3 +189,13 @@ def test_argument_errors_of_the_fp32_attention(lib):
     assert f32(64, q=None) == -1 and b'null' in lib.svhip_last_error()
     assert f32(64, sk_k=66) == -1 and b'16-byte' in lib.svhip_last_error()
     assert f32(64, sv=(64 * 64, 64 * 64, 2, 3)) == -1 and b'unit stride' in lib.svhip_last_error()
+
+    def f32m(mask=lengths, kv_len=None, D=64):
+        sizes = [1, 1, 128, D, 64]
+        strides = [128 * 64, 128 * 64, 64, 64 * 64, 64 * 64, 64, 64 * 64, 64 * 64, 64, 1, 128 * 64, 128 * 64, 64]
+        return lib.svhip_xattn_fwd_f32_masked(fake, fake, fake, fake, mask, 64, kv_len, None, *sizes, *strides,
+                                              0.125, None)
+
+    assert f32m(mask=None) == -1 and b'null key mask' in lib.svhip_last_error()
+    assert f32m(D=40) == -1 and b'head_dim' in lib.svhip_last_error()
+    assert f32m(kv_len=lengths, D=96) == -1 and b'head_dim' in lib.svhip_last_error()
