@@ -657,9 +657,9 @@ enum Staging { kRegister = 0, kDirect = 1, kDirectFull = 2, kRegisterFull = 3 };
 // ONES: head_dim below 32 DT, the row sum comes from the matrix cores (V^T row D of ones). The e4m3 V^T kernel up
 // to head_dim 64 is held to 168 VGPRs (three waves per SIMD; it needs 170 unbounded, without spilling at 168); the
 // bf16 direct-staged ones fit by themselves.
-// KMASK: a key mask (p.kv_mask) on top of the window length: a block whose keys it all masks is skipped, one whose
-// keys it all attends is computed as without a mask, any other masks its scores (the register-staged V^T form
-// masks every block).
+// KMASK: a key mask (p.kv_mask) on top of the window length: the window ends at its last attended key, a block
+// whose keys it all masks is skipped, one whose keys it all attends is computed as without a mask, any other masks
+// its scores (the register-staged V^T form masks every block).
 // PV8: e4m3 K/V take the second product on the fp8 matrix cores (see the comment at the top).
 // VD8: with PV8, V^T takes direct loads for full blocks (e4m3 rows of 16-byte aligned runs).
 template <bool FP8, bool VT, int STAGING, int DT, bool ONES, bool KMASK = false, bool PV8 = false, bool VD8 = false>
