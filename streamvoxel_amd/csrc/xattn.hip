@@ -1053,12 +1053,14 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
 
   SVHIP_TRACE(WaveTrace trace;)
   SVHIP_TRACE(trace.begin(!FP8 && !KMASK && STAGING == kDirectFull, w, lane, b, h, qt, nfull);)
-  auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vt, int kv0) __attribute__((always_inline)) {
+  // bits: the block's key mask (block_bits, all ones without one), taken by the caller before it issues the next
+  // block's loads.
+  auto compute = [&](auto masked, const uint16_t* Ks, const uint16_t* Vt, int kv0, uint64_t bits)
+      __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked)::value;
     SVHIP_TRACE(trace.block(MASKED ? -1 : kv0 / kKB);)
     const char* kp = reinterpret_cast<const char*>(Ks);
     const char* vp = reinterpret_cast<const char*>(Vt);
-    const uint64_t bits = block_bits(kv0);
     // A key mask that masks every key of the block: the block adds nothing to O, l or m (its P are all 0), so it
     // is skipped (wave-uniform; the block's barrier is outside). Not in the register-staged V^T form, which has no
     // registers to spare for it.
@@ -1301,10 +1303,14 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
   using Full = std::false_type;
   using Partial = std::true_type;
 
-  // Full block blk from (Ks, Vt) while full block blk + 1 is staged into (nK, nV).
+  // Full block blk from (Ks, Vt) while full block blk + 1 is staged into (nK, nV). With a key mask the block's bits
+  // are taken, and the next block's mask bytes fetched, before the next block's loads are issued: the wait for the
+  // mask bytes (loaded during the previous block, waited for at its end) then waits for nothing in flight, where
+  // after those loads it waited for them all.
   auto full_step = [&](int blk, const uint16_t* Ks, const uint16_t* Vt, uint16_t* nK, uint16_t* nV) __attribute__((always_inline)) {
+    const uint64_t bits = block_bits(blk * kKB);
     stage_issue(blk + 1, nK, nV);
-    compute(Full{}, Ks, Vt, blk * kKB);
+    compute(Full{}, Ks, Vt, blk * kKB, bits);
     stage_commit(nK, nV);
     wait_vmem();
     __syncthreads();
@@ -1338,19 +1344,20 @@ __global__ __launch_bounds__(kThreads, (DT == 2 && (VT || !PV8)) ? 3 : 2) void x
     if (nfull > 0) {
       // The partial block's loads are in flight during the last full block (the other tiles are free since the
       // last barrier).
+      const uint64_t bits = block_bits(blk * kKB);
       Stage<FP8, VT, DT> tl;
       if (tail) stage_load<FP8, VT, DT, true, ONES>(tl, p, K, V, L, nfull * kKB, dchunks, vt_vec);
-      compute(Full{}, cK, cV, blk * kKB);
+      compute(Full{}, cK, cV, blk * kKB, bits);
       settle();
       if (tail) {
         stage_store<FP8, VT, DT, ONES, PV8>(tl, nK, nV, dchunks, Dv);
         wait_vmem();
         __syncthreads();
-        compute(Partial{}, nK, nV, nfull * kKB);
+        compute(Partial{}, nK, nV, nfull * kKB, block_bits(nfull * kKB));
         settle();
       }
     } else {
-      compute(Partial{}, cK, cV, 0);
+      compute(Partial{}, cK, cV, 0, block_bits(0));
       settle();
     }
   }
